@@ -1,0 +1,322 @@
+// Gated-delta-rule recurrent slot step for gfx950.
+//
+// Recurrence (per row n, value head hv, real token t), as src/hs_guard/engine/fused_kernels.py:166-188:
+//   q <- q / sqrt(|q|^2 + 1e-6) * scale,  k <- k / sqrt(|k|^2 + 1e-6)
+//   g = -exp(A_log) * softplus(a + dt_bias)   (threshold 20),  beta = sigmoid(b)
+//   S <- exp(g) S;  v' = beta (v - S^T k);  S <- S + k v'^T;  o = S^T q
+//
+// Mapping: one 256-thread workgroup per (row, value head); wave w owns value columns [32w, 32w+32).
+// Lane (c = lane & 7, rg = lane >> 3) holds the 16 x 4 block S[16rg .. 16rg+15][32w+4c .. +3] in
+// registers for the whole tick, so the 64 KiB fp32 state of a (slot, head) is read once and written once
+// per tick whatever the token count. Each state load is a 16-byte vector; the 8 lanes of one rg cover a
+// 128-byte row segment, so every load instruction reads 8 full 128-byte lines. The k.S and q.S
+// reductions over the 128 key rows are in-lane (16 rows) plus a 3-step butterfly over rg (lane xor 8,
+// 16, 32). exp(g) is folded in as (exp(g) S)^T k = exp(g) (S^T k), and the decay and rank-1 update share
+// one pass over the registers.
+#include "hsg_common.h"
+
+namespace hsg {
+namespace {
+
+constexpr int KD = 128;
+constexpr int VD = 128;
+constexpr int TILE_V = 32;
+constexpr int ROWS = 16;
+
+struct GdnParams {
+  const uint16_t* qkv;
+  int64_t qkv_stride;
+  int q_off, k_off, v_off;
+  const uint16_t* a;
+  const uint16_t* b;
+  int64_t ab_stride;
+  const uint16_t* A_log;
+  const uint16_t* dt_bias;
+  void* state;
+  int64_t state_rows;
+  const int64_t* slots;
+  const int64_t* lens;
+  const int64_t* offsets;
+  int L, H, HV;
+  float scale;
+  uint16_t* o;
+  float* sq;
+  const uint16_t* z;
+  int64_t z_stride;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* out;
+};
+
+template <typename ST>
+struct StateIO;
+
+template <>
+struct StateIO<float> {
+  static __device__ __forceinline__ void load(const float* p, float* v) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+template <>
+struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
+  static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    v[0] = h2f((uint16_t)(w.x & 0xffffu)); v[1] = h2f((uint16_t)(w.x >> 16));
+    v[2] = h2f((uint16_t)(w.y & 0xffffu)); v[3] = h2f((uint16_t)(w.y >> 16));
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float* v) {
+    uint2 w;
+    w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+    w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    *reinterpret_cast<uint2*>(p) = w;
+  }
+};
+
+// Sum over the 8 lanes sharing (lane & 7): lane xor 8, 16, 32.
+__device__ __forceinline__ float sum_rg(float x) {
+  x = xor_add<8>(x);
+  x = xor_add<16>(x);
+  x = xor_add<32>(x);
+  return x;
+}
+
+// Sum over the 8 lanes sharing (lane >> 3): lane xor 1, 2, 4.
+__device__ __forceinline__ float sum_c(float x) {
+  x = xor_add<1>(x);
+  x = xor_add<2>(x);
+  x = xor_add<4>(x);
+  return x;
+}
+
+template <typename ST, bool GATED>
+__global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 7;
+  const int rg = lane >> 3;
+  const int n = blockIdx.x / p.HV;
+  const int hv = blockIdx.x - n * p.HV;
+  const int h = hv / (p.HV / p.H);
+  const int64_t slot = p.slots[n];
+  int ntok = (int)p.lens[n];
+  const bool padded = p.offsets == nullptr;
+  if (slot < 0 || slot >= p.state_rows || ntok < 0) ntok = 0;
+  if (padded && ntok > p.L) ntok = p.L;  // a row never reads past its L padded positions
+  const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
+  const int col = wave * TILE_V + c * 4;
+
+  float S[ROWS][4];
+  ST* sp = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * KD + rg * ROWS) * (int64_t)VD + col;
+  if (ntok > 0) {
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) StateIO<ST>::load(sp + j * VD, S[j]);
+  }
+  const float A = expf(bf2f(p.A_log[hv]));
+  const float dt = bf2f(p.dt_bias[hv]);
+  __shared__ float red[2][4];
+
+  for (int t = 0; t < ntok; ++t) {
+    const int64_t tok = tok0 + t;
+    const uint16_t* row = p.qkv + tok * p.qkv_stride;
+    float q[ROWS], k[ROWS], v[4];
+    load8_bf16(row + p.q_off + h * KD + rg * ROWS, q);
+    load8_bf16(row + p.q_off + h * KD + rg * ROWS + 8, q + 8);
+    load8_bf16(row + p.k_off + h * KD + rg * ROWS, k);
+    load8_bf16(row + p.k_off + h * KD + rg * ROWS + 8, k + 8);
+    load4_bf16(row + p.v_off + hv * VD + col, v);
+    float qq = 0.f, kk = 0.f;
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) {
+      qq += q[j] * q[j];
+      kk += k[j] * k[j];
+    }
+    qq = sum_rg(qq);
+    kk = sum_rg(kk);
+    const float rq = 1.0f / sqrtf(qq + 1e-6f);
+    const float rk = 1.0f / sqrtf(kk + 1e-6f);
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) {
+      q[j] = q[j] * rq * p.scale;
+      k[j] = k[j] * rk;
+    }
+    const float x = bf2f(p.a[tok * p.ab_stride + hv]) + dt;
+    const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
+    const float beta = sigmoidf_(bf2f(p.b[tok * p.ab_stride + hv]));
+    const float decay = expf(g);
+
+    float kv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kv[i] += S[j][i] * k[j];
+    }
+    float vn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vn[i] = beta * (v[i] - decay * sum_rg(kv[i]));
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        S[j][i] = S[j][i] * decay + k[j] * vn[i];
+        o[i] += S[j][i] * q[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = sum_rg(o[i]);
+
+    if constexpr (!GATED) {
+      if (rg == 0) {
+        const int64_t base = (tok * p.HV + hv) * VD + col;
+        store4_bf16(p.o + base, o);
+        if (p.sq != nullptr) {
+          float s4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float ob = rbf(o[i]);
+            s4[i] = ob * ob;
+          }
+          *reinterpret_cast<float4*>(p.sq + base) = make_float4(s4[0], s4[1], s4[2], s4[3]);
+        }
+      }
+    } else {
+      float ob[4];
+      float part = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ob[i] = rbf(o[i]);
+        part += ob[i] * ob[i];
+      }
+      part = sum_c(part);
+      if (lane == 0) red[t & 1][wave] = part;
+      __syncthreads();
+      const float var = (red[t & 1][0] + red[t & 1][1] + red[t & 1][2] + red[t & 1][3]) * (1.0f / VD);
+      const float r = rsqrtf(var + p.eps);
+      if (rg == 0) {
+        float y[4], w4[4], z4[4];
+        load4_bf16(p.norm_w + col, w4);
+        load4_bf16(p.z + tok * p.z_stride + hv * VD + col, z4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float hb = rbf(ob[i] * r);
+          const float tw = rbf(w4[i] * hb);
+          y[i] = tw * siluf_(z4[i]);
+        }
+        store4_bf16(p.out + tok * (int64_t)(p.HV * VD) + hv * VD + col, y);
+      }
+    }
+  }
+
+  if (padded && rg == 0) {
+    const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int t = ntok; t < p.L; ++t) {
+      const int64_t tok = tok0 + t;
+      if constexpr (!GATED) {
+        const int64_t base = (tok * p.HV + hv) * VD + col;
+        store4_bf16(p.o + base, zero);
+        if (p.sq != nullptr) *reinterpret_cast<float4*>(p.sq + base) = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        store4_bf16(p.out + tok * (int64_t)(p.HV * VD) + hv * VD + col, zero);
+      }
+    }
+  }
+
+  if (ntok > 0) {
+#pragma unroll
+    for (int j = 0; j < ROWS; ++j) StateIO<ST>::store(sp + j * VD, S[j]);
+  }
+}
+
+int check_common(const GdnParams& p, int state_dtype, int n_rows, int K, int V) {
+  if (n_rows < 0 || p.H <= 0 || p.HV <= 0 || p.L < 0 || p.state_rows <= 0) return HSG_ERR_ARG;
+  if (n_rows == 0) return HSG_OK;
+  if (!p.qkv || !p.a || !p.b || !p.A_log || !p.dt_bias || !p.state || !p.slots || !p.lens) return HSG_ERR_ARG;
+  if (p.offsets == nullptr && p.L <= 0) return HSG_ERR_ARG;
+  if (K != KD || V != VD || p.HV % p.H != 0) return HSG_ERR_SHAPE;
+  if (state_dtype != HSG_STATE_F32 && state_dtype != HSG_STATE_F16) return HSG_ERR_ARG;
+  if (!aligned(p.qkv, 16) || p.qkv_stride % 8 || p.q_off % 8 || p.k_off % 8 || p.v_off % 4) return HSG_ERR_ALIGN;
+  if (!aligned(p.state, 16)) return HSG_ERR_ALIGN;
+  return 1;  // proceed
+}
+
+template <bool GATED>
+int launch(const GdnParams& p, int state_dtype, int n_rows, void* stream) {
+  const dim3 grid((unsigned)(n_rows * p.HV));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (state_dtype == HSG_STATE_F32)
+    hipLaunchKernelGGL((gdn_step_kernel<float, GATED>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((gdn_step_kernel<uint16_t, GATED>), grid, dim3(256), 0, s, p);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace hsg
+
+using hsg::GdnParams;
+
+extern "C" int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
+                                 int32_t v_off, const void* a, const void* b, int64_t ab_stride,
+                                 const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
+                                 int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                                 const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
+                                 int32_t K, int32_t V, float scale, void* o, float* sq, void* stream) {
+  GdnParams p{};
+  p.qkv = static_cast<const uint16_t*>(qkv);
+  p.qkv_stride = qkv_stride;
+  p.q_off = q_off; p.k_off = k_off; p.v_off = v_off;
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.ab_stride = ab_stride;
+  p.A_log = static_cast<const uint16_t*>(A_log);
+  p.dt_bias = static_cast<const uint16_t*>(dt_bias);
+  p.state = state;
+  p.state_rows = state_rows;
+  p.slots = slots; p.lens = lens; p.offsets = offsets;
+  p.L = L; p.H = H; p.HV = HV; p.scale = scale;
+  p.o = static_cast<uint16_t*>(o);
+  p.sq = sq;
+  const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
+  if (rc <= 0) return rc;
+  if (!o) return HSG_ERR_ARG;
+  if (!hsg::aligned(o, 8) || (sq && !hsg::aligned(sq, 16))) return HSG_ERR_ALIGN;
+  return hsg::launch<false>(p, state_dtype, n_rows, stream);
+}
+
+extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
+                                       int32_t v_off, const void* a, const void* b, int64_t ab_stride,
+                                       const void* A_log, const void* dt_bias, void* state,
+                                       int32_t state_dtype, int64_t state_rows, const int64_t* slots,
+                                       const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t L,
+                                       int32_t H, int32_t HV, int32_t K, int32_t V, float scale,
+                                       const void* z, int64_t z_stride, const void* norm_w, float eps,
+                                       void* out, void* stream) {
+  GdnParams p{};
+  p.qkv = static_cast<const uint16_t*>(qkv);
+  p.qkv_stride = qkv_stride;
+  p.q_off = q_off; p.k_off = k_off; p.v_off = v_off;
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.ab_stride = ab_stride;
+  p.A_log = static_cast<const uint16_t*>(A_log);
+  p.dt_bias = static_cast<const uint16_t*>(dt_bias);
+  p.state = state;
+  p.state_rows = state_rows;
+  p.slots = slots; p.lens = lens; p.offsets = offsets;
+  p.L = L; p.H = H; p.HV = HV; p.scale = scale;
+  p.z = static_cast<const uint16_t*>(z);
+  p.z_stride = z_stride;
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
+  p.out = static_cast<uint16_t*>(out);
+  const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
+  if (rc <= 0) return rc;
+  if (!z || !norm_w || !out) return HSG_ERR_ARG;
+  if (!hsg::aligned(z, 8) || z_stride % 4 || !hsg::aligned(norm_w, 8) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
+  return hsg::launch<true>(p, state_dtype, n_rows, stream);
+}

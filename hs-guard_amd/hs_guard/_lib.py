@@ -1,0 +1,73 @@
+"""ctypes binding of libhsg.so (the C ABI declared in include/hsg.h).
+
+The library is required: there is no CPU or torch fallback for any kernel. ``lib()`` raises a
+RuntimeError naming the missing file when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhsg.so")
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/hsg.h
+SIGNATURES = {
+    "hsg_version": (ctypes.c_int, []),
+    "hsg_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "hsg_gdn_slot_step": (ctypes.c_int, [
+        _P, _I64, _I32, _I32, _I32,          # qkv, qkv_stride, q_off, k_off, v_off
+        _P, _P, _I64, _P, _P,                # a, b, ab_stride, A_log, dt_bias
+        _P, _I32, _I64,                      # state, state_dtype, state_rows
+        _P, _P, _P, _I32, _I32,              # slots, lens, offsets, n_rows, L
+        _I32, _I32, _I32, _I32, _F,          # H, HV, K, V, scale
+        _P, _P, _P]),                        # o, sq, stream
+    "hsg_gdn_slot_step_gated": (ctypes.c_int, [
+        _P, _I64, _I32, _I32, _I32,
+        _P, _P, _I64, _P, _P,
+        _P, _I32, _I64,
+        _P, _P, _P, _I32, _I32,
+        _I32, _I32, _I32, _I32, _F,
+        _P, _I64, _P, _F, _P, _P]),          # z, z_stride, norm_w, eps, out, stream
+    "hsg_ring_attention": (ctypes.c_int, [
+        _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
+        _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window
+        _P, _I64, _I64, _I64,                # new_k, nk_sn, nk_sl, nk_sh
+        _P, _I64, _I64, _I64,                # new_v, nv_sn, nv_sl, nv_sh
+        _P, _I64, _I64, _I64, _I64, _I64,    # gate, g_sn, g_sl, g_sh, g_sg, g_off
+        _P, _P, _P, _P, _P,                  # ring_pos, slots, starts, lens, offsets
+        _I32, _I32, _I32, _I32, _I32, _F, _I32,  # n_rows, lb, hkv, groups, head_dim, scale, write_ring
+        _P, _I64, _I64, _I64, _I64, _P]),    # out, o_sn, o_sl, o_sh, o_sg, stream
+}
+
+_lib = None
+
+
+def lib():
+    """Load libhsg.so once and attach the signatures; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"HS-Guard HIP library not built: {LIB_PATH} is missing "
+                               "(run `python -c 'import __graft_entry__ as g; g.build()'` at the repo root)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def check(rc, name):
+    """Map a non-zero return code of an hsg_* call to an exception (ValueError for rejected arguments)."""
+    if rc == 0:
+        return
+    text = lib().hsg_error_string(rc).decode()
+    if rc < 0:
+        raise ValueError(f"{name}: {text} (code {rc})")
+    raise RuntimeError(f"{name}: HIP launch failed: {text} (code {rc})")

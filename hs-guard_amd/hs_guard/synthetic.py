@@ -1,0 +1,91 @@
+"""Seeded synthetic inputs of the BASELINE configurations (generated on the CPU, then moved).
+
+Every generator draws from one ``torch.Generator`` seeded as given (0 by default) in the documented order,
+so the GPU path and the CPU checker consume identical bytes.
+"""
+from __future__ import annotations
+
+import torch
+
+BF16 = torch.bfloat16
+
+
+def _bf16_randn(gen, *shape):
+    return torch.randn(*shape, generator=gen).to(BF16)
+
+
+def _l2_bf16(x):
+    xf = x.float()
+    return (xf / xf.norm(dim=-1, keepdim=True)).to(BF16)
+
+
+def gdn_step_inputs(slots=16, heads=16, head_dim=128, steps=64, seed=0, state_dtype=torch.float32):
+    """Config 1: ``slots`` rows x 1 token for ``steps`` sequential steps, H = HV = heads, K = V = head_dim.
+
+    Draw order: state0 [slots+1, H, K, V] ~ N(0, 0.02) (the extra row is the scratch slot, zeroed), then per
+    step q [slots, H, K], k [slots, H, K] (bf16 N(0,1), then L2-normalised per head and rounded to bf16),
+    v [slots, H, V] bf16 N(0,1), a [slots, H] bf16 N(0,1), b [slots, H] bf16 N(0,1). A_log = dt_bias = 0,
+    so the kernel's g = -softplus(a) and beta = sigmoid(b).
+    Returns dict with state0, packed [steps, slots, 1, 3*H*K], a/b [steps, slots, 1, H], A_log, dt_bias.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    H, K = heads, head_dim
+    state0 = torch.randn(slots + 1, H, K, K, generator=gen) * 0.02
+    state0[slots] = 0
+    packed, a_all, b_all = [], [], []
+    for _ in range(steps):
+        q = _l2_bf16(_bf16_randn(gen, slots, H, K))
+        k = _l2_bf16(_bf16_randn(gen, slots, H, K))
+        v = _bf16_randn(gen, slots, H, K)
+        a = _bf16_randn(gen, slots, H)
+        b = _bf16_randn(gen, slots, H)
+        packed.append(torch.cat([q.reshape(slots, -1), k.reshape(slots, -1), v.reshape(slots, -1)], -1)[:, None])
+        a_all.append(a[:, None])
+        b_all.append(b[:, None])
+    return {
+        "state0": state0.to(state_dtype),
+        "packed": torch.stack(packed),
+        "a": torch.stack(a_all),
+        "b": torch.stack(b_all),
+        "A_log": torch.zeros(H, dtype=BF16),
+        "dt_bias": torch.zeros(H, dtype=BF16),
+        "heads": H,
+        "head_dim": K,
+    }
+
+
+def ring_decode_inputs(rows=64, hq=16, hkv=4, head_dim=256, window=512, seed=0, pool_rows=None):
+    """Config 2: ``rows`` slots x 1 new token, GQA hq/hkv, ring [pool_rows, hkv, window+1, D].
+
+    Draw order: per row ptr ~ U{0..W-1} and fill ~ U{1..W} (both via torch.randint), then q [rows, hkv,
+    G, D], ring_k, ring_v [pool_rows, hkv, W+1, D], new_k [rows, hkv, 1, D], new_v [rows, hkv, 1, D],
+    gate [rows, hq, D], all bf16 N(0,1). start = 16 W + ptr; ring_pos[c] = p for p in [start-fill, start-1]
+    with c = p mod W, else -1 (column W is -1). Slot of row r is r (pool_rows defaults to rows + 1, the
+    last row being the scratch slot).
+    """
+    gen = torch.Generator().manual_seed(seed)
+    W, D, G = window, head_dim, hq // hkv
+    S = rows + 1 if pool_rows is None else pool_rows
+    ptr = torch.randint(0, W, (rows,), generator=gen)
+    fill = torch.randint(1, W + 1, (rows,), generator=gen)
+    q = _bf16_randn(gen, rows, hkv, G, D)
+    ring_k = _bf16_randn(gen, S, hkv, W + 1, D)
+    ring_v = _bf16_randn(gen, S, hkv, W + 1, D)
+    new_k = _bf16_randn(gen, rows, hkv, 1, D)
+    new_v = _bf16_randn(gen, rows, hkv, 1, D)
+    gate_half = _bf16_randn(gen, rows, hq, D)
+    starts = 16 * W + ptr
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for r in range(rows):
+        for p in range(int(starts[r] - fill[r]), int(starts[r])):
+            ring_pos[r, p % W] = p
+    # q_proj output layout [N, 1, Hq*2D]: query half (unused here) then gate half per head
+    gate = torch.cat([torch.zeros(rows, hq, D, dtype=BF16), gate_half], -1).reshape(rows, 1, hq * 2 * D)
+    value = new_v.permute(0, 2, 1, 3).reshape(rows, 1, hkv * D).contiguous()
+    return {
+        "q": q.reshape(rows, hkv, G, D).contiguous(),
+        "ring_k": ring_k, "ring_v": ring_v, "new_k": new_k, "new_v": new_v, "value": value,
+        "gate": gate, "ring_pos": ring_pos, "slots": torch.arange(rows, dtype=torch.long),
+        "starts": starts.long(), "lens": torch.ones(rows, dtype=torch.long), "fill": fill, "ptr": ptr,
+        "window": W, "hq": hq, "hkv": hkv, "head_dim": D,
+    }

@@ -1,0 +1,109 @@
+/*
+ * hsg.h -- C ABI of libhsg.so, the MI355X (gfx950) kernels of HS-Guard's streaming slot step.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HIP global memory); sizes and strides are in ELEMENTS.
+ *   - bf16 / fp16 tensors are passed as raw 16-bit storage (void*); int64 index tensors as int64_t*.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *   - Nothing allocates, synchronizes or reads device memory on the host, so every call can be
+ *     recorded into a hipGraph. Kernels mutate the per-slot pools in place at rows slots[n].
+ *   - Row layout: when `offsets` is NULL, row n's tokens are positions n*L .. n*L+L-1 (the reference's
+ *     padded [N, L, ...] layout; positions >= lens[n] are written as zeros). When `offsets` is non-NULL
+ *     (packed layout) row n's tokens are positions offsets[n] .. offsets[n]+lens[n]-1 and nothing else is
+ *     written.
+ *   - A row whose slot lies outside [0, state_rows) is treated as empty (lens 0).
+ *   - Return value: HSG_OK (0), a negative HSG_ERR_* for a rejected argument (nothing launched), or a
+ *     positive hipError_t from the launch.
+ *
+ * Reference interfaces each entry point replaces are cited as path:line in the HS-Guard repository.
+ */
+#ifndef HSG_H_
+#define HSG_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HSG_OK 0
+#define HSG_ERR_ARG (-1)     /* null pointer or non-positive / inconsistent size */
+#define HSG_ERR_ALIGN (-2)   /* pointer or stride breaks the vector-load alignment the kernel needs */
+#define HSG_ERR_SHAPE (-3)   /* head size / window outside what the kernels are built for */
+
+#define HSG_STATE_F32 0
+#define HSG_STATE_F16 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int hsg_version(void);
+
+/* Human-readable text for an HSG_ERR_* or hipError_t code. */
+const char* hsg_error_string(int code);
+
+/*
+ * Gated-delta-rule recurrent slot step.
+ * Replaces gdn_slot_v8 (src/hs_guard/engine/fused_kernels.py:197-211; kernel :140-194) and
+ * gdn_slot_recurrent (src/hs_guard/engine/gdn_slot_kernel.py:57-73).
+ *   qkv      [tokens, qkv_stride] bf16; q of key head h at q_off + h*K, k at k_off + h*K,
+ *            v of value head hv at v_off + hv*V (conv_silu_update output layout).
+ *   a, b     [tokens, ab_stride] bf16 raw projections (column hv).
+ *   A_log, dt_bias [HV] bf16.
+ *   state    [state_rows, HV, K, V] fp32 (state_dtype HSG_STATE_F32) or fp16; V contiguous.
+ *   o        [tokens, HV, V] bf16;  sq [tokens, HV, V] fp32 = bf16(o)^2 (sq may be NULL).
+ * Supported: K == V == 128, HV % H == 0.
+ */
+int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
+                      const void* a, const void* b, int64_t ab_stride, const void* A_log,
+                      const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
+                      const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
+                      int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
+                      float* sq, void* stream);
+
+/*
+ * The same step with Qwen3.5's gated RMSNorm fused into the epilogue.
+ * Replaces gdn_slot_v8 followed by gated_finish (src/hs_guard/engine/fused_kernels.py:215-233,
+ * composed at src/hs_guard/engine/slot_engine_v8.py:234-238):
+ *   out[tok, hv*V + c] = bf16( bf16(w[c] * bf16(o*rsqrt(mean(bf16(o)^2)+eps))) * silu(z[tok, hv*V + c]) )
+ *   z [tokens, z_stride] bf16, norm_w [V] bf16, out [tokens, HV*V] bf16.
+ */
+int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
+                            int32_t v_off, const void* a, const void* b, int64_t ab_stride,
+                            const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
+                            int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                            const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
+                            int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
+                            const void* norm_w, float eps, void* out, void* stream);
+
+/*
+ * Window-W GQA attention of this tick's queries over the slot's ring plus this tick's new keys.
+ * Replaces ring_attention_v8 (src/hs_guard/engine/fused_kernels.py:358-376; kernel :288-356),
+ * ring_attention (src/hs_guard/engine/ring_attention_kernel.py:91-105) and the Lb > 1 ring scatter
+ * (src/hs_guard/engine/slot_engine_v8.py:253-255).
+ * Element addresses (row base B(x) = offsets ? offsets[n]*x_sl : n*x_sn):
+ *   q[n,l,h,g,:]     = q     + B(q) + l*q_sl + h*q_sh + g*q_sg
+ *   new_k[n,l,h,:]   = new_k + B(nk) + l*nk_sl + h*nk_sh         (same for new_v)
+ *   gate[n,l,h,g,:]  = gate  + B(g) + l*g_sl + h*g_sh + g*g_sg + g_off   (gate may be NULL: no gating)
+ *   out[n,l,h,g,:]   = out   + B(o) + l*o_sl + h*o_sh + g*o_sg
+ *   ring_k/ring_v    [ring_rows, hkv, window+1, head_dim] bf16, ring_pos [ring_rows, window+1] int64.
+ * Key j of the ring (column c < window, position ring_pos[slot,c]) or of the tick (position start+j when
+ * j < len) is visible to query step l (position start+l, l < len) iff 0 <= kpos <= qpos and
+ * kpos > qpos - window. Output = softmax-weighted values, rounded to bf16, times bf16(sigmoid(gate)).
+ * write_ring != 0: after every read, new key/value of each valid step j go to ring column
+ * (start+j) % window. ring_pos itself is not written (see hsg_ring_pos_update).
+ * Supported: head_dim == 256, window <= 512 and a multiple of 16, lb <= 64.
+ */
+int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,
+                       void* ring_k, void* ring_v, int64_t ring_rows, int32_t window, const void* new_k,
+                       int64_t nk_sn, int64_t nk_sl, int64_t nk_sh, const void* new_v, int64_t nv_sn,
+                       int64_t nv_sl, int64_t nv_sh, const void* gate, int64_t g_sn, int64_t g_sl,
+                       int64_t g_sh, int64_t g_sg, int64_t g_off, const int64_t* ring_pos,
+                       const int64_t* slots, const int64_t* starts, const int64_t* lens,
+                       const int64_t* offsets, int32_t n_rows, int32_t lb, int32_t hkv, int32_t groups,
+                       int32_t head_dim, float scale, int32_t write_ring, void* out, int64_t o_sn,
+                       int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HSG_H_ */

@@ -1,0 +1,56 @@
+"""The C-ABI library loads and exports every entry point include/hsg.h declares (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hsg.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hsg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "hsg_gdn_slot_step" in names and "hsg_ring_attention" in names
+
+
+def test_library_exports_every_declared_symbol():
+    from hs_guard._lib import LIB_PATH, SIGNATURES
+    if not os.path.exists(LIB_PATH):
+        pytest.fail(f"{LIB_PATH} missing: build() first")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name in _declared():
+        assert hasattr(handle, name), f"{name} not exported"
+    assert set(SIGNATURES) == set(_declared()), "ctypes signatures out of sync with include/hsg.h"
+
+
+def test_version_and_error_strings():
+    from hs_guard._lib import lib
+    assert lib().hsg_version() >= 100
+    assert b"alignment" in lib().hsg_error_string(-2)
+
+
+def test_argument_errors_are_rejected_before_launch():
+    """Invalid shapes return HSG_ERR_* without touching the GPU (null pointers are never dereferenced)."""
+    from hs_guard._lib import lib
+    L = lib()
+    # n_rows > 0 with null pointers -> HSG_ERR_ARG; unsupported head size -> HSG_ERR_SHAPE
+    rc = L.hsg_gdn_slot_step(None, 6144, 0, 2048, 4096, None, None, 16, None, None, None, 0, 17, None, None, None,
+                             4, 1, 16, 16, 128, 128, 1.0, None, None, None)
+    assert rc == -1
+    rc = L.hsg_gdn_slot_step(8, 6144, 0, 2048, 4096, 8, 8, 16, 8, 8, 16, 0, 17, 8, 8, None, 4, 1, 16, 16, 64, 128,
+                             1.0, 8, None, None)
+    assert rc == -3
+    rc = L.hsg_ring_attention(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
+                              8, 8, 8, 8, None, 2, 1, 4, 4, 128, 1.0, 0, 16, 0, 0, 0, 0, None)
+    assert rc == -3
+    # n_rows == 0 is a no-op success
+    assert L.hsg_ring_attention(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                                0, 0, None, None, None, None, None, 0, 1, 4, 4, 256, 1.0, 0, None, 0, 0, 0, 0,
+                                None) == 0

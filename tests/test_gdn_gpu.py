@@ -1,0 +1,168 @@
+"""GPU parity of the GDN slot step (hsg_gdn_slot_step / _gated) against the CPU oracle.
+
+Tolerances (north star): fp32 recurrent state within 1e-3 relative error, both as the norm ratio
+||S_gpu - S_ref|| / ||S_ref|| and as max |S_gpu - S_ref| / max |S_ref|. bf16 outputs within one bf16
+rounding (2**-8 relative) plus 1e-3 of the output scale. Untouched pool rows are compared bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn as ogdn
+from oracle import glue as oglue
+
+pytestmark = pytest.mark.gpu
+
+STATE_TOL = 1e-3
+
+
+def _state_err(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    d = got - ref
+    return float(np.linalg.norm(d) / np.linalg.norm(ref)), float(np.abs(d).max() / np.abs(ref).max())
+
+
+def _out_close(got, ref, rtol=2.0 ** -8, atol_frac=1e-3):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    atol = atol_frac * max(np.abs(ref).max(), 1e-30)
+    bad = np.abs(got - ref) > rtol * np.abs(ref) + atol
+    return int(bad.sum()), float(np.abs(got - ref).max())
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.float16])
+def test_config1_64_steps(state_dtype):
+    """Config 1: 16 slots x 1 token, 16 heads x 128, 64 sequential steps, seed 0."""
+    from hs_guard.engine.kernels import gdn_slot_v8
+    from hs_guard.synthetic import gdn_step_inputs
+    print(f"[gdn] config1 state={state_dtype}", flush=True)
+    inp = gdn_step_inputs(state_dtype=state_dtype)
+    H, K = inp["heads"], inp["head_dim"]
+    dev = torch.device("cuda:0")
+    state = inp["state0"].to(dev)
+    slots = torch.arange(16, dtype=torch.long, device=dev)
+    lens = torch.ones(16, dtype=torch.long, device=dev)
+    A_log, dt = inp["A_log"].to(dev), inp["dt_bias"].to(dev)
+    ref_state = _np(inp["state0"]).astype(np.float64)
+    for t in range(inp["packed"].shape[0]):
+        packed = inp["packed"][t]
+        o, sq = gdn_slot_v8(packed.to(dev), H * K, H, K, H, K, inp["a"][t].to(dev), inp["b"][t].to(dev),
+                            A_log, dt, state, slots, lens)
+        o_ref, sq_ref, ref_state = ogdn.gdn_slot_step(_np(packed), H * K, H, K, H, K, _np(inp["a"][t]),
+                                                      _np(inp["b"][t]), _np(inp["A_log"]), _np(inp["dt_bias"]),
+                                                      ref_state, np.arange(16), np.ones(16, np.int64))
+        if state_dtype == torch.float16:
+            ref_state = ref_state.astype(np.float16).astype(np.float64)  # storage rounding of the pool
+        bad, worst = _out_close(_np(o), o_ref, rtol=2.0 ** -7 if state_dtype == torch.float16 else 2.0 ** -8)
+        assert bad == 0, f"step {t}: {bad} outputs off (max diff {worst})"
+        ob = _np(o).astype(np.float64)
+        np.testing.assert_array_equal(_np(sq), (ob * ob).astype(np.float32))
+    torch.cuda.synchronize()
+    rel, mx = _state_err(_np(state[:16]), ref_state[:16])
+    tol = STATE_TOL if state_dtype == torch.float32 else 4e-3
+    assert rel <= tol and mx <= tol, f"state error norm {rel:.2e} max {mx:.2e}"
+    assert torch.count_nonzero(state[16]).item() == 0  # scratch slot untouched
+
+
+def test_multi_token_and_padding():
+    """L=7 tick with lens [7, 3, 0, 1, 5]; slots permuted; a row with lens 0 leaves its slot bit-exact."""
+    from hs_guard.engine.kernels import gdn_slot_v8
+    print("[gdn] multi-token padded tick", flush=True)
+    gen = torch.Generator().manual_seed(1)
+    N, L, H, K = 5, 7, 4, 128
+    HV = 8  # two value heads per key head
+    S = 9
+    packed = torch.randn(N, L, 2 * H * K + HV * K, generator=gen).to(torch.bfloat16)
+    a = torch.randn(N, L, HV, generator=gen).to(torch.bfloat16)
+    b = torch.randn(N, L, HV, generator=gen).to(torch.bfloat16)
+    A_log = (torch.rand(HV, generator=gen) * 2 - 1).to(torch.bfloat16)
+    dt = torch.randn(HV, generator=gen).to(torch.bfloat16)
+    state0 = torch.randn(S, HV, K, K, generator=gen) * 0.05
+    slots = torch.tensor([6, 2, 4, 0, 8], dtype=torch.long)
+    lens = torch.tensor([7, 3, 0, 1, 5], dtype=torch.long)
+    dev = torch.device("cuda:0")
+    state = state0.to(dev)
+    o, sq = gdn_slot_v8(packed.to(dev), H * K, H, K, HV, K, a.to(dev), b.to(dev), A_log.to(dev), dt.to(dev),
+                        state, slots.to(dev), lens.to(dev))
+    o_ref, _, st_ref = ogdn.gdn_slot_step(_np(packed), H * K, H, K, HV, K, _np(a), _np(b), _np(A_log), _np(dt),
+                                          _np(state0), slots.numpy(), lens.numpy())
+    bad, worst = _out_close(_np(o), o_ref)
+    assert bad == 0, f"{bad} outputs off (max diff {worst})"
+    for n in range(N):
+        assert torch.count_nonzero(o[n, int(lens[n]):]).item() == 0
+    got = _np(state)
+    for s in range(S):
+        if s in (6, 2, 0, 8):
+            rel, mx = _state_err(got[s], st_ref[s])
+            assert rel <= STATE_TOL and mx <= STATE_TOL, f"slot {s}: {rel:.2e} {mx:.2e}"
+        else:  # slot 4 (lens 0) and unused slots are not touched
+            np.testing.assert_array_equal(got[s], _np(state0[s]))
+
+
+def test_packed_gated_matches_oracle():
+    """Packed rows (offsets) with the fused gated RMSNorm epilogue, z read from a strided projection."""
+    from hs_guard._lib import lib
+    print("[gdn] packed + gated", flush=True)
+    gen = torch.Generator().manual_seed(2)
+    H = HV = 16
+    K = 128
+    lens = torch.tensor([3, 1, 0, 4], dtype=torch.long)
+    offsets = torch.tensor([0, 3, 4, 4], dtype=torch.long)
+    T = int(lens.sum())
+    C = 2 * H * K + HV * K
+    stride = C + HV * K + 2 * HV + 8   # fused projection row: qkv | z | b | a | pad
+    proj = torch.randn(T, stride, generator=gen).to(torch.bfloat16)
+    qkv, z = proj[:, :C], proj[:, C:C + HV * K]
+    ab = torch.randn(T, 2 * HV, generator=gen).to(torch.bfloat16)
+    A_log = torch.zeros(HV, dtype=torch.bfloat16)
+    dt = (torch.randn(HV, generator=gen) * 0.5).to(torch.bfloat16)
+    norm_w = (1 + 0.1 * torch.randn(K, generator=gen)).to(torch.bfloat16)
+    state0 = torch.randn(6, HV, K, K, generator=gen) * 0.02
+    slots = torch.tensor([1, 3, 0, 5], dtype=torch.long)
+    dev = torch.device("cuda:0")
+    proj_d, ab_d, state = proj.to(dev), ab.to(dev), state0.to(dev)
+    out = torch.empty(T, HV * K, dtype=torch.bfloat16, device=dev)
+    slots_d, lens_d, off_d = slots.to(dev), lens.to(dev), offsets.to(dev)
+    A_d, dt_d, w_d = A_log.to(dev), dt.to(dev), norm_w.to(dev)
+    rc = lib().hsg_gdn_slot_step_gated(
+        proj_d.data_ptr(), stride, 0, H * K, 2 * H * K, ab_d[:, HV:].data_ptr(), ab_d.data_ptr(), 2 * HV,
+        A_d.data_ptr(), dt_d.data_ptr(), state.data_ptr(), 0, 6, slots_d.data_ptr(), lens_d.data_ptr(),
+        off_d.data_ptr(), 4, 0, H, HV, K, K, K ** -0.5, proj_d[:, C:].data_ptr(), stride, w_d.data_ptr(), 1e-6,
+        out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    # oracle in padded form
+    L = int(lens.max())
+    packed_pad = np.zeros((4, L, C))
+    a_pad = np.zeros((4, L, HV))
+    b_pad = np.zeros((4, L, HV))
+    z_pad = np.zeros((4, L, HV, K))
+    for n in range(4):
+        o0, ln = int(offsets[n]), int(lens[n])
+        packed_pad[n, :ln] = _np(qkv[o0:o0 + ln])
+        a_pad[n, :ln] = _np(ab[o0:o0 + ln, HV:])
+        b_pad[n, :ln] = _np(ab[o0:o0 + ln, :HV])
+        z_pad[n, :ln] = _np(z[o0:o0 + ln]).reshape(ln, HV, K)
+    o_ref, _, st_ref = ogdn.gdn_slot_step(packed_pad, H * K, H, K, HV, K, a_pad, b_pad, _np(A_log), _np(dt),
+                                          _np(state0), slots.numpy(), lens.numpy())
+    from oracle.bf16 import bf16
+    gated_ref = oglue.gated_rmsnorm(bf16(o_ref), z_pad, _np(norm_w), 1e-6)
+    got = _np(out)
+    for n in range(4):
+        o0, ln = int(offsets[n]), int(lens[n])
+        if ln == 0:
+            continue
+        bad, worst = _out_close(got[o0:o0 + ln], gated_ref[n, :ln].reshape(ln, HV * K), rtol=2.0 ** -6,
+                                atol_frac=4e-3)
+        assert bad == 0, f"row {n}: {bad} gated outputs off (max {worst})"
+    torch.cuda.synchronize()
+    gs = _np(state)
+    for s in (1, 3, 5):
+        rel, mx = _state_err(gs[s], st_ref[s])
+        assert rel <= STATE_TOL and mx <= STATE_TOL
+    np.testing.assert_array_equal(gs[0], _np(state0[0]))
+    np.testing.assert_array_equal(gs[2], _np(state0[2]))

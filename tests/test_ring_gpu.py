@@ -1,0 +1,102 @@
+"""GPU parity of the ring-window attention (hsg_ring_attention) against the CPU oracle.
+
+Outputs are bf16: they must agree with the float64 oracle (rounded at the reference's rounding points)
+within two bf16 rounding steps (2**-7 relative) plus 1e-3 of the output scale. Ring writes and untouched
+ring columns are compared bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ring as oring
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _check(got, ref, rtol=2.0 ** -7, atol_frac=1e-3, what="out"):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    atol = atol_frac * max(np.abs(ref).max(), 1e-30)
+    bad = np.abs(got - ref) > rtol * np.abs(ref) + atol
+    assert not bad.any(), f"{what}: {int(bad.sum())} values off, max diff {np.abs(got - ref).max():.3e}"
+
+
+def test_config2_decode_with_ring_write():
+    """Config 2: 64 slots x 1 token, 16q/4kv, D=256, W=512, random write pointer and fill, seed 0."""
+    from hs_guard.engine.kernels import ring_attention_v8
+    from hs_guard.synthetic import ring_decode_inputs
+    print("[ring] config2 decode + write", flush=True)
+    inp = ring_decode_inputs()
+    dev = torch.device("cuda:0")
+    W, D = inp["window"], inp["head_dim"]
+    d = {k: v.to(dev) for k, v in inp.items() if torch.is_tensor(v)}
+    rk, rv = d["ring_k"].clone(), d["ring_v"].clone()
+    out = ring_attention_v8(d["q"].reshape(64, 4, 4, D), rk, rv, d["new_k"], d["value"], d["gate"], d["ring_pos"],
+                            d["slots"], d["starts"], d["lens"], D ** -0.5, W, True)
+    ref, _, rk_ref, rv_ref = oring.ring_attention_v8(
+        _np(inp["q"]), _np(inp["ring_k"]), _np(inp["ring_v"]), _np(inp["new_k"]), _np(inp["value"]),
+        _np(inp["gate"]), inp["ring_pos"].numpy(), inp["slots"].numpy(), inp["starts"].numpy(),
+        inp["lens"].numpy(), D ** -0.5, W, True)
+    _check(_np(out), ref)
+    np.testing.assert_array_equal(_np(rk), rk_ref)   # written column = start % W, others untouched
+    np.testing.assert_array_equal(_np(rv), rv_ref)
+
+
+def test_multi_token_tick_no_write():
+    """Lb=4 tick with lens [4, 2, 0, 1] (v8 contract, write_ring False): masking of the new keys."""
+    from hs_guard.engine.kernels import ring_attention_v8
+    print("[ring] Lb=4 tick", flush=True)
+    gen = torch.Generator().manual_seed(3)
+    N, Hkv, G, D, W, Lb = 4, 4, 4, 256, 512, 4
+    S = 6
+    q = torch.randn(N, Hkv, G * Lb, D, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    new_k = torch.randn(N, Hkv, Lb, D, generator=gen).to(torch.bfloat16)
+    value = torch.randn(N, Lb, Hkv * D, generator=gen).to(torch.bfloat16)
+    gate = torch.randn(N, Lb, Hkv * G * 2 * D, generator=gen).to(torch.bfloat16)
+    slots = torch.tensor([3, 0, 5, 1])
+    starts = torch.tensor([700, 5, 0, 511])
+    lens = torch.tensor([4, 2, 0, 1])
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s, st in zip(slots.tolist(), starts.tolist()):
+        for p in range(max(0, st - 600), st):
+            ring_pos[s, p % W] = p
+    dev = torch.device("cuda:0")
+    out = ring_attention_v8(q.to(dev), ring_k.to(dev), ring_v.to(dev), new_k.to(dev), value.to(dev), gate.to(dev),
+                            ring_pos.to(dev), slots.to(dev), starts.to(dev), lens.to(dev), D ** -0.5, W, False)
+    ref, _, _, _ = oring.ring_attention_v8(_np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(value), _np(gate),
+                                           ring_pos.numpy(), slots.numpy(), starts.numpy(), lens.numpy(),
+                                           D ** -0.5, W, False)
+    _check(_np(out), ref)
+    assert torch.count_nonzero(out[2]).item() == 0  # lens 0 row
+
+
+def test_reference_contract_ungated():
+    """ring_attention (v4 contract, ungated [N, Hkv, G*Lb, D] output) vs ring_attention_reference."""
+    from hs_guard.engine.kernels import ring_attention
+    print("[ring] ungated contract", flush=True)
+    gen = torch.Generator().manual_seed(4)
+    N, Hkv, G, D, W, Lb = 3, 2, 4, 256, 512, 2
+    S = 4
+    q = torch.randn(N, Hkv, G * Lb, D, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    new_k = torch.randn(N, Hkv, Lb, D, generator=gen).to(torch.bfloat16)
+    new_v = torch.randn(N, Hkv, Lb, D, generator=gen).to(torch.bfloat16)
+    slots, starts, lens = torch.tensor([2, 0, 1]), torch.tensor([1000, 3, 40]), torch.tensor([2, 2, 1])
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s, st in zip(slots.tolist(), starts.tolist()):
+        for p in range(0, st):
+            ring_pos[s, p % W] = p
+    dev = torch.device("cuda:0")
+    out = ring_attention(q.to(dev), ring_k.to(dev), ring_v.to(dev), new_k.to(dev), new_v.to(dev), ring_pos.to(dev),
+                         slots.to(dev), starts.to(dev), lens.to(dev), D ** -0.5, W)
+    ref = oring.ring_attention_reference(_np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(new_v), ring_pos.numpy(),
+                                         slots.numpy(), starts.numpy(), lens.numpy(), D ** -0.5, W)
+    from oracle.bf16 import bf16
+    _check(_np(out), bf16(ref), rtol=2.0 ** -8)
