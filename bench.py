@@ -1,0 +1,286 @@
+"""Benchmark of the streaming slot step on one MI355X (BASELINE.json's metric and config 5).
+
+Workload (config 5, mixed serving): 352 concurrent slots on the full random-init backbone (hidden 1024,
+24 layers 3 GDN : 1 attention, GDN 16x128, attention 16q/4kv/256, MLP 3584, vocab 151,936, bf16 weights
+N(0, 0.02)), fp32 recurrent state. Every slot first gets an initial context drawn uniformly from
+{512, 2048, 8000} tokens (untimed prefill). Each step every slot appends c tokens, c = 1 (p 0.8),
+U{2..16} (p 0.15), U{17..64} (p 0.05); the step is one StreamingGuard-engine tick under hipGraph:
+H2D of the packed tick, graph replay, D2H of both roles' probabilities, stream sync. After each step every
+slot is reset with p = 0.01 and re-prefilled with a fresh context, untimed (prefill is outside the
+reference's timing scope, docs/technical_report.tex:117).
+
+value = streamed tokens / summed host-to-host step time over the K timed steps. Also reported: p50/p95
+of those step times, the pure 352 x 1-token decode step and the 1-slot single-token step (20 warm-up +
+200 measured each, docs/technical_report.tex:115), the roofline of the dominant kernel (the GDN slot step
+at the 352 x 1-token decode shape, HIP events on its launch stream) and the CPU baseline (the repo's CPU
+restatement of the same step timed on this host on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "hs-guard_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+REF_L20 = {"min_tokens_per_s_352": 15075.6, "worst_p95_ms_352": 18.368, "single_token_p50_ms": 2.384}
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def percentile(xs, q):
+    import numpy as np
+    return float(np.percentile(np.asarray(xs), q))
+
+
+def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
+    """Average duration of hsg_gdn_slot_step_gated at the decode shape (rows x 1 token, 16 heads x 128x128),
+    HIP events recorded on the stream the kernel is launched on. Algorithmic bytes per launch: per (row,
+    head) the state read + write 2*K*V*4 B, plus per (row, head, token) q, k, v, z in and out = 5 x 256 B and
+    a, b = 4 B."""
+    dev = torch.device("cuda:0")
+    H = HV = 16
+    K = V = 128
+    C = 3 * H * K
+    stride = C + HV * V + 2 * HV
+    gen = torch.Generator(device=dev).manual_seed(1)
+    state = (torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02)
+    if state_dtype == 1:
+        state = state.half()
+    conv = torch.randn(rows, C, generator=gen, device=dev).bfloat16()
+    proj = torch.randn(rows, stride, generator=gen, device=dev).bfloat16()
+    out = torch.empty(rows, HV * V, dtype=torch.bfloat16, device=dev)
+    A = torch.zeros(HV, dtype=torch.bfloat16, device=dev)
+    w = torch.ones(V, dtype=torch.bfloat16, device=dev)
+    slots = torch.arange(rows, device=dev)
+    lens = torch.ones(rows, dtype=torch.long, device=dev)
+    offs = torch.arange(rows, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    base = proj.data_ptr()
+
+    def launch():
+        rc = lib.hsg_gdn_slot_step_gated(conv.data_ptr(), C, 0, H * K, 2 * H * K, base + 2 * (C + HV * V + HV),
+                                         base + 2 * (C + HV * V), stride, A.data_ptr(), A.data_ptr(), state.data_ptr(),
+                                         state_dtype, rows + 1, slots.data_ptr(), lens.data_ptr(), offs.data_ptr(),
+                                         rows, 0, H, HV, K, V, K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6,
+                                         out.data_ptr(), stream.cuda_stream)
+        assert rc == 0, rc
+    for _ in range(10):
+        launch()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(iters):
+        launch()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / iters
+    elem = 4 if state_dtype == 0 else 2
+    per_unit_state = 2 * K * V * elem
+    per_token = 5 * 256 + 4
+    traffic_alg = rows * HV * (per_unit_state + per_token)
+    gbs = traffic_alg / (us * 1e-6) / 1e9
+    return {"kernel": "gdn_step_kernel (hsg_gdn_slot_step_gated)", "shape": f"{rows} rows x 1 token x 16 heads",
+            "avg_us": round(us, 2), "alg_bytes_per_launch": traffic_alg, "achieved_gbs": round(gbs, 1)}
+
+
+def ring_decode_rate(torch, rows=352, iters=50):
+    """Achieved algorithmic GB/s of hsg_ring_attention at the 352 x 1-token decode shape with full rings."""
+    from hs_guard.engine.kernels import ring_attention_v8
+    from hs_guard.synthetic import ring_decode_inputs
+    r = ring_decode_inputs(rows=rows)
+    d = {k: v.to("cuda:0") for k, v in r.items() if torch.is_tensor(v)}
+
+    def run():
+        ring_attention_v8(d["q"], d["ring_k"], d["ring_v"], d["new_k"], d["value"], d["gate"], d["ring_pos"],
+                          d["slots"], d["starts"], d["lens"], 1 / 16, 512, False)
+    for _ in range(5):
+        run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(iters):
+        run()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / iters
+    valid = sum(min(int(f), 511) for f in r["fill"])
+    alg = valid * 4 * 256 * 2 * 2 + rows * 16 * 256 * 2 * 3 + rows * 4 * 256 * 2 * 2 + valid * 8
+    return {"avg_us": round(us, 2), "alg_bytes_per_launch": alg, "achieved_gbs": round(alg / (us * 1e-6) / 1e9, 1)}
+
+
+def cpu_baseline(model, cfg, seed=0, slots=8, ticks=3):
+    """The CPU restatement (oracle.backbone.StreamOracle: numpy fp32 GEMMs, float64 recurrence) on a bounded
+    sample of config 5: ``slots`` slots with a 32-token context (untimed), then ``ticks`` mixed ticks with
+    config-5 chunk sizes. Returns streamed tokens per CPU second."""
+    import numpy as np
+    from oracle.backbone import StreamOracle
+    from hs_guard.synthetic import MixedServingLoad
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        cores = os.cpu_count()
+    w = {k: v.float().cpu().numpy() for k, v in model.weights.items()}
+    orc = StreamOracle(w, cfg, max_slots=slots)
+    load = MixedServingLoad(slots=slots, vocab=cfg.vocab_size, seed=seed + 7)
+    rng = np.random.default_rng(seed)
+    orc.step([(s, rng.integers(0, cfg.vocab_size, 32).tolist()) for s in range(slots)])
+    tokens, secs = 0, 0.0
+    for _ in range(ticks):
+        req = load.step_requests()
+        t0 = time.perf_counter()
+        orc.step(req)
+        secs += time.perf_counter() - t0
+        tokens += sum(len(ids) for _, ids in req)
+    return {"value": round(tokens / secs, 2), "unit": "tokens/s", "cores": int(cores), "kind": "port",
+            "sample": f"oracle.backbone.StreamOracle, full backbone, {slots} slots after 32-token contexts, "
+                      f"{ticks} config-5 mixed ticks ({tokens} tokens, {secs:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--slots", type=int, default=352)
+    ap.add_argument("--state-dtype", default="float32", choices=("float32", "float16"))
+    ap.add_argument("--contexts", default="512,2048,8000")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant-kernel measurement (the command profiled under rocprofv3)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU: the streaming step shards by slot with no exchange between GPUs, "
+              f"and this build measures one GPU's share (asked for --gpus {args.gpus}, WORLD_SIZE {world}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from hs_guard._lib import lib
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    from hs_guard.synthetic import MixedServingLoad
+
+    dev = torch.device("cuda:0")
+    log(f"device {torch.cuda.get_device_name(0)}")
+    state_code = 0 if args.state_dtype == "float32" else 1
+    roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
+    log(f"GDN roofline {roof}")
+    if args.roofline_only:
+        print(json.dumps({"roofline_only": roof}), flush=True)
+        return
+    ring = ring_decode_rate(torch, rows=args.slots)
+    log(f"ring decode {ring}")
+
+    cfg = GuardConfig.baseline()
+    t0 = time.time()
+    model = GuardModel.random(cfg, seed=args.seed, device=dev, gen_device=dev)
+    log(f"model {model.num_parameters() / 1e6:.1f}M params in {time.time() - t0:.1f}s")
+    eng = SlotStreamEngine(model, args.slots, state_dtype=args.state_dtype)
+    load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
+                            contexts=tuple(int(x) for x in args.contexts.split(",")))
+
+    # ---- untimed initial contexts ----
+    t0 = time.time()
+    ctx = [(s, load.context()) for s in range(args.slots)]
+    eng.step(ctx)
+    torch.cuda.synchronize()
+    log(f"prefilled {sum(len(c) for _, c in ctx)} context tokens in {time.time() - t0:.1f}s "
+        f"({eng.stats['captures']} graphs)")
+
+    def reprefill(slots):
+        if slots:
+            eng.reset(slots)
+            eng.step([(s, load.context()) for s in slots])
+
+    # ---- warm-up + timed mixed steps ----
+    for i in range(args.warmup):
+        eng.step(load.step_requests())
+        reprefill(load.resets())
+    torch.cuda.synchronize()
+    log("warm-up done")
+    times, tokens = [], 0
+    for i in range(args.steps):
+        req = load.step_requests()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.step(req)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        tokens += sum(len(ids) for _, ids in req)
+        reprefill(load.resets())
+        if (i + 1) % 50 == 0:
+            log(f"step {i + 1}/{args.steps}: {tokens / sum(times):.0f} tok/s")
+    total = sum(times)
+    value = tokens / total
+
+    # ---- pure decode: 352 x 1 token, and 1 slot x 1 token (20 warm-up + 200 measured) ----
+    def timed(make, n=200, warm=20):
+        out = []
+        for i in range(n + warm):
+            req = make()
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            eng.step(req)
+            torch.cuda.synchronize()
+            if i >= warm:
+                out.append((time.perf_counter() - t) * 1e3)
+        return out
+    rng = np.random.default_rng(args.seed + 1)
+    dec = timed(lambda: [(s, [int(rng.integers(0, cfg.vocab_size))]) for s in range(args.slots)])
+    one = timed(lambda: [(0, [int(rng.integers(0, cfg.vocab_size))])])
+    log(f"decode 352x1 p50 {percentile(dec, 50):.3f} ms; single-token p50 {percentile(one, 50):.3f} ms")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        cpu = cpu_baseline(model, cfg, seed=args.seed)
+        log(f"cpu baseline {cpu} in {time.time() - t0:.1f}s")
+
+    step_ms = [t * 1e3 for t in times]
+    result = {
+        "metric": "stream tokens/s @352 slots + p50/p95 single-token step latency (ms)",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REF_L20["min_tokens_per_s_352"], 3),
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02), uniform token ids)",
+        "config": {"workload": "config5 mixed serving: 352 slots, chunks {1 p.8, 2-16 p.15, 17-64 p.05}, contexts "
+                               "U{512,2048,8000} prefilled untimed, resets p=0.01 re-prefilled untimed, hipGraph",
+                   "slots": args.slots, "state_dtype": args.state_dtype, "tokens": tokens,
+                   "geometry": "hidden 1024, 24 layers 3 GDN:1 attn, GDN 16x128, attn 16q/4kv/256 window 512, "
+                               "MLP 3584, vocab 151936", "parallelism": "none (1 GPU)"},
+        "latency_ms": {"p50": round(percentile(step_ms, 50), 3), "p95": round(percentile(step_ms, 95), 3),
+                       "max": round(max(step_ms), 3)},
+        "decode_352x1_ms": {"p50": round(percentile(dec, 50), 3), "p95": round(percentile(dec, 95), 3),
+                            "tokens_per_s": round(args.slots / (np.mean(dec) / 1e3), 1)},
+        "single_token_ms": {"p50": round(percentile(one, 50), 3), "p95": round(percentile(one, 95), 3)},
+        "reference_l20": REF_L20,
+        "roofline": {"bound": "hbm", "achieved": roof["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": roof["kernel"], "shape": roof["shape"], "avg_us": roof["avg_us"],
+                     "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
+        "ring_decode_352": ring,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

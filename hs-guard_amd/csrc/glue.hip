@@ -1,0 +1,367 @@
+// Per-token glue of the streaming step for gfx950: embedding + RMSNorm, residual add + RMSNorm,
+// causal conv + SiLU with the per-slot conv-history update, per-head RMSNorm + partial RoPE, SiLU-mul,
+// the two risk heads, and the ring_pos bookkeeping. Rounding points follow the reference's fused kernels
+// (cited per kernel); every RMSNorm computes its variance in-kernel instead of a separate mean launch.
+#include <math.h>
+
+#include "hsg_common.h"
+
+namespace hsg {
+namespace {
+
+// ---------------------------------------------------------------------------------------------------
+// RMSNorm over a 1024-wide row, one wave per token (16 values per lane, two 16-byte loads).
+// add_square + rms_finish (src/hs_guard/engine/fused_kernels.py:30-72): h = bf16(res + mix) (plain fp32
+// add), out = bf16((h * rsqrt(mean(h^2) + eps)) * w1), w1 = 1 + weight in fp32.
+// Embedding variant (slot_engine_v8.py:205,209-210): h = embedding row of the token id.
+// ---------------------------------------------------------------------------------------------------
+constexpr int HID_PER_LANE = 16;
+
+template <bool EMBED, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* hidden, const uint16_t* mix, const int64_t* ids,
+                                                      const uint16_t* emb, const float* w1, float eps,
+                                                      uint16_t* normed, int tokens, int width, int64_t vocab) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= tokens) return;
+  const int per_lane = width / 64;  // 16 for width 1024
+  const int d0 = lane * per_lane;
+  float h[HID_PER_LANE];
+  const int64_t row = (int64_t)tok * width;
+  if constexpr (EMBED) {
+    int64_t id = ids[tok];
+    if (id < 0 || id >= vocab) id = 0;  // out-of-vocab ids are rejected on the host; never read OOB
+    const uint16_t* src = emb + id * width + d0;
+    for (int i = 0; i < per_lane; i += 8) load8_bf16(src + i, h + i);
+    for (int i = 0; i < per_lane; i += 4) {
+      *reinterpret_cast<uint2*>(hidden + row + d0 + i) = *reinterpret_cast<const uint2*>(src + i);
+    }
+  } else {
+    for (int i = 0; i < per_lane; i += 8) load8_bf16(hidden + row + d0 + i, h + i);
+    if constexpr (ADD) {
+      float m[HID_PER_LANE];
+      for (int i = 0; i < per_lane; i += 8) load8_bf16(mix + row + d0 + i, m + i);
+      for (int i = 0; i < per_lane; ++i) h[i] = rbf(__fadd_rn(h[i], m[i]));
+      for (int i = 0; i < per_lane; i += 4) store4_bf16(hidden + row + d0 + i, h + i);
+    }
+  }
+  float ss = 0.f;
+  for (int i = 0; i < per_lane; ++i) ss += h[i] * h[i];
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)width + eps);
+  float y[HID_PER_LANE];
+  for (int i = 0; i < per_lane; ++i) y[i] = (h[i] * r) * w1[d0 + i];
+  for (int i = 0; i < per_lane; i += 4) store4_bf16(normed + row + d0 + i, y + i);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Causal depthwise conv (KS = 4) + SiLU with the conv-history pool update.
+// _conv_silu_kernel (src/hs_guard/engine/fused_kernels.py:94-136): acc = sum_k w[c,k] * ext[t+k] in fp32,
+// out = bf16(silu(bf16(acc))); when len > 0, pool[slot, i] = ext[len + i] for i < KS-1, where
+// ext = [pool rows ; new tokens]. One thread per channel; the 3-row window slides in registers.
+// ---------------------------------------------------------------------------------------------------
+constexpr int KS = 4;
+
+__global__ __launch_bounds__(256) void conv_silu_kernel(const uint16_t* qkv, int64_t qkv_stride, uint16_t* pool,
+                                                        int64_t pool_rows, const uint16_t* weight,
+                                                        const int64_t* slots, const int64_t* lens,
+                                                        const int64_t* offsets, int L, int C, uint16_t* out,
+                                                        int64_t out_stride) {
+  const int n = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int64_t slot = slots[n];
+  int64_t len = lens[n];
+  const bool padded = offsets == nullptr;
+  const bool slot_ok = slot >= 0 && slot < pool_rows;
+  if (!slot_ok || len < 0) len = 0;
+  if (padded && len > L) len = L;
+  const int steps = padded ? L : (int)len;
+  if (!padded && len == 0) return;
+  const int64_t tok0 = padded ? (int64_t)n * L : offsets[n];
+  float w[KS];
+  for (int k = 0; k < KS; ++k) w[k] = bf2f(weight[c * KS + k]);
+  uint16_t e[KS - 1], keep[KS - 1];
+  for (int i = 0; i < KS - 1; ++i) {
+    e[i] = slot_ok ? pool[(slot * (KS - 1) + i) * (int64_t)C + c] : (uint16_t)0;
+    keep[i] = e[i];
+  }
+  for (int t = 0; t < steps; ++t) {
+    const int64_t tok = tok0 + t;
+    const uint16_t x = qkv[tok * qkv_stride + c];
+    float acc = 0.f;
+    acc = fmaf(w[0], bf2f(e[0]), acc);
+    acc = fmaf(w[1], bf2f(e[1]), acc);
+    acc = fmaf(w[2], bf2f(e[2]), acc);
+    acc = fmaf(w[3], bf2f(x), acc);
+    out[tok * out_stride + c] = f2bf(siluf_(rbf(acc)));
+    e[0] = e[1];
+    e[1] = e[2];
+    e[2] = x;
+    if (t == len - 1) {  // window after the last real token = ext[len .. len+2]
+      keep[0] = e[0];
+      keep[1] = e[1];
+      keep[2] = e[2];
+    }
+  }
+  if (len > 0) {
+    for (int i = 0; i < KS - 1; ++i) pool[(slot * (KS - 1) + i) * (int64_t)C + c] = keep[i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Per-head RMSNorm(1+w) + partial rotate-half RoPE for q and k in one launch, one wave per (token, head).
+// square_rows + norm_rope (src/hs_guard/engine/fused_kernels.py:237-284) with the rotary cos/sin of the
+// Qwen3.5 rotary embedding computed in-kernel: freq = pos * inv_freq[i] (fp32), cos/sin rounded to bf16.
+// y = bf16(x * rsqrt(mean(x^2)+eps) * w1); for d < rot: out = bf16(bf16(y*cos) + bf16(rot_half(y)*sin)).
+// ---------------------------------------------------------------------------------------------------
+struct RopeTensor {
+  const uint16_t* src; int64_t src_row, src_head; int heads;
+  const float* w1;
+  uint16_t* out; int64_t out_row, out_head;
+};
+
+__global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor b, const int64_t* pos,
+                                                        const float* inv_freq, int rot, float eps_a, float eps_b,
+                                                        int tokens, int D) {
+  const int lane = threadIdx.x & 63;
+  const int heads_total = a.heads + b.heads;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= tokens * heads_total) return;
+  const int tok = item / heads_total;
+  int head = item - tok * heads_total;
+  const bool is_a = head < a.heads;
+  const RopeTensor& t = is_a ? a : b;
+  if (!is_a) head -= a.heads;
+  const float eps = is_a ? eps_a : eps_b;
+  const int per_lane = D / 64;  // 4 for D = 256
+  const int d0 = lane * per_lane;
+  float x[4];
+  load4_bf16(t.src + tok * t.src_row + head * t.src_head + d0, x);
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)D + eps);
+  float y[4];
+  for (int i = 0; i < 4; ++i) y[i] = rbf((x[i] * r) * t.w1[d0 + i]);
+  const int half = rot / 2;
+  // the partner of dim d (d +- half) sits in lane ^ (half / 4) at the same slot
+  float yp[4];
+  const int pmask = half / 4;
+  for (int i = 0; i < 4; ++i) yp[i] = __shfl_xor(y[i], pmask, 64);
+  float o[4];
+  const float p = (float)pos[tok];
+  for (int i = 0; i < 4; ++i) {
+    const int d = d0 + i;
+    if (d < rot) {
+      const float f = p * inv_freq[d < half ? d : d - half];
+      const float cs = rbf(cosf(f));
+      const float sn = rbf(sinf(f));
+      const float rh = d < half ? -yp[i] : yp[i];
+      o[i] = __fadd_rn(rbf(y[i] * cs), rbf(rh * sn));
+    } else {
+      o[i] = y[i];
+    }
+  }
+  store4_bf16(t.out + tok * t.out_row + head * t.out_head + d0, o);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// SiLU-mul (src/hs_guard/engine/fused_kernels.py:76-90): out = bf16(bf16(silu(gate)) * up); gate and up
+// are the two halves of the fused gate|up projection row.
+// ---------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64_t gu_stride, int width,
+                                                       uint16_t* out, int tokens) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int tok = (int)(idx / width);
+  const int c = (int)(idx - (int64_t)tok * width);
+  if (tok >= tokens) return;
+  float g[4], u[4], y[4];
+  load4_bf16(gu + tok * gu_stride + c, g);
+  load4_bf16(gu + tok * gu_stride + width + c, u);
+  for (int i = 0; i < 4; ++i) y[i] = rbf(siluf_(g[i])) * u[i];
+  store4_bf16(out + (int64_t)tok * width + c, y);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Risk heads (src/hs_guard/runtime.py:61-74, src/hs_guard/engine/slot_engine_v7.py:58-61,
+// slot_engine_v8.py:223): given y = bf16(Linear_1024->512(x) + b1) for each role (columns
+// [role*512, role*512+512) of the fused projection), LayerNorm(512) in fp32, SiLU, round to bf16, Linear
+// 512->3 with bf16 output, softmax in fp32. One wave per (token, role).
+// ---------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void risk_head_kernel(const uint16_t* y, int64_t y_stride, const uint16_t* ln_w,
+                                                        const uint16_t* ln_b, const uint16_t* w2,
+                                                        const uint16_t* b2, float eps, int roles, int width,
+                                                        float* probs, int tokens) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= tokens * roles) return;
+  const int role = item / tokens;
+  const int tok = item - role * tokens;
+  const int per_lane = width / 64;  // 8 for width 512
+  const int d0 = lane * per_lane;
+  float v[8];
+  load8_bf16(y + tok * y_stride + role * width + d0, v);
+  float s = 0.f;
+  for (int i = 0; i < per_lane; ++i) s += v[i];
+  const float mean = wave_sum(s) / (float)width;
+  float s2 = 0.f;
+  for (int i = 0; i < per_lane; ++i) s2 += (v[i] - mean) * (v[i] - mean);
+  const float rstd = rsqrtf(wave_sum(s2) / (float)width + eps);
+  float lw[8], lb[8];
+  load8_bf16(ln_w + role * width + d0, lw);
+  load8_bf16(ln_b + role * width + d0, lb);
+  float a[8];
+  for (int i = 0; i < per_lane; ++i) a[i] = rbf(siluf_((v[i] - mean) * rstd * lw[i] + lb[i]));
+  float logit[3];
+  for (int j = 0; j < 3; ++j) {
+    float w[8];
+    load8_bf16(w2 + ((int64_t)role * 3 + j) * width + d0, w);
+    float acc = 0.f;
+    for (int i = 0; i < per_lane; ++i) acc += a[i] * w[i];
+    logit[j] = rbf(wave_sum(acc) + bf2f(b2[role * 3 + j]));
+  }
+  if (lane == 0) {
+    const float m = fmaxf(logit[0], fmaxf(logit[1], logit[2]));
+    const float e0 = expf(logit[0] - m), e1 = expf(logit[1] - m), e2 = expf(logit[2] - m);
+    const float z = e0 + e1 + e2;
+    float* dst = probs + ((int64_t)role * tokens + tok) * 3;
+    dst[0] = e0 / z;
+    dst[1] = e1 / z;
+    dst[2] = e2 / z;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// ring_pos[slot, (start + j) % W] = start + j for the valid steps of every row
+// (src/hs_guard/engine/slot_engine_v8.py:208,224; column W stays -1).
+// ---------------------------------------------------------------------------------------------------
+__global__ void ring_pos_kernel(int64_t* ring_pos, int64_t ring_rows, const int64_t* slots, const int64_t* starts,
+                                const int64_t* lens, int W, int lb_max) {
+  const int n = blockIdx.x;
+  const int64_t slot = slots[n];
+  int64_t len = lens[n];
+  if (slot < 0 || slot >= ring_rows || len <= 0) return;
+  if (len > lb_max) len = lb_max;
+  const int64_t start = starts[n];
+  for (int j = threadIdx.x; j < len; j += blockDim.x) {
+    const int64_t p = start + j;
+    ring_pos[slot * (W + 1) + p % W] = p;
+  }
+}
+
+}  // namespace
+}  // namespace hsg
+
+using namespace hsg;
+
+extern "C" int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vocab, const float* w1, float eps,
+                                 void* hidden, void* normed, int32_t tokens, int32_t width, void* stream) {
+  if (tokens < 0 || width != 1024 || vocab <= 0) return tokens < 0 || vocab <= 0 ? HSG_ERR_ARG : HSG_ERR_SHAPE;
+  if (tokens == 0) return HSG_OK;
+  if (!ids || !emb || !w1 || !hidden || !normed) return HSG_ERR_ARG;
+  if (!aligned(emb, 16) || !aligned(hidden, 16) || !aligned(normed, 16)) return HSG_ERR_ALIGN;
+  hipLaunchKernelGGL((rmsnorm_kernel<true, false>), dim3((tokens + 3) / 4), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<uint16_t*>(hidden), nullptr, ids,
+                     static_cast<const uint16_t*>(emb), w1, eps, static_cast<uint16_t*>(normed), tokens, width, vocab);
+  return launch_status();
+}
+
+extern "C" int hsg_add_rmsnorm(void* hidden, const void* mix, const float* w1, float eps, void* normed,
+                               int32_t tokens, int32_t width, void* stream) {
+  if (tokens < 0) return HSG_ERR_ARG;
+  if (width != 1024) return HSG_ERR_SHAPE;
+  if (tokens == 0) return HSG_OK;
+  if (!hidden || !w1 || !normed) return HSG_ERR_ARG;
+  if (!aligned(hidden, 16) || (mix && !aligned(mix, 16)) || !aligned(normed, 16)) return HSG_ERR_ALIGN;
+  const dim3 grid((tokens + 3) / 4);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (mix)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, true>), grid, dim3(256), 0, s, static_cast<uint16_t*>(hidden),
+                       static_cast<const uint16_t*>(mix), nullptr, nullptr, w1, eps, static_cast<uint16_t*>(normed),
+                       tokens, width, (int64_t)0);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<false, false>), grid, dim3(256), 0, s, static_cast<uint16_t*>(hidden),
+                       nullptr, nullptr, nullptr, w1, eps, static_cast<uint16_t*>(normed), tokens, width, (int64_t)0);
+  return launch_status();
+}
+
+extern "C" int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* pool, int64_t pool_rows,
+                                    const void* weight, int32_t kernel_size, const int64_t* slots, const int64_t* lens,
+                                    const int64_t* offsets, int32_t n_rows, int32_t L, int32_t channels, void* out,
+                                    int64_t out_stride, void* stream) {
+  if (n_rows < 0 || channels <= 0 || pool_rows <= 0 || L < 0) return HSG_ERR_ARG;
+  if (kernel_size != KS) return HSG_ERR_SHAPE;
+  if (n_rows == 0) return HSG_OK;
+  if (!qkv || !pool || !weight || !slots || !lens || !out || (!offsets && L <= 0)) return HSG_ERR_ARG;
+  const dim3 grid((channels + 255) / 256, n_rows);
+  hipLaunchKernelGGL(conv_silu_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(qkv), qkv_stride, static_cast<uint16_t*>(pool), pool_rows,
+                     static_cast<const uint16_t*>(weight), slots, lens, offsets, L, channels,
+                     static_cast<uint16_t*>(out), out_stride);
+  return launch_status();
+}
+
+extern "C" int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_heads, const float* q_w1,
+                             float q_eps, void* q_out, int64_t q_out_row, int64_t q_out_head, const void* k_src,
+                             int64_t k_row, int64_t k_head, int32_t k_heads, const float* k_w1, float k_eps,
+                             void* k_out, int64_t k_out_row, int64_t k_out_head, const int64_t* pos,
+                             const float* inv_freq, int32_t rot, int32_t tokens, int32_t head_dim, void* stream) {
+  if (tokens < 0 || q_heads < 0 || k_heads < 0) return HSG_ERR_ARG;
+  if (head_dim != 256 || rot <= 0 || rot > head_dim || rot % 8 != 0 || ((rot / 8) & (rot / 8 - 1)) != 0)
+    return HSG_ERR_SHAPE;
+  if (tokens == 0 || q_heads + k_heads == 0) return HSG_OK;
+  if (!pos || !inv_freq || (q_heads && (!q_src || !q_w1 || !q_out)) || (k_heads && (!k_src || !k_w1 || !k_out)))
+    return HSG_ERR_ARG;
+  const int64_t strides[] = {q_row, q_head, q_out_row, q_out_head, k_row, k_head, k_out_row, k_out_head};
+  for (int64_t s : strides)
+    if (s % 4) return HSG_ERR_ALIGN;
+  RopeTensor a{static_cast<const uint16_t*>(q_src), q_row, q_head, q_heads, q_w1, static_cast<uint16_t*>(q_out),
+               q_out_row, q_out_head};
+  RopeTensor b{static_cast<const uint16_t*>(k_src), k_row, k_head, k_heads, k_w1, static_cast<uint16_t*>(k_out),
+               k_out_row, k_out_head};
+  const int items = tokens * (q_heads + k_heads);
+  hipLaunchKernelGGL(norm_rope_kernel, dim3((items + 3) / 4), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a,
+                     b, pos, inv_freq, rot, q_eps, k_eps, tokens, head_dim);
+  return launch_status();
+}
+
+extern "C" int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* out, int32_t tokens,
+                            void* stream) {
+  if (tokens < 0 || width <= 0) return HSG_ERR_ARG;
+  if (width % 4 || row_stride % 4) return HSG_ERR_ALIGN;
+  if (tokens == 0) return HSG_OK;
+  if (!gate_up || !out) return HSG_ERR_ARG;
+  const int64_t total = (int64_t)tokens * width / 4;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), row_stride, width,
+                     static_cast<uint16_t*>(out), tokens);
+  return launch_status();
+}
+
+extern "C" int hsg_risk_head(const void* y, int64_t y_stride, const void* ln_w, const void* ln_b, const void* w2,
+                             const void* b2, float eps, int32_t roles, int32_t width, float* probs, int32_t tokens,
+                             void* stream) {
+  if (tokens < 0 || roles <= 0) return HSG_ERR_ARG;
+  if (width != 512) return HSG_ERR_SHAPE;
+  if (tokens == 0) return HSG_OK;
+  if (!y || !ln_w || !ln_b || !w2 || !b2 || !probs) return HSG_ERR_ARG;
+  if (y_stride % 8 || !aligned(y, 16) || !aligned(ln_w, 16) || !aligned(ln_b, 16) || !aligned(w2, 16))
+    return HSG_ERR_ALIGN;
+  const int items = tokens * roles;
+  hipLaunchKernelGGL(risk_head_kernel, dim3((items + 3) / 4), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(y), y_stride, static_cast<const uint16_t*>(ln_w),
+                     static_cast<const uint16_t*>(ln_b), static_cast<const uint16_t*>(w2),
+                     static_cast<const uint16_t*>(b2), eps, roles, width, probs, tokens);
+  return launch_status();
+}
+
+extern "C" int hsg_ring_pos_update(int64_t* ring_pos, int64_t ring_rows, int32_t window, const int64_t* slots,
+                                   const int64_t* starts, const int64_t* lens, int32_t n_rows, int32_t lb_max,
+                                   void* stream) {
+  if (n_rows < 0 || window <= 0 || ring_rows <= 0 || lb_max <= 0) return HSG_ERR_ARG;
+  if (n_rows == 0) return HSG_OK;
+  if (!ring_pos || !slots || !starts || !lens) return HSG_ERR_ARG;
+  hipLaunchKernelGGL(ring_pos_kernel, dim3(n_rows), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), ring_pos,
+                     ring_rows, slots, starts, lens, window, lb_max);
+  return launch_status();
+}

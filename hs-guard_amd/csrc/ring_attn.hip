@@ -121,8 +121,8 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_kernel(const RingParams p) 
         kp = p.ring_k + ring_base + (int64_t)(c0 + vi) * D;
       } else if (vi < ncols) {
         const int j = wave + (vi - cw) * NW;
-        const int64_t kpos = start + j;
-        ok = kpos <= qpos;  // j < len by construction, kpos > qpos - W since j <= l < LB_MAX <= W
+        const int64_t kpos = start + j;  // j < len by construction
+        ok = kpos <= qpos && kpos > qpos - W;
         kp = p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh;
       }
       float s[4] = {0.f, 0.f, 0.f, 0.f};
@@ -270,6 +270,7 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
   if (!q || !ring_k || !ring_v || !new_k || !new_v || !ring_pos || !slots || !starts || !lens || !out)
     return HSG_ERR_ARG;
   if (head_dim != D || window <= 0 || window > W_MAX || window % (4 * NW) != 0 || lb > LB_MAX) return HSG_ERR_SHAPE;
+  if (write_ring && lb > window) return HSG_ERR_SHAPE;  // two steps of one tick would share a ring column
   const int64_t s16[] = {q_sn, q_sl, q_sh, q_sg};
   for (int64_t s : s16)
     if (s % 8) return HSG_ERR_ALIGN;

@@ -42,6 +42,16 @@ SIGNATURES = {
         _P, _P, _P, _P, _P,                  # ring_pos, slots, starts, lens, offsets
         _I32, _I32, _I32, _I32, _I32, _F, _I32,  # n_rows, lb, hkv, groups, head_dim, scale, write_ring
         _P, _I64, _I64, _I64, _I64, _P]),    # out, o_sn, o_sl, o_sh, o_sg, stream
+    "hsg_embed_rmsnorm": (ctypes.c_int, [_P, _P, _I64, _P, _F, _P, _P, _I32, _I32, _P]),
+    "hsg_add_rmsnorm": (ctypes.c_int, [_P, _P, _P, _F, _P, _I32, _I32, _P]),
+    "hsg_conv_silu_update": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _P,
+                                            _I64, _P]),
+    "hsg_norm_rope": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _F, _P, _I64, _I64,
+                                     _P, _I64, _I64, _I32, _P, _F, _P, _I64, _I64,
+                                     _P, _P, _I32, _I32, _I32, _P]),
+    "hsg_silu_mul": (ctypes.c_int, [_P, _I64, _I32, _P, _I32, _P]),
+    "hsg_risk_head": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
+    "hsg_ring_pos_update": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I32, _P]),
 }
 
 _lib = None

@@ -1,0 +1,422 @@
+"""MI355X slot-stream engine: per-slot state pools, packed ticks, one hipGraph per (rows, tokens) bucket.
+
+Host orchestration mirrors SlotStreamEngineV7/V8 (src/hs_guard/engine/slot_engine_v7.py:117-167,
+slot_engine_v8.py:197-256): a request list is cut into ticks of at most ``max_tick_tokens`` tokens per slot
+and at most the largest session bucket of rows; each tick is one H2D copy of a packed int64 buffer, one
+graph replay, one D2H copy of the per-token class probabilities of both roles and one stream sync.
+
+Differences by design (the device program is the MI355X one, not a translation):
+* Tokens are PACKED: row n owns tokens offsets[n] .. offsets[n] + lens[n] - 1 of the tick, so GEMMs and
+  per-token kernels run over the tick's real tokens rounded up to a token bucket instead of
+  rows x 64-token buckets.
+* Projections are fused per layer (GDN: qkv|z|b|a; attention: q|k|v; MLP: gate|up; both heads' first
+  Linear), each one hipBLASLt GEMM.
+* Every other op is a libhsg.so kernel: embed+RMSNorm, conv+SiLU+pool update, GDN step with the gated
+  RMSNorm fused, q/k RMSNorm+RoPE in one launch, ring attention with the gate and the in-place ring write
+  for any tick length, add+RMSNorm, SiLU-mul, both risk heads, ring_pos update.
+* GDN state is fp32 by default (``state_dtype='float16'`` gives the reference StreamingGuard's storage).
+"""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import torch
+
+from .._lib import check, lib
+from ..model import ROLES, GuardModel
+
+SESSION_BUCKETS = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 160, 192, 224, 256, 320, 352, 384, 448, 512)
+STATE_DTYPES = {"float32": torch.float32, "float16": torch.float16}
+_STATE_CODE = {torch.float32: 0, torch.float16: 1}
+
+
+def bucket(value, choices):
+    """Smallest choice >= value (src/hs_guard/engine/bucketed_engine.py:12-16)."""
+    for choice in choices:
+        if value <= choice:
+            return choice
+    raise ValueError(f"{value} exceeds the largest bucket {choices[-1]}")
+
+
+def token_buckets(max_tokens):
+    """Packed-token buckets: powers of two to 256, then steps of 256 to 4096, then steps of 2048."""
+    out = [1, 2, 4, 8, 16, 32, 64, 128, 256]
+    out += list(range(512, 4097, 256))
+    out += list(range(6144, max(max_tokens, 6144) + 2048, 2048))
+    out = sorted({b for b in out if b < max_tokens} | {max_tokens})
+    return tuple(out)
+
+
+def pack_ticks(chunks, slots, length, nb, tb, max_slots, out):
+    """Packed tick layout in one int64 buffer ``[ids tb | pos tb | offsets nb | lens nb | slots nb | starts nb]``.
+
+    Rows n >= len(chunks) are padding: offset = total tokens, len 0, the scratch slot ``max_slots``, start 0
+    (the packed counterpart of pack_inputs, src/hs_guard/engine/slot_engine_v7.py:7-25). Token positions
+    beyond the real tokens carry id 0 and position 0. Returns (lens [n], offsets [n])."""
+    n = len(chunks)
+    lens = np.fromiter(map(len, chunks), dtype=np.int64, count=n)
+    total = int(lens.sum())
+    ids = out[:tb]
+    pos = out[tb:2 * tb]
+    offs = out[2 * tb:2 * tb + nb]
+    lns = out[2 * tb + nb:2 * tb + 2 * nb]
+    sls = out[2 * tb + 2 * nb:2 * tb + 3 * nb]
+    sts = out[2 * tb + 3 * nb:2 * tb + 4 * nb]
+    ids[:total] = np.fromiter(itertools.chain.from_iterable(chunks), dtype=np.int64, count=total)
+    ids[total:] = 0
+    offsets = np.zeros(n, dtype=np.int64)
+    if n > 1:
+        np.cumsum(lens[:-1], out=offsets[1:])
+    starts = np.asarray(length, dtype=np.int64)[slots]
+    pos[:total] = np.repeat(starts - offsets, lens) + np.arange(total, dtype=np.int64)
+    pos[total:] = 0
+    offs[:n] = offsets
+    offs[n:] = total
+    lns[:n] = lens
+    lns[n:] = 0
+    sls[:n] = slots
+    sls[n:] = max_slots
+    sts[:n] = starts
+    sts[n:] = 0
+    return lens, offsets
+
+
+class SlotStreamEngine:
+    """Fixed per-slot state for ``max_slots`` live streams (row ``max_slots`` of every pool is the scratch
+    slot of padding rows)."""
+
+    def __init__(self, model: GuardModel, max_slots, state_dtype="float32", use_graphs=True, roles=ROLES,
+                 session_buckets=None, max_tick_tokens=64):
+        if not isinstance(max_slots, int) or max_slots < 1:
+            raise ValueError("max_slots must be a positive integer")
+        if state_dtype not in STATE_DTYPES:
+            raise ValueError("state_dtype must be float32 or float16")
+        if not 1 <= max_tick_tokens <= 64:
+            raise ValueError("max_tick_tokens must be in [1, 64]")
+        lib()  # fail loudly here if the HIP library is missing
+        cfg = model.config
+        self.model, self.cfg = model, cfg
+        self.max_slots, self.roles, self.use_graphs = max_slots, tuple(roles), use_graphs
+        self.window = cfg.window_tokens
+        # a tick never holds more steps than the window: its steps then own distinct ring columns
+        self.max_tick_tokens = min(max_tick_tokens, self.window)
+        if session_buckets is None:
+            session_buckets = tuple(x for x in SESSION_BUCKETS if x <= max_slots)
+            if not session_buckets or session_buckets[-1] != max_slots:
+                session_buckets += (max_slots,)
+        self.session_buckets = tuple(session_buckets)
+        self.max_rows = self.session_buckets[-1]
+        self.max_tokens = self.max_rows * self.max_tick_tokens
+        self.token_buckets = token_buckets(self.max_tokens)
+        types = list(cfg.layer_types)
+        self.kind = [(t, sum(1 for u in types[:i] if u == t)) for i, t in enumerate(types)]
+        n_gdn, n_att = types.count("linear_attention"), types.count("full_attention")
+        dev = model.device
+        self.device = dev
+        S = max_slots + 1
+        bf16 = torch.bfloat16
+        self.state_dtype = STATE_DTYPES[state_dtype]
+        # ---- per-slot pools (layouts of src/hs_guard/engine/bucketed_engine.py:37-45, slot_engine.py:14-17) ----
+        self.rec = torch.zeros(n_gdn, S, cfg.linear_num_value_heads, cfg.linear_key_head_dim,
+                               cfg.linear_value_head_dim, dtype=self.state_dtype, device=dev)
+        self.conv = torch.zeros(n_gdn, S, cfg.linear_conv_kernel_dim - 1, cfg.conv_dim, dtype=bf16, device=dev)
+        self.ring_k = torch.zeros(n_att, S, cfg.num_key_value_heads, self.window + 1, cfg.head_dim, dtype=bf16,
+                                  device=dev)
+        self.ring_v = torch.zeros_like(self.ring_k)
+        self.ring_pos = torch.full((S, self.window + 1), -1, dtype=torch.long, device=dev)
+        self.length = np.zeros(max_slots, dtype=np.int64)
+        self.stats = {"graph_replays": 0, "eager_steps": 0, "captures": 0}
+        self.graphs = {}
+        self.pool = None
+        self._prepare_weights()
+        self._allocate_buffers()
+
+    # ------------------------------------------------------------------------------------------------
+    def _prepare_weights(self):
+        m, cfg = self.model, self.cfg
+        f32 = torch.float32
+        self.layers = []
+        for i, (kind, _) in enumerate(self.kind):
+            p = f"backbone.layers.{i}."
+            L = {"in_w1": (1.0 + m[p + "input_layernorm.weight"].float()).contiguous(),
+                 "post_w1": (1.0 + m[p + "post_attention_layernorm.weight"].float()).contiguous(),
+                 "w_gu": torch.cat([m[p + "mlp.gate_proj.weight"], m[p + "mlp.up_proj.weight"]]).contiguous(),
+                 "w_down": m[p + "mlp.down_proj.weight"].contiguous()}
+            if kind == "linear_attention":
+                a = p + "linear_attn."
+                L["w_in"] = torch.cat([m[a + "in_proj_qkv.weight"], m[a + "in_proj_z.weight"],
+                                       m[a + "in_proj_b.weight"], m[a + "in_proj_a.weight"]]).contiguous()
+                L["conv_w"] = m[a + "conv1d.weight"].reshape(cfg.conv_dim, -1).contiguous()
+                L["A_log"] = m[a + "A_log"].contiguous()
+                L["dt_bias"] = m[a + "dt_bias"].contiguous()
+                L["norm_w"] = m[a + "norm.weight"].contiguous()
+                L["w_out"] = m[a + "out_proj.weight"].contiguous()
+            else:
+                a = p + "self_attn."
+                L["w_in"] = torch.cat([m[a + "q_proj.weight"], m[a + "k_proj.weight"],
+                                       m[a + "v_proj.weight"]]).contiguous()
+                L["q_w1"] = (1.0 + m[a + "q_norm.weight"].float()).contiguous()
+                L["k_w1"] = (1.0 + m[a + "k_norm.weight"].float()).contiguous()
+                L["w_out"] = m[a + "o_proj.weight"].contiguous()
+            self.layers.append(L)
+        self.final_w1 = (1.0 + m["backbone.norm.weight"].float()).contiguous()
+        self.emb = m["backbone.embed_tokens.weight"].contiguous()
+        rot = cfg.rotary_dim
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=f32) / rot))).to(self.device)
+        self.head_w1 = torch.cat([m[f"heads.{r}.projection.0.weight"] for r in self.roles]).contiguous()
+        self.head_b1 = torch.cat([m[f"heads.{r}.projection.0.bias"] for r in self.roles]).contiguous()
+        self.head_ln_w = torch.stack([m[f"heads.{r}.projection.1.weight"] for r in self.roles]).contiguous()
+        self.head_ln_b = torch.stack([m[f"heads.{r}.projection.1.bias"] for r in self.roles]).contiguous()
+        self.head_w2 = torch.stack([m[f"heads.{r}.risk.weight"] for r in self.roles]).contiguous()
+        self.head_b2 = torch.stack([m[f"heads.{r}.risk.bias"] for r in self.roles]).contiguous()
+
+    def _allocate_buffers(self):
+        cfg, T, dev = self.cfg, self.max_tokens, self.device
+        bf16 = torch.bfloat16
+        hq, hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.gdn_in = cfg.conv_dim + cfg.value_dim + 2 * cfg.linear_num_value_heads
+        self.att_in = hq * 2 * D + 2 * hkv * D
+        widest = max(self.gdn_in, self.att_in, 2 * cfg.intermediate_size)
+        self.buf = {
+            "hidden": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
+            "normed": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
+            "mix": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
+            "proj": torch.zeros(T * widest, dtype=bf16, device=dev),
+            "conv": torch.zeros(T * cfg.conv_dim, dtype=bf16, device=dev),
+            "mid": torch.zeros(T * max(cfg.value_dim, hq * D, cfg.intermediate_size), dtype=bf16, device=dev),
+            "q": torch.zeros(T * hq * D, dtype=bf16, device=dev),
+            "k": torch.zeros(T * hkv * D, dtype=bf16, device=dev),
+            "head": torch.zeros(T * cfg.head_hidden * len(self.roles), dtype=bf16, device=dev),
+            "probs": torch.zeros(len(self.roles) * T * 3, dtype=torch.float32, device=dev),
+            "inputs": torch.zeros(2 * T + 4 * self.max_rows, dtype=torch.long, device=dev),
+        }
+
+    def _view(self, name, *shape):
+        n = 1
+        for s in shape:
+            n *= s
+        return self.buf[name][:n].view(*shape)
+
+    # ------------------------------------------------------------------------------------------------
+    def state_bytes_per_session(self):
+        tensors = (self.rec, self.conv, self.ring_k, self.ring_v, self.ring_pos)
+        return sum(t.element_size() * t.numel() for t in tensors) // (self.max_slots + 1)
+
+    def reset(self, slots=None):
+        """Zero the state of every slot (``slots=None``, the reference's reset,
+        src/hs_guard/engine/bucketed_engine.py:51-55) or of the given slots only."""
+        if slots is None:
+            for t in (self.rec, self.conv, self.ring_k, self.ring_v):
+                t.zero_()
+            self.ring_pos.fill_(-1)
+            self.length = np.zeros(self.max_slots, dtype=np.int64)
+            return
+        idx = torch.as_tensor(list(slots), dtype=torch.long, device=self.device)
+        self.rec[:, idx] = 0
+        self.conv[:, idx] = 0
+        self.ring_k[:, idx] = 0
+        self.ring_v[:, idx] = 0
+        self.ring_pos[idx] = -1
+        self.length[idx.cpu().numpy()] = 0
+
+    def snapshot(self, slot):
+        """Copy of one slot's state (the pool rows examples/demo/runtime_v10.py:117-122 clones)."""
+        return {"rec": self.rec[:, slot].clone(), "conv": self.conv[:, slot].clone(),
+                "ring_k": self.ring_k[:, slot].clone(), "ring_v": self.ring_v[:, slot].clone(),
+                "ring_pos": self.ring_pos[slot].clone(), "length": int(self.length[slot])}
+
+    def restore(self, slot, snap):
+        """Write a snapshot back into a slot (examples/demo/runtime_v10.py:98-111)."""
+        self.rec[:, slot] = snap["rec"]
+        self.conv[:, slot] = snap["conv"]
+        self.ring_k[:, slot] = snap["ring_k"]
+        self.ring_v[:, slot] = snap["ring_v"]
+        self.ring_pos[slot] = snap["ring_pos"]
+        self.length[slot] = snap["length"]
+
+    # ------------------------------------------------------------------------------------------------
+    def _inputs(self, nb, tb):
+        x = self.buf["inputs"]
+        return {"ids": x[:tb], "pos": x[tb:2 * tb], "offsets": x[2 * tb:2 * tb + nb],
+                "lens": x[2 * tb + nb:2 * tb + 2 * nb], "slots": x[2 * tb + 2 * nb:2 * tb + 3 * nb],
+                "starts": x[2 * tb + 3 * nb:2 * tb + 4 * nb], "all": x[:2 * tb + 4 * nb]}
+
+    def _forward(self, nb, tb, inp):
+        """The tick's device program (src/hs_guard/engine/slot_engine_v8.py:197-225), launched on the current
+        stream. Reads only device memory, so it can be captured into a hipGraph."""
+        L = lib()
+        cfg = self.cfg
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        H, W = cfg.hidden_size, self.window
+        S = self.max_slots + 1
+        eps = cfg.rms_norm_eps
+        hq, hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        G = hq // hkv
+        nh, hv, kd, vd = cfg.linear_num_key_heads, cfg.linear_num_value_heads, cfg.linear_key_head_dim, \
+            cfg.linear_value_head_dim
+        ids, pos, offsets, lens, slots, starts = (inp[k] for k in ("ids", "pos", "offsets", "lens", "slots",
+                                                                    "starts"))
+        hidden = self._view("hidden", tb, H)
+        normed = self._view("normed", tb, H)
+        mix = self._view("mix", tb, H)
+        check(L.hsg_embed_rmsnorm(ids.data_ptr(), self.emb.data_ptr(), cfg.vocab_size,
+                                  self.layers[0]["in_w1"].data_ptr(), eps, hidden.data_ptr(), normed.data_ptr(), tb,
+                                  H, st), "hsg_embed_rmsnorm")
+        for i, ((kind, idx), Lw) in enumerate(zip(self.kind, self.layers)):
+            if kind == "linear_attention":
+                C = cfg.conv_dim
+                proj = self._view("proj", tb, self.gdn_in)
+                torch.mm(normed, Lw["w_in"].t(), out=proj)
+                conv = self._view("conv", tb, C)
+                check(L.hsg_conv_silu_update(proj.data_ptr(), self.gdn_in, self.conv[idx].data_ptr(), S,
+                                             Lw["conv_w"].data_ptr(), cfg.linear_conv_kernel_dim, slots.data_ptr(),
+                                             lens.data_ptr(), offsets.data_ptr(), nb, 0, C, conv.data_ptr(), C, st),
+                      "hsg_conv_silu_update")
+                out = self._view("mid", tb, cfg.value_dim)
+                base = proj.data_ptr()
+                check(L.hsg_gdn_slot_step_gated(
+                    conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
+                    base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), self.gdn_in,
+                    Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), self.rec[idx].data_ptr(),
+                    _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb, 0,
+                    nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in, Lw["norm_w"].data_ptr(), eps,
+                    out.data_ptr(), st), "hsg_gdn_slot_step_gated")
+                torch.mm(out, Lw["w_out"].t(), out=mix)
+            else:
+                proj = self._view("proj", tb, self.att_in)
+                torch.mm(normed, Lw["w_in"].t(), out=proj)
+                q = self._view("q", tb, hq * D)
+                k = self._view("k", tb, hkv * D)
+                base = proj.data_ptr()
+                check(L.hsg_norm_rope(base, self.att_in, 2 * D, hq, Lw["q_w1"].data_ptr(), eps, q.data_ptr(), hq * D,
+                                      D, base + 2 * hq * 2 * D, self.att_in, D, hkv, Lw["k_w1"].data_ptr(), eps,
+                                      k.data_ptr(), hkv * D, D, pos.data_ptr(), self.inv_freq.data_ptr(),
+                                      cfg.rotary_dim, tb, D, st), "hsg_norm_rope")
+                att = self._view("mid", tb, hq * D)
+                check(L.hsg_ring_attention(
+                    q.data_ptr(), 0, hq * D, G * D, D,
+                    self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
+                    k.data_ptr(), 0, hkv * D, D,
+                    base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
+                    base, 0, self.att_in, G * 2 * D, 2 * D, D,
+                    self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
+                    nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1,
+                    att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
+                torch.mm(att, Lw["w_out"].t(), out=mix)
+            check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), Lw["post_w1"].data_ptr(), eps,
+                                    normed.data_ptr(), tb, H, st), "hsg_add_rmsnorm")
+            I = cfg.intermediate_size
+            gu = self._view("proj", tb, 2 * I)
+            torch.mm(normed, Lw["w_gu"].t(), out=gu)
+            act = self._view("mid", tb, I)
+            check(L.hsg_silu_mul(gu.data_ptr(), 2 * I, I, act.data_ptr(), tb, st), "hsg_silu_mul")
+            torch.mm(act, Lw["w_down"].t(), out=mix)
+            nxt = self.layers[i + 1]["in_w1"] if i + 1 < len(self.layers) else self.final_w1
+            check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), nxt.data_ptr(), eps, normed.data_ptr(), tb, H,
+                                    st), "hsg_add_rmsnorm")
+        R, E = len(self.roles), cfg.head_hidden
+        y = self._view("head", tb, R * E)
+        torch.addmm(self.head_b1, normed, self.head_w1.t(), out=y)
+        probs = self._view("probs", R, tb, 3)
+        check(L.hsg_risk_head(y.data_ptr(), R * E, self.head_ln_w.data_ptr(), self.head_ln_b.data_ptr(),
+                              self.head_w2.data_ptr(), self.head_b2.data_ptr(), cfg.layer_norm_eps, R, E,
+                              probs.data_ptr(), tb, st), "hsg_risk_head")
+        check(L.hsg_ring_pos_update(self.ring_pos.data_ptr(), S, W, slots.data_ptr(), starts.data_ptr(),
+                                    lens.data_ptr(), nb, self.max_tick_tokens, st), "hsg_ring_pos_update")
+        return probs
+
+    def _static(self, nb, tb):
+        key = (nb, tb)
+        if key not in self.graphs:
+            inp = self._inputs(nb, tb)
+            inp["all"].zero_()
+            inp["slots"].fill_(self.max_slots)       # empty rows on the scratch slot: no state is touched
+            graph = None
+            if self.use_graphs:
+                side = torch.cuda.Stream(self.device)
+                side.wait_stream(torch.cuda.current_stream(self.device))
+                with torch.cuda.stream(side):
+                    for _ in range(2):
+                        self._forward(nb, tb, inp)
+                torch.cuda.current_stream(self.device).wait_stream(side)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=self.pool):
+                    probs = self._forward(nb, tb, inp)
+                self.pool = graph.pool()
+                self.stats["captures"] += 1
+            else:
+                probs = self._view("probs", len(self.roles), tb, 3)
+            host_in = torch.zeros(2 * tb + 4 * nb, dtype=torch.long, pin_memory=True)
+            host_out = torch.zeros(len(self.roles), tb, 3, dtype=torch.float32, pin_memory=True)
+            self.graphs[key] = (graph, inp, probs, host_in, host_in.numpy(), host_out, host_out.numpy())
+        return self.graphs[key]
+
+    def _run_arrays(self, chunks, slots):
+        """One tick: <= max_rows rows of <= max_tick_tokens tokens. Returns (probs [R, T, 3] numpy, lens,
+        offsets) with row r's probabilities at [:, offsets[r] : offsets[r] + lens[r]]."""
+        n = len(chunks)
+        total = sum(len(c) for c in chunks)
+        nb = bucket(n, self.session_buckets)
+        tb = bucket(total, self.token_buckets)
+        graph, inp, probs, host_in, host_np, host_out, out_np = self._static(nb, tb)
+        lens, offsets = pack_ticks(chunks, slots, self.length, nb, tb, self.max_slots, host_np)
+        inp["all"].copy_(host_in, non_blocking=True)
+        if graph is not None:
+            graph.replay()
+            self.stats["graph_replays"] += 1
+        else:
+            probs = self._forward(nb, tb, inp)
+            self.stats["eager_steps"] += 1
+        host_out.copy_(probs, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        self.length[slots] += lens
+        return out_np[:, :total].copy(), lens, offsets
+
+    def _validate(self, requests):
+        slots = [s for s, _ in requests]
+        if len(set(slots)) != len(slots):
+            raise ValueError("a session may appear once per tick")
+        for s, ids in requests:
+            if not 0 <= s < self.max_slots:
+                raise ValueError("Slot is outside the allocated range")
+            if len(ids) == 0:
+                raise ValueError("Each request requires nonempty token IDs")
+
+    @torch.inference_mode()
+    def step_packed(self, requests):
+        """One tick without per-row objects (src/hs_guard/engine/slot_engine_v7.py:138-145): requests as
+        step(), each <= max_tick_tokens tokens and at most the largest session bucket of them. Returns
+        (probs [R, n, lb, 3] numpy, lens [n]); row r holds request r's first lens[r] positions."""
+        self._validate(requests)
+        if len(requests) > self.max_rows or any(len(c) > self.max_tick_tokens for _, c in requests):
+            raise ValueError("step_packed takes one tick: too many rows or tokens")
+        slots = np.fromiter((s for s, _ in requests), dtype=np.int64, count=len(requests))
+        flat, lens, offsets = self._run_arrays([list(c) for _, c in requests], slots)
+        lb = bucket(int(lens.max()), (1, 2, 4, 8, 16, 32, 64))
+        out = np.zeros((flat.shape[0], len(requests), lb, 3), dtype=np.float32)
+        for r, (o, ln) in enumerate(zip(offsets, lens)):
+            out[:, r, :ln] = flat[:, o:o + ln]
+        return out, lens
+
+    @torch.inference_mode()
+    def step(self, requests):
+        """requests: list of (slot, token_ids), each slot at most once. Returns {role: [CPU tensor [L_i, 3]]}
+        (src/hs_guard/engine/slot_engine_v7.py:147-167)."""
+        self._validate(requests)
+        largest, rows = self.max_tick_tokens, self.max_rows
+        results = {role: [[] for _ in requests] for role in self.roles}
+        pending = [(i, s, list(ids)) for i, (s, ids) in enumerate(requests)]
+        while pending:
+            batch = [(i, s, ids[:largest]) for i, s, ids in pending]
+            for start in range(0, len(batch), rows):
+                part = batch[start:start + rows]
+                slots = np.fromiter((s for _, s, _ in part), dtype=np.int64, count=len(part))
+                flat, lens, offsets = self._run_arrays([c for _, _, c in part], slots)
+                probs = torch.from_numpy(flat)
+                for role_index, role in enumerate(self.roles):
+                    for row, (i, _, _) in enumerate(part):
+                        results[role][i].append(probs[role_index, offsets[row]:offsets[row] + lens[row]])
+            pending = [(i, s, ids[largest:]) for i, s, ids in pending if len(ids) > largest]
+        return {role: [chunks[0] if len(chunks) == 1 else torch.cat(chunks) for chunks in rows_]
+                for role, rows_ in results.items()}

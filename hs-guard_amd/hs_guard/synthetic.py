@@ -89,3 +89,38 @@ def ring_decode_inputs(rows=64, hq=16, hkv=4, head_dim=256, window=512, seed=0, 
         "starts": starts.long(), "lens": torch.ones(rows, dtype=torch.long), "fill": fill, "ptr": ptr,
         "window": W, "hq": hq, "hkv": hkv, "head_dim": D,
     }
+
+
+class MixedServingLoad:
+    """Config 5: ``slots`` concurrent streams. Initial contexts uniform over ``contexts`` tokens; each step
+    every slot appends c tokens with c = 1 (p 0.8), U{2..16} (p 0.15), U{17..64} (p 0.05); after a step
+    each slot is reset with probability ``reset_p`` and gets a fresh context. Token ids uniform in
+    [0, vocab). One numpy Generator seeded ``seed`` drives every draw, in call order."""
+
+    def __init__(self, slots=352, vocab=151936, contexts=(512, 2048, 8000), reset_p=0.01, seed=0):
+        import numpy as np
+        self.np = np
+        self.rng = np.random.default_rng(seed)
+        self.slots, self.vocab, self.contexts, self.reset_p = slots, vocab, tuple(contexts), reset_p
+
+    def context(self):
+        n = int(self.rng.choice(self.contexts))
+        return self.rng.integers(0, self.vocab, n).tolist()
+
+    def chunk_sizes(self):
+        u = self.rng.random(self.slots)
+        small = self.rng.integers(2, 17, self.slots)
+        large = self.rng.integers(17, 65, self.slots)
+        return self.np.where(u < 0.8, 1, self.np.where(u < 0.95, small, large))
+
+    def step_requests(self):
+        sizes = self.chunk_sizes()
+        ids = self.rng.integers(0, self.vocab, int(sizes.sum()))
+        out, at = [], 0
+        for s, c in enumerate(sizes.tolist()):
+            out.append((s, ids[at:at + c].tolist()))
+            at += c
+        return out
+
+    def resets(self):
+        return self.np.nonzero(self.rng.random(self.slots) < self.reset_p)[0].tolist()

@@ -90,7 +90,8 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * kpos > qpos - window. Output = softmax-weighted values, rounded to bf16, times bf16(sigmoid(gate)).
  * write_ring != 0: after every read, new key/value of each valid step j go to ring column
  * (start+j) % window. ring_pos itself is not written (see hsg_ring_pos_update).
- * Supported: head_dim == 256, window <= 512 and a multiple of 16, lb <= 64.
+ * Supported: head_dim == 256, window <= 512 and a multiple of 16, lb <= 64 (rows with lens[n] > 64 are
+ * treated as empty); write_ring needs lb <= window so that the steps of one tick own distinct columns.
  */
 int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,
                        void* ring_k, void* ring_v, int64_t ring_rows, int32_t window, const void* new_k,
@@ -101,6 +102,79 @@ int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, 
                        const int64_t* offsets, int32_t n_rows, int32_t lb, int32_t hkv, int32_t groups,
                        int32_t head_dim, float scale, int32_t write_ring, void* out, int64_t o_sn,
                        int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream);
+
+/*
+ * Embedding gather + RMSNorm of the first layer. Replaces embed_tokens + add_square(hidden) + rms_finish
+ * (src/hs_guard/engine/slot_engine_v8.py:205,209-210; fused_kernels.py:30-72):
+ *   hidden[t] = emb[ids[t]];  normed[t] = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1)
+ *   emb [vocab, width] bf16, w1 [width] fp32 (= 1 + weight), hidden/normed [tokens, width] bf16.
+ * Supported: width == 1024. Ids outside [0, vocab) read row 0 (the host rejects them first).
+ */
+int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vocab, const float* w1, float eps,
+                      void* hidden, void* normed, int32_t tokens, int32_t width, void* stream);
+
+/*
+ * Residual add + RMSNorm. Replaces add_square + sq.mean + rms_finish
+ * (src/hs_guard/engine/fused_kernels.py:30-72; slot_engine_v8.py:216-222):
+ *   hidden = bf16(hidden + mix) (in place; mix may be NULL: no add);
+ *   normed = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1). Supported: width == 1024.
+ */
+int hsg_add_rmsnorm(void* hidden, const void* mix, const float* w1, float eps, void* normed, int32_t tokens,
+                    int32_t width, void* stream);
+
+/*
+ * Causal depthwise conv + SiLU with the per-slot conv-history update. Replaces conv_silu_update
+ * (src/hs_guard/engine/fused_kernels.py:126-136; kernel :94-123):
+ *   qkv [tokens, qkv_stride] bf16 (first `channels` columns), pool [pool_rows, kernel_size-1, channels]
+ *   bf16 (updated in place at slots[n] when lens[n] > 0), weight [channels, kernel_size] bf16,
+ *   out [tokens, out_stride] bf16. Padded layout computes all L positions of every row like the reference.
+ * Supported: kernel_size == 4.
+ */
+int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* pool, int64_t pool_rows, const void* weight,
+                         int32_t kernel_size, const int64_t* slots, const int64_t* lens, const int64_t* offsets,
+                         int32_t n_rows, int32_t L, int32_t channels, void* out, int64_t out_stride,
+                         void* stream);
+
+/*
+ * Per-head RMSNorm(1+w) + partial rotate-half RoPE of q and k in one launch. Replaces square_rows +
+ * mean + norm_rope x2 (src/hs_guard/engine/fused_kernels.py:237-284; slot_engine_v8.py:246-249) and the
+ * rotary cos/sin of the backbone (slot_engine_v8.py:206): cos/sin = bf16(cos/sin(pos[t] * inv_freq[i])).
+ *   x[t, h, :] at src + t*row + h*head;  out[t, h, :] at out + t*out_row + h*out_head (bf16).
+ *   w1 [head_dim] fp32 per tensor; inv_freq [rot/2] fp32; pos [tokens] int64.
+ * Supported: head_dim == 256, rot a power of two in [8, 256].
+ */
+int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_heads, const float* q_w1,
+                  float q_eps, void* q_out, int64_t q_out_row, int64_t q_out_head, const void* k_src,
+                  int64_t k_row, int64_t k_head, int32_t k_heads, const float* k_w1, float k_eps, void* k_out,
+                  int64_t k_out_row, int64_t k_out_head, const int64_t* pos, const float* inv_freq, int32_t rot,
+                  int32_t tokens, int32_t head_dim, void* stream);
+
+/*
+ * SiLU-mul of the fused gate|up projection. Replaces silu_mul (src/hs_guard/engine/fused_kernels.py:86-90):
+ *   out[t, c] = bf16(bf16(silu(gu[t, c])) * gu[t, width + c]), out [tokens, width] bf16.
+ */
+int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* out, int32_t tokens,
+                 void* stream);
+
+/*
+ * Risk heads after the fused first projection. Replaces _risk + softmax
+ * (src/hs_guard/engine/slot_engine_v7.py:58-61; slot_engine_v8.py:223; src/hs_guard/runtime.py:61-74):
+ *   for role r: v = y[t, r*width : (r+1)*width] (bf16 Linear output incl. bias), LayerNorm(eps) in fp32
+ *   with ln_w/ln_b [roles, width], SiLU, bf16, Linear to 3 with w2 [roles, 3, width], b2 [roles, 3],
+ *   bf16 logits, softmax -> probs [roles, tokens, 3] fp32. Supported: width == 512.
+ */
+int hsg_risk_head(const void* y, int64_t y_stride, const void* ln_w, const void* ln_b, const void* w2,
+                  const void* b2, float eps, int32_t roles, int32_t width, float* probs, int32_t tokens,
+                  void* stream);
+
+/*
+ * Ring position bookkeeping after all layers. Replaces ring_pos[slots, ring_col] = where(valid, pos, -1)
+ * (src/hs_guard/engine/slot_engine_v8.py:208,224): ring_pos[slot, (start + j) % window] = start + j for
+ * j < min(lens[n], lb_max); column `window` is never written (it stays -1).
+ */
+int hsg_ring_pos_update(int64_t* ring_pos, int64_t ring_rows, int32_t window, const int64_t* slots,
+                        const int64_t* starts, const int64_t* lens, int32_t n_rows, int32_t lb_max,
+                        void* stream);
 
 #ifdef __cplusplus
 }

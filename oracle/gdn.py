@@ -67,21 +67,19 @@ def gdn_slot_step(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_l
     S = st[slots[live]]                                     # [R, HV, K, V]
     g_all, beta_all = gates(np.asarray(a)[live], np.asarray(b)[live], A_log, dt_bias)
     for t in range(int(lens[live].max())):
-        on = lens[live] > t                                 # rows still running
-        q = packed[live, t, :key_dim].reshape(-1, H, K)[:, kh]
-        k = packed[live, t, key_dim:2 * key_dim].reshape(-1, H, K)[:, kh]
-        v = packed[live, t, 2 * key_dim:2 * key_dim + HV * V].reshape(-1, HV, V)
+        on = np.nonzero(lens[live] > t)[0]                  # rows still running (only they are computed)
+        rows = live[on]
+        q = packed[rows, t, :key_dim].reshape(-1, H, K)[:, kh]
+        k = packed[rows, t, key_dim:2 * key_dim].reshape(-1, H, K)[:, kh]
+        v = packed[rows, t, 2 * key_dim:2 * key_dim + HV * V].reshape(-1, HV, V)
         q = l2norm(q) * scale
         k = l2norm(k)
-        decay = np.exp(g_all[:, t])                          # [R, HV]
-        decay = np.where(on[:, None], decay, 1.0)
-        S_new = S * decay[:, :, None, None]
-        kv = np.einsum('rhkv,rhk->rhv', S_new, k)
-        vn = beta_all[:, t][:, :, None] * (v - kv)
-        S_new = S_new + k[:, :, :, None] * vn[:, :, None, :]
-        ot = np.einsum('rhkv,rhk->rhv', S_new, q)
-        S = np.where(on[:, None, None, None], S_new, S)
-        o[live[on], t] = ot[on]
+        Sr = S[on] * np.exp(g_all[on, t])[:, :, None, None]
+        kv = np.einsum('rhkv,rhk->rhv', Sr, k)
+        vn = beta_all[on, t][:, :, None] * (v - kv)
+        Sr += k[:, :, :, None] * vn[:, :, None, :]
+        o[rows, t] = np.einsum('rhkv,rhk->rhv', Sr, q)
+        S[on] = Sr
     st[slots[live]] = S
     return o, bf16(o).astype(np.float64) ** 2, st
 

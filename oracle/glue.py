@@ -26,10 +26,12 @@ from .bf16 import bf16, silu
 
 
 def linear_bf16(x, w, bias=None):
-    """bf16 GEMM under autocast: fp32 accumulate of bf16 operands, bias added, output rounded to bf16."""
-    y = np.asarray(x, dtype=np.float32) @ np.asarray(w, dtype=np.float32).T
+    """bf16 GEMM under autocast: fp32 accumulate of bf16 operands, bias added, output rounded to bf16
+    (float64 throughout inside ``oracle.bf16.exact()``)."""
+    dt = np.float32 if bf16(np.float32(1.5)).dtype == np.float32 else np.float64
+    y = np.asarray(x, dtype=dt) @ np.asarray(w, dtype=dt).T
     if bias is not None:
-        y = y + np.asarray(bias, dtype=np.float32)
+        y = y + np.asarray(bias, dtype=dt)
     return bf16(y)
 
 
@@ -119,7 +121,11 @@ def layer_norm(x, w, b, eps=1e-5):
 
 def risk_probs(hidden, w1, b1, ln_w, ln_b, w2, b2, eps=1e-5):
     """hidden [T, hidden] bf16 values -> softmax(risk logits) [T, 3] float64."""
-    y = linear_bf16(hidden, w1, b1)
+    return risk_probs_from_projection(linear_bf16(hidden, w1, b1), ln_w, ln_b, w2, b2, eps)
+
+
+def risk_probs_from_projection(y, ln_w, ln_b, w2, b2, eps=1e-5):
+    """The head after its first Linear: y [T, 512] bf16 values -> softmax(risk logits) [T, 3] float64."""
     y = silu(layer_norm(y, ln_w, ln_b, eps))
     logits = linear_bf16(bf16(y), w2, b2).astype(np.float64)
     logits = logits - logits.max(-1, keepdims=True)

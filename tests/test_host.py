@@ -1,0 +1,121 @@
+"""Host-side logic without a GPU: packed tick layout, buckets, StreamingGuard validation (fake engine)."""
+import numpy as np
+import pytest
+
+from oracle import pack as opack
+
+
+def test_pack_ticks_matches_padded_layout():
+    """The packed layout carries the same ids, lens, slots and starts as pack_inputs' padded layout (the
+    reference's contract, slot_engine_v7.py:7-25), and pos = start + step for every real token."""
+    from hs_guard.engine.slot_engine import pack_ticks
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        max_slots = 9
+        n = int(rng.integers(1, 7))
+        slots = rng.permutation(max_slots)[:n]
+        chunks = [rng.integers(0, 100, int(rng.integers(1, 9))).tolist() for _ in range(n)]
+        length = rng.integers(0, 1000, max_slots)
+        nb = n + int(rng.integers(0, 3))
+        total = sum(map(len, chunks))
+        tb = total + int(rng.integers(0, 5))
+        out = np.full(2 * tb + 4 * nb, -7, dtype=np.int64)
+        lens, offsets = pack_ticks(chunks, slots, length, nb, tb, max_slots, out)
+        lb = max(map(len, chunks))
+        ref = np.empty(nb * lb + 3 * nb, dtype=np.int64)
+        ref_lens = opack.pack_inputs(chunks, slots, nb, lb, length, max_slots, ref)
+        np.testing.assert_array_equal(lens, ref_lens)
+        ids, pos = out[:tb], out[tb:2 * tb]
+        offs, lns, sls, sts = (out[2 * tb + i * nb:2 * tb + (i + 1) * nb] for i in range(4))
+        np.testing.assert_array_equal(lns, ref[nb * lb:nb * lb + nb])
+        np.testing.assert_array_equal(sls, ref[nb * lb + nb:nb * lb + 2 * nb])
+        np.testing.assert_array_equal(sts, ref[nb * lb + 2 * nb:])
+        ref_ids = ref[:nb * lb].reshape(nb, lb)
+        for r in range(n):
+            np.testing.assert_array_equal(ids[offs[r]:offs[r] + lns[r]], ref_ids[r, :lns[r]])
+            np.testing.assert_array_equal(pos[offs[r]:offs[r] + lns[r]], sts[r] + np.arange(lns[r]))
+        assert (offs[n:] == total).all() and (ids[total:] == 0).all()
+
+
+def test_buckets():
+    from hs_guard.engine.slot_engine import bucket, token_buckets
+    tb = token_buckets(352 * 64)
+    assert tb[0] == 1 and tb[-1] == 352 * 64 and list(tb) == sorted(set(tb))
+    assert bucket(1470, tb) == 1536 and bucket(1, tb) == 1
+    with pytest.raises(ValueError):
+        bucket(352 * 64 + 1, tb)
+
+
+class _FakeEngine:
+    """The reference's fake-backend pattern (examples/demo/test_batching.py:7-27): scores from an integer
+    recurrence instead of a GPU."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+        self.calls = []
+
+    def step(self, requests):
+        self.calls.append(requests)
+        out = []
+        for slot, ids in requests:
+            p = self.torch.zeros(len(ids), 3)
+            p[:, 0] = self.torch.tensor([(7 * slot + i) % 10 / 10 for i in ids])
+            out.append(p)
+        return {"user": out, "assistant": out}
+
+    def reset(self):
+        self.calls.append("reset")
+
+
+def _guard():
+    from hs_guard.runtime import StreamingGuard, random_metadata
+    g = StreamingGuard.__new__(StreamingGuard)
+    g.engine, g.metadata, g.vocab_size, g.max_slots = _FakeEngine(), random_metadata(), 100, 4
+    return g
+
+
+def test_streaming_guard_validation_matches_reference_messages():
+    """Same ValueError conditions and messages as src/hs_guard/runtime.py:151-171."""
+    from hs_guard.runtime import StreamingGuard
+    g = _guard()
+    cases = [(([(0, [1])], "system"), "role must be user or assistant"),
+             (([], "user"), "Each tick requires nonempty requests and unique slots"),
+             (([(1, [1]), (1, [2])], "user"), "Each tick requires nonempty requests and unique slots"),
+             (([(4, [1])], "user"), "Slot is outside the allocated range"),
+             (([(-1, [1])], "user"), "Slot is outside the allocated range"),
+             (([(True, [1])], "user"), None),   # bool is an int in Python, as in the reference
+             (([(0, [])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
+             (([(0, [100])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
+             (([(0, [1.0])], "user"), "Each request requires nonempty in-vocabulary integer token IDs")]
+    for (req, role), msg in cases:
+        if msg is None:
+            g.step(req, role=role)
+            continue
+        with pytest.raises(ValueError, match=msg):
+            g.step(req, role=role)
+    for bad in (0, -1, 1.5, "2"):
+        with pytest.raises(ValueError, match="max_slots must be a positive integer"):
+            StreamingGuard(None, {}, max_slots=bad)
+
+
+def test_streaming_guard_cut_scores():
+    g = _guard()
+    out = g.step([(2, [3, 4]), (0, [9])], role="assistant")
+    assert out[0]["slot"] == 2 and out[1]["slot"] == 0
+    np.testing.assert_allclose(out[0]["cut_scores"], [1 - 0.7, 1 - 0.8], rtol=1e-6)
+    np.testing.assert_allclose(out[1]["cut_scores"], [1 - 0.9], rtol=1e-6)
+    assert out[0]["threshold"] == pytest.approx(0.1117895246)
+    g.reset()
+    assert g.engine.calls[-1] == "reset"
+
+
+def test_load_model_offline_behaviour(tmp_path):
+    from hs_guard.runtime import load_model
+    with pytest.raises(ValueError):
+        load_model("random", head="other")
+    with pytest.raises(RuntimeError, match="does not download"):
+        load_model("KrisLiu16/HS-Guard-v10")
+    (tmp_path / "hs_guard.json").write_text('{"format": "other"}')
+    with pytest.raises(ValueError, match="Unsupported model format"):
+        load_model(str(tmp_path))

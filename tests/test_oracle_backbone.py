@@ -1,0 +1,109 @@
+"""Pins the composition of the whole-step oracle -- CPU only.
+
+The streamed oracle (ticks of several sizes over per-slot pools) must reproduce transformers'
+Qwen3_5TextModel forward over the whole sequence (the complete-message path, docs/ENGINE.md:13) when the
+sequence fits the window. With the oracle's bf16 rounding switched off (``oracle.bf16.exact``) and
+transformers in float64 the two agree to the pools' fp32 storage round-off (~1e-6), which pins the composition (layer order, norm
+placement and offsets, head maps, RoPE, gates, conv history, recurrent state, ring). With rounding on they
+agree at bf16-noise level. Planted mistakes (a dropped attention gate, a wrong RMSNorm offset) move the
+result by orders of magnitude more.
+"""
+import numpy as np
+import pytest
+
+from oracle.backbone import StreamOracle
+from oracle.bf16 import exact
+
+torch = pytest.importorskip("torch")
+
+
+def _tiny_cfg():
+    from hs_guard.model import GuardConfig
+    return GuardConfig(vocab_size=50, hidden_size=64, num_hidden_layers=4, intermediate_size=96,
+                       linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=16,
+                       linear_value_head_dim=16, num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+                       window_tokens=16, head_hidden=32)
+
+
+def _weights(cfg, seed=0):
+    from hs_guard.model import GuardModel
+    m = GuardModel.random(cfg, seed=seed, device="cpu", std=0.2)
+    return {k: v.float().numpy() for k, v in m.weights.items()}
+
+
+def _hf_hidden(cfg, w, ids):
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextModel
+    hc = Qwen3_5TextConfig(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size,
+                           num_hidden_layers=cfg.num_hidden_layers, intermediate_size=cfg.intermediate_size,
+                           linear_num_key_heads=cfg.linear_num_key_heads,
+                           linear_num_value_heads=cfg.linear_num_value_heads,
+                           linear_key_head_dim=cfg.linear_key_head_dim, linear_value_head_dim=cfg.linear_value_head_dim,
+                           num_attention_heads=cfg.num_attention_heads, num_key_value_heads=cfg.num_key_value_heads,
+                           head_dim=cfg.head_dim, rms_norm_eps=cfg.rms_norm_eps,
+                           rope_parameters={"rope_type": "default", "rope_theta": cfg.rope_theta,
+                                            "partial_rotary_factor": cfg.partial_rotary_factor,
+                                            "mrope_section": [1, 1, 2]})
+    hc._attn_implementation = "eager"
+    model = Qwen3_5TextModel(hc).double().eval()
+    sd = {k[len("backbone."):]: torch.from_numpy(v).double() for k, v in w.items() if k.startswith("backbone.")}
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    with torch.no_grad():
+        out = model(input_ids=torch.tensor([ids]), use_cache=False).last_hidden_state[0]
+    return out.numpy()
+
+
+def _stream_hidden(oracle, slot, ids, ticks):
+    hid = []
+    at = 0
+    for size in ticks:
+        _, normed = oracle.tick([(slot, ids[at:at + size])])
+        hid.append(normed[0, :size])
+        at += size
+    return np.concatenate(hid)
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def test_streamed_oracle_matches_transformers_forward():
+    cfg = _tiny_cfg()
+    w = _weights(cfg)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, cfg.vocab_size, 15).tolist()          # < window: windowed == causal attention
+    ref = _hf_hidden(cfg, w, ids)
+    with exact():
+        oracle = StreamOracle(w, cfg, max_slots=3)
+        got = _stream_hidden(oracle, 1, ids, [5, 1, 7, 2])
+        assert _rel(got, ref) < 1e-5, _rel(got, ref)   # pools store fp32: ~1e-6 round-off
+        # a second slot streamed with other tick sizes agrees too (slot 1's state does not leak into it)
+        got2 = _stream_hidden(oracle, 2, ids, [1] * 15)
+        assert _rel(got2, ref) < 1e-5
+    rounded = _stream_hidden(StreamOracle(w, cfg, max_slots=3), 1, ids, [5, 1, 7, 2])
+    assert _rel(rounded, ref) < 0.1
+
+
+def test_planted_mistakes_are_detected():
+    cfg = _tiny_cfg()
+    w = _weights(cfg)
+    ids = np.random.default_rng(1).integers(0, cfg.vocab_size, 12).tolist()
+    ref = _hf_hidden(cfg, w, ids)
+    import oracle.ring as oring
+    orig = oring.ring_attention_v8
+
+    def no_gate(q, rk, rv, nk, value, gate, *a, **k):
+        return orig(q, rk, rv, nk, value, np.full_like(gate, 30.0), *a, **k)   # sigmoid ~ 1: gate dropped
+    oring.ring_attention_v8 = no_gate
+    try:
+        with exact():
+            bad = _stream_hidden(StreamOracle(w, cfg, 2), 0, ids, [4, 8])
+    finally:
+        oring.ring_attention_v8 = orig
+    assert _rel(bad, ref) > 1e-2
+    w2 = dict(w)
+    w2["backbone.layers.1.post_attention_layernorm.weight"] = w["backbone.layers.1.post_attention_layernorm.weight"] - 1.0
+    with exact():
+        bad = _stream_hidden(StreamOracle(w2, cfg, 2), 0, ids, [4, 8])
+    assert _rel(bad, ref) > 1e-2
