@@ -90,6 +90,20 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
             "avg_us": round(us, 2), "alg_bytes_per_launch": traffic_alg, "achieved_gbs": round(gbs, 1)}
 
 
+def measured_traffic(rows, state_dtype):
+    """HBM bytes per launch of the GDN slot step at the decode shape, as rocprofv3's FETCH_SIZE and WRITE_SIZE
+    counters read it (each scaled by the same counter's reading for a device copy of known size). The counter
+    runs cannot happen inside this process, so the figure comes from the committed counter summary of the
+    same command; it exists only for the default shape (352 rows, fp32 state), otherwise None."""
+    path = os.path.join(ROOT, "profiles", "gdn_step_352x1_counters.md")
+    if rows != 352 or state_dtype != 0 or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def ring_decode_rate(torch, rows=352, iters=50):
     """Achieved algorithmic GB/s of hsg_ring_attention at the 352 x 1-token decode shape with full rings."""
     from hs_guard.engine.kernels import ring_attention_v8
@@ -177,7 +191,13 @@ def main():
     roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
     log(f"GDN roofline {roof}")
     if args.roofline_only:
-        print(json.dumps({"roofline_only": roof}), flush=True)
+        # calibration for HBM-traffic counters: a plain 512 MiB device-to-device copy (512 MiB read + written)
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"roofline_only": roof, "calibration_copy_bytes": 512 << 20}), flush=True)
         return
     ring = ring_decode_rate(torch, rows=args.slots)
     log(f"ring decode {ring}")
@@ -204,6 +224,13 @@ def main():
             eng.step([(s, load.context()) for s in slots])
 
     # ---- warm-up + timed mixed steps ----
+    # graphs for every token bucket a mixed tick can plausibly hit (mean 4.175 tok/slot, sd 9.5 per slot),
+    # so no capture lands inside a timed step
+    t0 = time.time()
+    mean, sd = 4.175 * args.slots, 9.48 * args.slots ** 0.5
+    eng.prepare(args.slots, range(args.slots, int(mean + 8 * sd) + 1, 16))
+    torch.cuda.synchronize()
+    log(f"{eng.stats['captures']} graphs captured ({time.time() - t0:.1f}s)")
     for i in range(args.warmup):
         eng.step(load.step_requests())
         reprefill(load.resets())
@@ -273,7 +300,8 @@ def main():
         "single_token_ms": {"p50": round(percentile(one, 50), 3), "p95": round(percentile(one, 95), 3)},
         "reference_l20": REF_L20,
         "roofline": {"bound": "hbm", "achieved": roof["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(args.slots, state_code),
                      "kernel": roof["kernel"], "shape": roof["shape"], "avg_us": roof["avg_us"],
                      "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
         "ring_decode_352": ring,

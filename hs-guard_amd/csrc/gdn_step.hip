@@ -12,7 +12,11 @@
 // 128-byte row segment, so every load instruction reads 8 full 128-byte lines. The k.S and q.S
 // reductions over the 128 key rows are in-lane (16 rows) plus a 3-step butterfly over rg (lane xor 8,
 // 16, 32). exp(g) is folded in as (exp(g) S)^T k = exp(g) (S^T k), and the decay and rank-1 update share
-// one pass over the registers.
+// one pass over the registers. The state streams in and out with nontemporal accesses (it is touched once
+// per tick, so it should not displace cached weights and activations).
+// Token inputs (q, k of the key head; v, z of the value head; a, b) are staged in LDS 16 tokens at a time
+// by one cooperative burst of 16-byte loads, so a 64-token tick pays the global-memory latency 4 times
+// instead of 64 and the sequential token loop only touches LDS.
 #include "hsg_common.h"
 
 namespace hsg {
@@ -22,6 +26,7 @@ constexpr int KD = 128;
 constexpr int VD = 128;
 constexpr int TILE_V = 32;
 constexpr int ROWS = 16;
+constexpr int CT = 16;   // tokens staged in LDS per chunk
 
 struct GdnParams {
   const uint16_t* qkv;
@@ -51,29 +56,33 @@ struct GdnParams {
 template <typename ST>
 struct StateIO;
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 template <>
 struct StateIO<float> {
   static __device__ __forceinline__ void load(const float* p, float* v) {
-    const float4 x = *reinterpret_cast<const float4*>(p);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
   }
   static __device__ __forceinline__ void store(float* p, const float* v) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    const f32x4_t x = {v[0], v[1], v[2], v[3]};
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x4_t*>(p));
   }
 };
 
 template <>
 struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
   static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
-    const uint2 w = *reinterpret_cast<const uint2*>(p);
-    v[0] = h2f((uint16_t)(w.x & 0xffffu)); v[1] = h2f((uint16_t)(w.x >> 16));
-    v[2] = h2f((uint16_t)(w.y & 0xffffu)); v[3] = h2f((uint16_t)(w.y >> 16));
+    const u32x2_t w = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    v[0] = h2f((uint16_t)(w[0] & 0xffffu)); v[1] = h2f((uint16_t)(w[0] >> 16));
+    v[2] = h2f((uint16_t)(w[1] & 0xffffu)); v[3] = h2f((uint16_t)(w[1] >> 16));
   }
   static __device__ __forceinline__ void store(uint16_t* p, const float* v) {
-    uint2 w;
-    w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
-    w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
-    *reinterpret_cast<uint2*>(p) = w;
+    u32x2_t w;
+    w[0] = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+    w[1] = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
   }
 };
 
@@ -119,16 +128,46 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   const float A = expf(bf2f(p.A_log[hv]));
   const float dt = bf2f(p.dt_bias[hv]);
   __shared__ float red[2][4];
+  __shared__ __align__(16) uint16_t sq_[CT][KD];
+  __shared__ __align__(16) uint16_t sk_[CT][KD];
+  __shared__ __align__(16) uint16_t sv_[CT][VD];
+  __shared__ __align__(16) uint16_t sz_[GATED ? CT : 1][VD];
+  __shared__ float sa_[CT], sb_[CT];
+  constexpr int SEGS = GATED ? 64 : 48;   // 16-byte segments per token: q, k, v (, z)
 
   for (int t = 0; t < ntok; ++t) {
+    const int tt = t % CT;
+    if (tt == 0) {  // stage the next chunk of tokens in LDS with one burst of coalesced loads
+      const int nt = min(CT, ntok - t);
+      __syncthreads();
+      for (int e = threadIdx.x; e < nt * SEGS; e += 256) {
+        const int u = e / SEGS;
+        const int sg = e - u * SEGS;
+        const int which = sg >> 4;
+        const int c = (sg & 15) * 8;
+        const uint16_t* row = p.qkv + (tok0 + t + u) * p.qkv_stride;
+        uint16_t* dst;
+        const uint16_t* src;
+        if (which == 0) { src = row + p.q_off + h * KD + c; dst = &sq_[u][c]; }
+        else if (which == 1) { src = row + p.k_off + h * KD + c; dst = &sk_[u][c]; }
+        else if (which == 2) { src = row + p.v_off + hv * VD + c; dst = &sv_[u][c]; }
+        else { src = p.z + (tok0 + t + u) * p.z_stride + hv * VD + c; dst = &sz_[GATED ? u : 0][c]; }
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+      }
+      if (threadIdx.x < nt) {
+        const int64_t tok = tok0 + t + threadIdx.x;
+        sa_[threadIdx.x] = bf2f(p.a[tok * p.ab_stride + hv]);
+        sb_[threadIdx.x] = bf2f(p.b[tok * p.ab_stride + hv]);
+      }
+      __syncthreads();
+    }
     const int64_t tok = tok0 + t;
-    const uint16_t* row = p.qkv + tok * p.qkv_stride;
     float q[ROWS], k[ROWS], v[4];
-    load8_bf16(row + p.q_off + h * KD + rg * ROWS, q);
-    load8_bf16(row + p.q_off + h * KD + rg * ROWS + 8, q + 8);
-    load8_bf16(row + p.k_off + h * KD + rg * ROWS, k);
-    load8_bf16(row + p.k_off + h * KD + rg * ROWS + 8, k + 8);
-    load4_bf16(row + p.v_off + hv * VD + col, v);
+    load8_bf16(&sq_[tt][rg * ROWS], q);
+    load8_bf16(&sq_[tt][rg * ROWS + 8], q + 8);
+    load8_bf16(&sk_[tt][rg * ROWS], k);
+    load8_bf16(&sk_[tt][rg * ROWS + 8], k + 8);
+    load4_bf16(&sv_[tt][col], v);
     float qq = 0.f, kk = 0.f;
 #pragma unroll
     for (int j = 0; j < ROWS; ++j) {
@@ -144,9 +183,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       q[j] = q[j] * rq * p.scale;
       k[j] = k[j] * rk;
     }
-    const float x = bf2f(p.a[tok * p.ab_stride + hv]) + dt;
+    const float x = sa_[tt] + dt;
     const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
-    const float beta = sigmoidf_(bf2f(p.b[tok * p.ab_stride + hv]));
+    const float beta = sigmoidf_(sb_[tt]);
     const float decay = expf(g);
 
     float kv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -200,7 +239,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       if (rg == 0) {
         float y[4], w4[4], z4[4];
         load4_bf16(p.norm_w + col, w4);
-        load4_bf16(p.z + tok * p.z_stride + hv * VD + col, z4);
+        load4_bf16(&sz_[GATED ? tt : 0][col], z4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float hb = rbf(ob[i] * r);
@@ -239,7 +278,7 @@ int check_common(const GdnParams& p, int state_dtype, int n_rows, int K, int V) 
   if (p.offsets == nullptr && p.L <= 0) return HSG_ERR_ARG;
   if (K != KD || V != VD || p.HV % p.H != 0) return HSG_ERR_SHAPE;
   if (state_dtype != HSG_STATE_F32 && state_dtype != HSG_STATE_F16) return HSG_ERR_ARG;
-  if (!aligned(p.qkv, 16) || p.qkv_stride % 8 || p.q_off % 8 || p.k_off % 8 || p.v_off % 4) return HSG_ERR_ALIGN;
+  if (!aligned(p.qkv, 16) || p.qkv_stride % 8 || p.q_off % 8 || p.k_off % 8 || p.v_off % 8) return HSG_ERR_ALIGN;
   if (!aligned(p.state, 16)) return HSG_ERR_ALIGN;
   return 1;  // proceed
 }
@@ -317,6 +356,6 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
   const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
   if (rc <= 0) return rc;
   if (!z || !norm_w || !out) return HSG_ERR_ARG;
-  if (!hsg::aligned(z, 8) || z_stride % 4 || !hsg::aligned(norm_w, 8) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
+  if (!hsg::aligned(z, 16) || z_stride % 8 || !hsg::aligned(norm_w, 8) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
   return hsg::launch<true>(p, state_dtype, n_rows, stream);
 }

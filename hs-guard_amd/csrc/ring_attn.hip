@@ -1,17 +1,22 @@
-// Window-W GQA ring attention (decode and short ticks) for gfx950.
+// Window-W GQA ring attention (decode, short ticks and 64-token window fills) for gfx950 on MFMA.
 //
-// Contract: src/hs_guard/engine/ring_attention_kernel.py:7-26 (torch reference) with the v8 epilogue of
-// src/hs_guard/engine/fused_kernels.py:341-355 (bf16 output times bf16(sigmoid(gate)), in-place ring write).
+// Contract: src/hs_guard/engine/ring_attention_kernel.py:7-26 (torch reference) with the v8 kernel's
+// numerics and epilogue (src/hs_guard/engine/fused_kernels.py:288-356): keys in blocks of 32 (the W ring
+// columns in order, then the tick's new keys), a running max per query row, probabilities rounded to bf16
+// in the P.V product and summed in fp32, output / sum rounded to bf16, times bf16(sigmoid(gate)); the
+// tick's keys/values are written into the ring in place after every read.
 //
-// Mapping: one workgroup of NW = 4 waves per (row, kv head); the workgroup owns that (slot, kv head)'s
-// ring, so the ring write at the end cannot race with any read. The W ring columns are split across the
-// waves (split-K inside the workgroup: each wave keeps its own max / sum / accumulator and the four are
-// merged through LDS), and the tick's new keys are dealt round-robin to the waves. Queries are processed
-// four rows at a time: the G = Hq/Hkv query heads of one token l share the token's position, so the
-// window predicate is uniform over the four rows and masked columns are skipped without reading K or V.
-//   Scores: 16 lanes per key (each a contiguous 32-byte slice of the 512-byte key row, so 16 lanes read
-//   one row), 4 keys per wave instruction, butterfly over the 16 lanes.
-//   Values: each lane owns 4 of the 256 dims, one coalesced 512-byte row per key.
+// Mapping: one workgroup (4 waves) per (row, kv head), so the workgroup owns that (slot, kv head)'s ring
+// and the ring write at the end cannot race with any read. Query rows r = l*G + g (token l, q group g)
+// form 16-row tiles; wave w takes tile 4*qg + w for query group qg. Per 64 keys the workgroup stages K
+// (row-major) and V (transposed) in LDS with coalesced 16-byte loads, skipping fills whose positions are
+// outside every query's window; then for each of the two 32-key softmax blocks of the fill each wave runs
+// on v_mfma_f32_16x16x32_bf16:
+//   S^T[key, m] = K . Q^T   (A = K rows from LDS, B = Q from registers; 2 key tiles x 8 d-steps)
+//   O^T[d, m] += V^T . P^T  (A = V^T from LDS, B = P straight from the S^T accumulators: the k order of the
+//                            product is the lane's own key order, so P never leaves registers)
+// The S^T accumulator layout puts one query row per lane column, so the running max / sum and the O^T
+// rescale are per-lane scalars plus a 2-step butterfly (lane xor 16, 32).
 #include <math.h>
 
 #include "hsg_common.h"
@@ -21,11 +26,16 @@ namespace {
 
 constexpr int D = 256;
 constexpr int NW = 4;
+constexpr int KB = 32;                 // keys per softmax block (the reference's BN)
+constexpr int SB = 2;                  // softmax blocks staged per LDS fill
+constexpr int KF = KB * SB;            // keys per LDS fill
 constexpr int W_MAX = 512;
 constexpr int LB_MAX = 64;
-constexpr int CW_MAX = W_MAX / NW;
-constexpr int NEW_MAX = LB_MAX / NW;
-constexpr int COLS_MAX = CW_MAX + NEW_MAX;
+constexpr int KS_STRIDE = D + 8;       // bf16 per K row in LDS (16-byte pad)
+constexpr int VT_STRIDE = KF + 8;      // bf16 per V^T row in LDS
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
 
 struct RingParams {
   const uint16_t* q; int64_t q_sn, q_sl, q_sh, q_sg;
@@ -41,15 +51,16 @@ struct RingParams {
   uint16_t* out; int64_t o_sn, o_sl, o_sh, o_sg;
 };
 
-__device__ __forceinline__ float sum16(float x) {
-  x = xor_add<1>(x); x = xor_add<2>(x); x = xor_add<4>(x); x = xor_add<8>(x);
-  return x;
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 w) { return __builtin_bit_cast(bf16x8, w); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-__global__ __launch_bounds__(NW * 64) void ring_attn_kernel(const RingParams p) {
-  __shared__ float sc[NW][4][COLS_MAX];
-  __shared__ float accs[NW][4][D];
-  __shared__ float mls[NW][4][2];
+__global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParams p) {
+  __shared__ __align__(16) uint16_t Ks[KF * KS_STRIDE];
+  __shared__ __align__(16) uint16_t Vt[D * VT_STRIDE];
+  __shared__ int64_t kp_s[KF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -70,175 +81,197 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_kernel(const RingParams p) 
   const int64_t g_row = padded ? n * p.g_sn : base_tok * p.g_sl;
   const int64_t o_row = padded ? n * p.o_sn : base_tok * p.o_sl;
   const int W = p.W;
-  const int cw = W / NW;
-  const int nnew = (int)len;                            // valid new keys (j < len)
+  const int G = p.G;
   const int64_t ring_base = ((slot * p.hkv + h) * (int64_t)(W + 1)) * D;
   const int64_t* rpos = p.ring_pos + slot * (int64_t)(W + 1);
-  const int sub = lane & 15;
-  const int ks = lane >> 4;
-  const int groups4 = (p.G + 3) >> 2;
+  const int M = G * steps;                              // query rows of this (row, kv head)
+  const int QT = (M + 15) >> 4;                         // 16-row tiles
+  const int q4 = lane >> 4;                             // lane group: keys 4*q4 .., dims 8*q4 ..
+  const int mcol = lane & 15;                           // the lane's query row within its tile
+  const int n_ring_blocks = len > 0 ? W / KB : 0;
+  const int n_new_blocks = (int)((len + KB - 1) / KB);
 
-  for (int quad = 0; quad < steps * groups4; ++quad) {
-    const int l = quad / groups4;
-    const int g0 = (quad - l * groups4) * 4;
-    const bool q_valid = l < len;
-    const int64_t qpos = start + l;
-    if (!q_valid) {  // no visible key: output 0 (times the gate is still 0)
-      for (int e = tid; e < 4 * (D / 4); e += NW * 64) {
-        const int i = e / (D / 4);
-        const int d = (e - i * (D / 4)) * 4;
-        if (g0 + i < p.G) {
-          const float zero[4] = {0.f, 0.f, 0.f, 0.f};
-          store4_bf16(p.out + o_row + l * p.o_sl + h * p.o_sh + (g0 + i) * p.o_sg + d, zero);
-        }
-      }
-      continue;
+  for (int qg = 0; qg * NW < QT; ++qg) {
+    const int tile = qg * NW + wave;
+    const bool has_tile = tile < QT;
+    // ---- this lane's query row ----
+    const int r = tile * 16 + mcol;
+    const int l_tok = r / G;
+    const int gq = r - l_tok * G;
+    const bool row_ok = has_tile && r < M;
+    const bool q_valid = row_ok && l_tok < len;
+    const int64_t qpos = start + l_tok;
+    bf16x8 qb[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (q_valid)
+        w = *reinterpret_cast<const uint4*>(p.q + q_row + l_tok * p.q_sl + h * p.q_sh + gq * p.q_sg + 32 * ks + 8 * q4);
+      qb[ks] = as_bf16x8(w);
     }
-    // ---- queries of the quad: lane holds dims [16 sub, 16 sub + 16) of each of the 4 rows ----
-    float qf[4][16];
+    // positions covered by this query group (all waves), for skipping whole key blocks
+    const int r_lo = qg * NW * 16;
+    const int r_hi = min(M, (qg + 1) * NW * 16) - 1;
+    const int64_t qpos_lo = start + r_lo / G;
+    const int64_t qpos_hi = start + min((int64_t)(r_hi / G), len - 1);
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 O[D / 16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (g0 + i < p.G) {
-        const uint16_t* qp = p.q + q_row + l * p.q_sl + h * p.q_sh + (g0 + i) * p.q_sg + sub * 16;
-        load8_bf16(qp, qf[i]);
-        load8_bf16(qp + 8, qf[i] + 8);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) qf[i][e] = 0.f;
+    for (int t = 0; t < D / 16; ++t) O[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    for (int blk = 0; blk < n_ring_blocks + n_new_blocks;) {
+      // a fill holds up to SB consecutive softmax blocks of one kind (ring columns or new keys)
+      const bool is_ring = blk < n_ring_blocks;
+      const int nb = is_ring ? min(SB, n_ring_blocks - blk) : min(SB, n_ring_blocks + n_new_blocks - blk);
+      const int nkeys = nb * KB;
+      const int c0 = is_ring ? blk * KB : (blk - n_ring_blocks) * KB;   // ring column or new-key index
+      blk += nb;
+      __syncthreads();  // the previous fill's LDS reads are done
+      int vis = 0;
+      if (tid < KF) {
+        int64_t kpos = -1;
+        if (tid < nkeys) kpos = is_ring ? rpos[c0 + tid] : ((c0 + tid < len) ? start + c0 + tid : -1);
+        kp_s[tid] = kpos;
+        vis = kpos >= 0 && kpos <= qpos_hi && kpos > qpos_lo - W;
       }
-    }
-    // ---- pass 1: scores of this wave's columns (ring slice, then its share of the new keys) ----
-    const int c0 = wave * cw;
-    const int my_new = nnew > wave ? (nnew - wave + NW - 1) / NW : 0;
-    const int ncols = cw + my_new;
-    for (int vb = 0; vb < ncols; vb += 4) {
-      const int vi = vb + ks;
-      bool ok = false;
-      const uint16_t* kp = nullptr;
-      if (vi < cw) {
-        const int64_t kpos = rpos[c0 + vi];
-        ok = kpos >= 0 && kpos <= qpos && kpos > qpos - W;
-        kp = p.ring_k + ring_base + (int64_t)(c0 + vi) * D;
-      } else if (vi < ncols) {
-        const int j = wave + (vi - cw) * NW;
-        const int64_t kpos = start + j;  // j < len by construction
-        ok = kpos <= qpos && kpos > qpos - W;
-        kp = p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh;
+      if (!__syncthreads_or(vis)) continue;  // no query of this group sees these keys
+      // ---- stage K (row-major): 4 threads per 512-byte row, 128 bytes each ----
+      {
+        const int row = tid >> 2, seg = tid & 3;
+        const uint16_t* src;
+        bool live;
+        if (is_ring) { src = p.ring_k + ring_base + (int64_t)(c0 + row) * D; live = row < nkeys; }
+        else { src = p.new_k + nk_row + (int64_t)(c0 + row) * p.nk_sl + h * p.nk_sh; live = row < nkeys && c0 + row < len; }
+        uint4 w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          w[i] = live ? *reinterpret_cast<const uint4*>(src + seg * 64 + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&Ks[row * KS_STRIDE + seg * 64 + 8 * i]) = w[i];
       }
-      float s[4] = {0.f, 0.f, 0.f, 0.f};
-      if (ok) {
-        float kf[16];
-        load8_bf16(kp + sub * 16, kf);
-        load8_bf16(kp + sub * 16 + 8, kf + 8);
+      // ---- stage V transposed: a key pair x 32 dims per thread ----
+      {
+        const int kp2 = tid & 31, chunk = tid >> 5;
+        const int k0 = 2 * kp2, d0 = chunk * 32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int half = 0; half < 2; ++half) {
+          const int dd = d0 + 16 * half;
+          uint4 a[2], b[2];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) s[i] += qf[i][e] * kf[e];
-        }
-      }
+          for (int e = 0; e < 2; ++e) {
+            const int key = k0 + e;
+            const uint16_t* src;
+            bool live;
+            if (is_ring) { src = p.ring_v + ring_base + (int64_t)(c0 + key) * D; live = key < nkeys; }
+            else { src = p.new_v + nv_row + (int64_t)(c0 + key) * p.nv_sl + h * p.nv_sh; live = key < nkeys && c0 + key < len; }
+            uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0;
+            if (live) {
+              x0 = *reinterpret_cast<const uint4*>(src + dd);
+              x1 = *reinterpret_cast<const uint4*>(src + dd + 8);
+            }
+            if (e == 0) { a[0] = x0; a[1] = x1; } else { b[0] = x0; b[1] = x1; }
+          }
+          const uint32_t* va = reinterpret_cast<const uint32_t*>(a);
+          const uint32_t* vb = reinterpret_cast<const uint32_t*>(b);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[i] = sum16(s[i]);
-      if (sub == 0 && vi < ncols) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[wave][i][vi] = ok ? s[i] * p.scale : -INFINITY;
-      }
-    }
-    // ---- wave-local softmax statistics (LDS written by this wave only; wave-synchronous) ----
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    float m[4], lsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = -INFINITY;
-      for (int vi = lane; vi < ncols; vi += 64) mx = fmaxf(mx, sc[wave][i][vi]);
-      m[i] = wave_max(mx);
-      float sm = 0.f;
-      for (int vi = lane; vi < ncols; vi += 64) {
-        const float sv = sc[wave][i][vi];
-        const float pv = (m[i] == -INFINITY || sv == -INFINITY) ? 0.f : expf(sv - m[i]);
-        sc[wave][i][vi] = pv;
-        sm += pv;
-      }
-      lsum[i] = wave_sum(sm);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // ---- pass 2: P V over the same columns; lane owns dims [4 lane, 4 lane + 4) ----
-    float acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[i][e] = 0.f;
-    }
-    for (int vi = 0; vi < ncols; ++vi) {
-      const float p0 = sc[wave][0][vi], p1 = sc[wave][1][vi], p2 = sc[wave][2][vi], p3 = sc[wave][3][vi];
-      if (p0 == 0.f && p1 == 0.f && p2 == 0.f && p3 == 0.f) continue;
-      const uint16_t* vp;
-      if (vi < cw) {
-        vp = p.ring_v + ring_base + (int64_t)(c0 + vi) * D;
-      } else {
-        const int j = wave + (vi - cw) * NW;
-        vp = p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh;
-      }
-      float vf[4];
-      load4_bf16(vp + lane * 4, vf);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc[0][e] += p0 * vf[e];
-        acc[1][e] += p1 * vf[e];
-        acc[2][e] += p2 * vf[e];
-        acc[3][e] += p3 * vf[e];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<float4*>(&accs[wave][i][lane * 4]) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-      if (lane == 0) {
-        mls[wave][i][0] = m[i];
-        mls[wave][i][1] = lsum[i];
-      }
-    }
-    __syncthreads();
-    // ---- merge the four waves, normalise, gate, store ----
-    {
-      const int i = tid >> 6;
-      const int d = (tid & 63) * 4;
-      if (g0 + i < p.G) {
-        float mmax = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) mmax = fmaxf(mmax, mls[w][i][0]);
-        float num[4] = {0.f, 0.f, 0.f, 0.f};
-        float den = 0.f;
-        if (mmax != -INFINITY) {
-#pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            const float mw = mls[w][i][0];
-            const float f = mw == -INFINITY ? 0.f : expf(mw - mmax);
-            den += f * mls[w][i][1];
-            const float4 a4 = *reinterpret_cast<const float4*>(&accs[w][i][d]);
-            num[0] += f * a4.x; num[1] += f * a4.y; num[2] += f * a4.z; num[3] += f * a4.w;
+          for (int i = 0; i < 8; ++i) {   // dims dd + 2i, dd + 2i + 1
+            const uint32_t lo = (va[i] & 0xffffu) | (vb[i] << 16);
+            const uint32_t hi = (va[i] >> 16) | (vb[i] & 0xffff0000u);
+            *reinterpret_cast<uint32_t*>(&Vt[(dd + 2 * i) * VT_STRIDE + k0]) = lo;
+            *reinterpret_cast<uint32_t*>(&Vt[(dd + 2 * i + 1) * VT_STRIDE + k0]) = hi;
           }
         }
-        float y[4];
+      }
+      __syncthreads();
+      if (!has_tile) continue;
+#pragma unroll 1
+      for (int sb = 0; sb < nb; ++sb) {
+        const int kb = sb * KB;   // softmax block within the fill
+        // ---- S^T = K . Q^T for keys kb + [16 kt, 16 kt + 16) ----
+        f32x4 S[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = den > 0.f ? rbf(num[e] / den) : 0.f;
-        if (p.gate != nullptr) {
-          float gt[4];
-          load4_bf16(p.gate + g_row + l * p.g_sl + h * p.g_sh + (g0 + i) * p.g_sg + p.g_off + d, gt);
+        for (int kt = 0; kt < 2; ++kt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          const uint16_t* krow = &Ks[(kb + 16 * kt + mcol) * KS_STRIDE + 8 * q4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = y[e] * rbf(1.0f / (1.0f + expf(-gt[e])));
+          for (int ks = 0; ks < D / 32; ++ks) {
+            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * ks));
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[ks], acc, 0, 0, 0);
+          }
+          S[kt] = acc;
         }
-        store4_bf16(p.out + o_row + l * p.o_sl + h * p.o_sh + (g0 + i) * p.o_sg + d, y);
+        // ---- mask, online softmax over the block (the lane's 8 keys: 4 q4 + i and 16 + 4 q4 + i) ----
+        float s[8];
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t kpos = kp_s[kb + 16 * kt + 4 * q4 + i];
+            const bool ok = q_valid && kpos >= 0 && kpos <= qpos && kpos > qpos - W;
+            const float v = ok ? S[kt][i] * p.scale : -INFINITY;
+            s[4 * kt + i] = v;
+            bmax = fmaxf(bmax, v);
+          }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const float m_new = fmaxf(m_run, bmax);
+        const float m_safe = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = expf(m_run - m_safe);   // exp(-inf) = 0 before the first visible key
+        float psum = 0.f;
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = expf(s[2 * i] - m_safe);
+          const float p1 = expf(s[2 * i + 1] - m_safe);
+          psum += p0 + p1;
+          pk[i] = pack_bf16(p0, p1);
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        const bf16x8 pb = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
+        // ---- O^T += V^T . P^T over the block's 32 keys, in the lane's key order ----
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+          const uint16_t* vrow = &Vt[(16 * t + mcol) * VT_STRIDE + kb];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * q4);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * q4);
+          const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+          f32x4 o = O[t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] *= alpha;
+          O[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o, 0, 0, 0);
+        }
       }
     }
-    __syncthreads();
+    // ---- normalise, gate, store this lane's row: dims 16 t + 4 q4 + i ----
+    if (row_ok) {
+      uint16_t* dst = p.out + o_row + l_tok * p.o_sl + h * p.o_sh + gq * p.o_sg;
+      const uint16_t* gsrc = p.gate ? p.gate + g_row + l_tok * p.g_sl + h * p.g_sh + gq * p.g_sg + p.g_off : nullptr;
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) {
+        const int d = 16 * t + 4 * q4;
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = l_run > 0.f ? rbf(O[t][i] / l_run) : 0.f;
+        if (gsrc) {
+          float gt[4];
+          load4_bf16(gsrc + d, gt);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[i] = y[i] * rbf(1.0f / (1.0f + expf(-gt[i])));
+        }
+        store4_bf16(dst + d, y);
+      }
+    }
   }
 
   // ---- in-place ring write of this tick's valid keys/values (all reads of this ring are done) ----
   if (p.write_ring && len > 0) {
-    for (int e = tid; e < nnew * (D / 4); e += NW * 64) {
+    __syncthreads();
+    for (int e = tid; e < (int)len * (D / 4); e += NW * 64) {
       const int j = e / (D / 4);
       const int d = (e - j * (D / 4)) * 4;
       const int64_t col = (start + j) % W;
@@ -269,16 +302,16 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
   if (n_rows == 0) return HSG_OK;
   if (!q || !ring_k || !ring_v || !new_k || !new_v || !ring_pos || !slots || !starts || !lens || !out)
     return HSG_ERR_ARG;
-  if (head_dim != D || window <= 0 || window > W_MAX || window % (4 * NW) != 0 || lb > LB_MAX) return HSG_ERR_SHAPE;
+  if (head_dim != D || window <= 0 || window > W_MAX || window % KB != 0 || lb > LB_MAX) return HSG_ERR_SHAPE;
   if (write_ring && lb > window) return HSG_ERR_SHAPE;  // two steps of one tick would share a ring column
-  const int64_t s16[] = {q_sn, q_sl, q_sh, q_sg};
+  const int64_t s16[] = {q_sn, q_sl, q_sh, q_sg, nk_sn, nk_sl, nk_sh, nv_sn, nv_sl, nv_sh};
   for (int64_t s : s16)
     if (s % 8) return HSG_ERR_ALIGN;
-  const int64_t s4[] = {nk_sn, nk_sl, nk_sh, nv_sn, nv_sl, nv_sh, g_sn, g_sl, g_sh, g_sg, g_off, o_sn, o_sl, o_sh, o_sg};
+  const int64_t s4[] = {g_sn, g_sl, g_sh, g_sg, g_off, o_sn, o_sl, o_sh, o_sg};
   for (int64_t s : s4)
     if (s % 4) return HSG_ERR_ALIGN;
   if (!aligned(q, 16) || !aligned(ring_k, 16) || !aligned(ring_v, 16) || !aligned(new_k, 16) ||
-      !aligned(new_v, 8) || !aligned(out, 8) || (gate && !aligned(gate, 8)))
+      !aligned(new_v, 16) || !aligned(out, 8) || (gate && !aligned(gate, 8)))
     return HSG_ERR_ALIGN;
   RingParams p{};
   p.q = static_cast<const uint16_t*>(q); p.q_sn = q_sn; p.q_sl = q_sl; p.q_sh = q_sh; p.q_sg = q_sg;
@@ -291,7 +324,7 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
   p.ring_pos = ring_pos; p.slots = slots; p.starts = starts; p.lens = lens; p.offsets = offsets;
   p.lb = lb; p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring;
   p.out = static_cast<uint16_t*>(out); p.o_sn = o_sn; p.o_sl = o_sl; p.o_sh = o_sh; p.o_sg = o_sg;
-  hipLaunchKernelGGL(ring_attn_kernel, dim3((unsigned)(n_rows * hkv)), dim3(NW * 64), 0,
+  hipLaunchKernelGGL(ring_attn_mfma_kernel, dim3((unsigned)(n_rows * hkv)), dim3(NW * 64), 0,
                      reinterpret_cast<hipStream_t>(stream), p);
   return launch_status();
 }

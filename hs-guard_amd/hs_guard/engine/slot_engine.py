@@ -40,9 +40,11 @@ def bucket(value, choices):
 
 
 def token_buckets(max_tokens):
-    """Packed-token buckets: powers of two to 256, then steps of 256 to 4096, then steps of 2048."""
-    out = [1, 2, 4, 8, 16, 32, 64, 128, 256]
-    out += list(range(512, 4097, 256))
+    """Packed-token buckets: 1, 2, 4, 8, 16, then steps of 16 to 512 (a decode tick of n slots pads to at most
+    15 tokens), steps of 128 to 4096, then steps of 2048."""
+    out = [1, 2, 4, 8]
+    out += list(range(16, 513, 16))
+    out += list(range(640, 4097, 128))
     out += list(range(6144, max(max_tokens, 6144) + 2048, 2048))
     out = sorted({b for b in out if b < max_tokens} | {max_tokens})
     return tuple(out)
@@ -351,6 +353,13 @@ class SlotStreamEngine:
             host_out = torch.zeros(len(self.roles), tb, 3, dtype=torch.float32, pin_memory=True)
             self.graphs[key] = (graph, inp, probs, host_in, host_in.numpy(), host_out, host_out.numpy())
         return self.graphs[key]
+
+    def prepare(self, rows, token_counts):
+        """Capture ahead of time the step graphs for ticks of ``rows`` rows and each total token count in
+        ``token_counts`` (by bucket), so that a serving loop never pays a capture inside a tick."""
+        nb = bucket(rows, self.session_buckets)
+        for tb in sorted({bucket(t, self.token_buckets) for t in token_counts}):
+            self._static(nb, tb)
 
     def _run_arrays(self, chunks, slots):
         """One tick: <= max_rows rows of <= max_tick_tokens tokens. Returns (probs [R, T, 3] numpy, lens,

@@ -90,7 +90,7 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * kpos > qpos - window. Output = softmax-weighted values, rounded to bf16, times bf16(sigmoid(gate)).
  * write_ring != 0: after every read, new key/value of each valid step j go to ring column
  * (start+j) % window. ring_pos itself is not written (see hsg_ring_pos_update).
- * Supported: head_dim == 256, window <= 512 and a multiple of 16, lb <= 64 (rows with lens[n] > 64 are
+ * Supported: head_dim == 256, window <= 512 and a multiple of 32, lb <= 64 (rows with lens[n] > 64 are
  * treated as empty); write_ring needs lb <= window so that the steps of one tick own distinct columns.
  */
 int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,

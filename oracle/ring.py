@@ -12,9 +12,16 @@ keeping exactly the keys with ``kpos >= 0 and kpos <= qpos and kpos > qpos - W``
 to ring column ``start % W``. ``ring_scatter`` is the Lb > 1 write of ``slot_engine_v8.py:253-255``
 (column ``pos % W`` for valid steps, scratch column W otherwise).
 
+``attend_blockwise`` restates the numerics of the reference's Triton kernels (fused_kernels.py:309-341,
+ring_attention_kernel.py:129-160): keys in blocks of 32 (the W ring columns in order, then the tick's new
+keys), a running max per query row, ``acc = acc * alpha + bf16(p) @ v`` and ``l = l * alpha + sum(p)`` with
+p in full precision in the sum; ``ring_attention_v8`` uses it. Without bf16 rounding (``oracle.bf16.exact``)
+it equals ``ring_attention_reference``.
+
 Pinning (``tests/test_oracle_ring.py``): torch ``scaled_dot_product_attention`` with an explicit boolean
 mask; fill 0 with only the new key gives ``v_new * sigmoid(gate)``; all-equal keys give the mean of the
-valid values; a brute-force enumeration of the window predicate.
+valid values; a brute-force enumeration of the window predicate; blockwise == exact without rounding and
+within the bf16 bound of p with it.
 """
 import numpy as np
 
@@ -64,6 +71,38 @@ def ring_attention_reference(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, s
     return np.einsum('nhmj,nhjd->nhmd', p, values)
 
 
+def attend_blockwise(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, lens, scale, window, block=32):
+    """Same contract as ring_attention_reference, with the Triton kernels' blockwise online softmax and bf16
+    probabilities in the P.V product. Returns [N, Hkv, G*Lb, D] float64."""
+    q = np.asarray(q, dtype=np.float64)
+    N, Hkv, M, D = q.shape
+    lb = new_k.shape[2]
+    ok = allowed_mask(ring_pos, slots, starts, lens, lb, M // lb, window)
+    slots = np.asarray(slots, dtype=np.int64)
+    keys = np.concatenate([np.asarray(ring_k, dtype=np.float64)[slots, :, :window],
+                           np.asarray(new_k, dtype=np.float64)], 2)
+    values = np.concatenate([np.asarray(ring_v, dtype=np.float64)[slots, :, :window],
+                             np.asarray(new_v, dtype=np.float64)], 2)
+    scores = np.where(ok[:, None], np.einsum('nhmd,nhjd->nhmj', q, keys) * scale, -np.inf)
+    m = np.full((N, Hkv, M), -np.inf)
+    l = np.zeros((N, Hkv, M))
+    acc = np.zeros((N, Hkv, M, D))
+    edges = list(range(0, window, block)) + [window + j for j in range(0, lb, block)]
+    ends = edges[1:] + [window + lb]
+    for b0, b1 in zip(edges, ends):
+        b1 = min(b1, window) if b0 < window else b1
+        sb = scores[..., b0:b1]
+        m_new = np.maximum(m, sb.max(-1))
+        m_safe = np.where(np.isfinite(m_new), m_new, 0.0)
+        pb = np.where(np.isfinite(sb), np.exp(sb - m_safe[..., None]), 0.0)
+        alpha = np.where(np.isfinite(m), np.exp(m - m_safe), 0.0)
+        acc = acc * alpha[..., None] + np.einsum('nhmj,nhjd->nhmd', np.asarray(bf16(pb), np.float64),
+                                                 values[:, :, b0:b1])
+        l = l * alpha + pb.sum(-1)
+        m = m_new
+    return np.where(l[..., None] > 0, acc / np.where(l > 0, l, 1.0)[..., None], 0.0)
+
+
 def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens, scale, window,
                       write_ring):
     """Returns (out [N, Lb, Hq*D] float32 of bf16 values, attn [N, Hkv, G*Lb, D] float64, ring_k', ring_v')."""
@@ -73,7 +112,7 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
     Hq = Hkv * G
     value = np.asarray(value, dtype=np.float64).reshape(N, lb, Hkv, D)
     new_v = value.transpose(0, 2, 1, 3)
-    attn = ring_attention_reference(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, lens, scale, window)
+    attn = attend_blockwise(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, lens, scale, window)
     o = attn.reshape(N, Hkv, G, lb, D).transpose(0, 3, 1, 2, 4).reshape(N, lb, Hq, D)
     gt = np.asarray(gate, dtype=np.float64).reshape(N, lb, Hq, 2 * D)[..., D:]
     sig = bf16(sigmoid(gt))

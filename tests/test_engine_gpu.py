@@ -88,7 +88,9 @@ def _matched_gemm(eng):
 
 
 def _max_diff(got, ref):
-    return max(np.abs(g.numpy() - e).max() for role in ("user", "assistant") for g, e in zip(got[role], ref[role]))
+    """Largest per-token difference of the cut score 1 - p(safe) over both roles (the north-star quantity)."""
+    return max(np.abs(g.numpy()[:, 0] - e[:, 0]).max() for role in ("user", "assistant")
+               for g, e in zip(got[role], ref[role]))
 
 
 @pytest.fixture(scope="module")
@@ -164,8 +166,9 @@ def test_engine_matches_oracle(setup):
     rk = eng.ring_k[:, :, :, :W].float().cpu().numpy()
     valid = orc.ring_pos[:4, :W] >= 0
     for s in range(4):
-        d = np.abs(rk[:, s][..., valid[s], :] - orc.ring_k[:, s, :, :W][..., valid[s], :]).max()
-        assert d < 5e-2, f"ring_k slot {s} diff {d}"
+        got_k, ref_k = rk[:, s][..., valid[s], :], orc.ring_k[:, s, :, :W][..., valid[s], :]
+        rel = np.linalg.norm(got_k - ref_k) / np.linalg.norm(ref_k)
+        assert rel < 2e-2, f"ring_k slot {s} rel diff {rel:.2e}"
 
 
 def test_graph_replays_match_eager(setup):

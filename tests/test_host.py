@@ -41,7 +41,7 @@ def test_buckets():
     from hs_guard.engine.slot_engine import bucket, token_buckets
     tb = token_buckets(352 * 64)
     assert tb[0] == 1 and tb[-1] == 352 * 64 and list(tb) == sorted(set(tb))
-    assert bucket(1470, tb) == 1536 and bucket(1, tb) == 1
+    assert bucket(1470, tb) == 1536 and bucket(1, tb) == 1 and bucket(352, tb) == 352
     with pytest.raises(ValueError):
         bucket(352 * 64 + 1, tb)
 

@@ -84,3 +84,18 @@ def test_equal_keys_give_mean_of_visible_values():
         vis = [c for c in range(W) if 0 <= rp[slots[n], c] <= starts[n] and rp[slots[n], c] > starts[n] - W]
         vals = np.concatenate([rv[slots[n], :, vis], nv[n, :, :1].transpose(1, 0, 2)], 0)   # [k, Hkv, D]
         np.testing.assert_allclose(out[n, :, 0], vals.mean(0), rtol=1e-12)
+
+
+def test_blockwise_equals_exact_without_rounding_and_is_within_bf16_p_bound():
+    from oracle.bf16 import exact
+    rng = np.random.default_rng(3)
+    for lb in (1, 3, 40):
+        q, rk, rv, nk, nv, rp, slots, starts, lens, W = _setup(rng, N=3, Lb=lb, W=64, D=16)
+        ref = oring.ring_attention_reference(q, rk, rv, nk, nv, rp, slots, starts, lens, 0.4, W)
+        with exact():
+            blk = oring.attend_blockwise(q, rk, rv, nk, nv, rp, slots, starts, lens, 0.4, W)
+        np.testing.assert_allclose(blk, ref, rtol=1e-10, atol=1e-12)
+        rounded = oring.attend_blockwise(q, rk, rv, nk, nv, rp, slots, starts, lens, 0.4, W)
+        # bf16 p: each weight moves by at most 2**-8 relative, so the output by at most 2**-8 * sum|p v| / l
+        bound = 2.0 ** -8 * np.abs(nv).max() * 2 + 1e-12
+        assert np.abs(rounded - ref).max() <= bound

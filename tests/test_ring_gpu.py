@@ -96,7 +96,8 @@ def test_reference_contract_ungated():
     dev = torch.device("cuda:0")
     out = ring_attention(q.to(dev), ring_k.to(dev), ring_v.to(dev), new_k.to(dev), new_v.to(dev), ring_pos.to(dev),
                          slots.to(dev), starts.to(dev), lens.to(dev), D ** -0.5, W)
-    ref = oring.ring_attention_reference(_np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(new_v), ring_pos.numpy(),
-                                         slots.numpy(), starts.numpy(), lens.numpy(), D ** -0.5, W)
+    # the Triton contract's numerics (bf16 probabilities in P.V, blockwise running max)
+    ref = oring.attend_blockwise(_np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(new_v), ring_pos.numpy(),
+                                 slots.numpy(), starts.numpy(), lens.numpy(), D ** -0.5, W)
     from oracle.bf16 import bf16
     _check(_np(out), bf16(ref), rtol=2.0 ** -8)
