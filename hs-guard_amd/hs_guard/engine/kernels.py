@@ -76,6 +76,39 @@ def gdn_slot_recurrent(q, k, v, a, b, A_log, dt_bias, state, slots, lens, scale=
     return o
 
 
+def gdn_chunk_prefill(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log, dt_bias, state, slots,
+                      lens, offsets=None, scale=None, with_sq=False):
+    """Chunked prefill (replaces FLA chunk_gated_delta_rule with initial_state = state[slots] and
+    output_final_state written back, bucketed_engine.py:109-111), with gdn_slot_v8's input contract.
+
+    Padded layout (offsets None): packed [N, L, C], a/b [N, L, HV]; returns o [N, L, HV, V] with zeros past
+    lens. Packed layout: packed [T, C], a/b [T, HV], row n's tokens at offsets[n] .. offsets[n]+lens[n]-1;
+    returns o [T, HV, V]. State rows slots[n] (lens > 0) are updated in place. Returns (o, sq or None)."""
+    for tensor in (packed, a, b, state):
+        _require(tensor.is_contiguous(), "tensors must be contiguous")
+    _gpu(packed, a, b, state, slots, lens, offsets)
+    _require(packed.dtype == torch.bfloat16, "packed must be bf16")
+    _require(state.dtype in _STATE_CODES, "state must be float32 or float16")
+    _require(state.shape[1:] == (value_heads, head_k, head_v), "state must be [S, HV, K, V]")
+    if offsets is None:
+        n, length, c = packed.shape
+        out_shape = (n, length, value_heads, head_v)
+    else:
+        _require(packed.dim() == 2, "packed layout takes [T, C]")
+        length, c = 0, packed.shape[1]
+        n = slots.shape[0]
+        out_shape = (packed.shape[0], value_heads, head_v)
+    o = torch.empty(out_shape, dtype=packed.dtype, device=packed.device)
+    sq = torch.empty(out_shape, dtype=torch.float32, device=packed.device) if with_sq else None
+    scale = head_k ** -0.5 if scale is None else scale
+    rc = lib().hsg_gdn_chunk_prefill(
+        _ptr(packed), c, 0, key_dim, 2 * key_dim, _ptr(a), _ptr(b), value_heads, _ptr(A_log), _ptr(dt_bias),
+        _ptr(state), _STATE_CODES[state.dtype], state.shape[0], _ptr(slots), _ptr(lens), _ptr(offsets), n,
+        length, heads, value_heads, head_k, head_v, scale, _ptr(o), _ptr(sq), _stream(packed.device))
+    check(rc, "hsg_gdn_chunk_prefill")
+    return o, sq
+
+
 def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens, scale, window,
                       write_ring, block_m=16, block_n=32, num_warps=4, num_stages=1):
     """Replaces fused_kernels.py:358-376. q [N, Hkv, G*Lb, D] and new_k [N, Hkv, Lb, D]; value [N, Lb, Hkv*D]

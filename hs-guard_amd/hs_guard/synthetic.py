@@ -54,6 +54,39 @@ def gdn_step_inputs(slots=16, heads=16, head_dim=128, steps=64, seed=0, state_dt
     }
 
 
+def chunk_prefill_inputs(rows=16, lengths=(512, 2048, 8000), heads=16, head_dim=128, seed=0, random_state=False):
+    """Config 4: ``rows`` rows whose lengths cycle through ``lengths`` (16 rows: 6 x 512, 5 x 2048, 5 x 8000 =
+    53,312 tokens), packed back to back; H = HV = heads, K = V = head_dim.
+
+    Draw order: state0 [rows+1, H, K, V] (zeros, or N(0, 0.02) with ``random_state``; the extra row is the
+    scratch slot, zeroed), then over all T tokens q [T, H, K], k [T, H, K] (bf16 N(0,1), L2-normalised per
+    head, rounded to bf16), v [T, H, V] bf16 N(0,1), a [T, H], b [T, H] bf16 N(0,1). A_log = dt_bias = 0.
+    Returns dict with state0, packed [T, 3*H*K], a/b [T, H], lens, offsets, A_log, dt_bias.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    H, K = heads, head_dim
+    lens = torch.tensor([lengths[i % len(lengths)] for i in range(rows)], dtype=torch.long)
+    offsets = torch.cumsum(lens, 0) - lens
+    T = int(lens.sum())
+    if random_state:
+        state0 = torch.randn(rows + 1, H, K, K, generator=gen) * 0.02
+    else:
+        state0 = torch.zeros(rows + 1, H, K, K)
+    state0[rows] = 0
+    q = _l2_bf16(_bf16_randn(gen, T, H, K))
+    k = _l2_bf16(_bf16_randn(gen, T, H, K))
+    v = _bf16_randn(gen, T, H, K)
+    a = _bf16_randn(gen, T, H)
+    b = _bf16_randn(gen, T, H)
+    return {
+        "state0": state0,
+        "packed": torch.cat([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], -1).contiguous(),
+        "a": a, "b": b, "lens": lens, "offsets": offsets,
+        "A_log": torch.zeros(H, dtype=BF16), "dt_bias": torch.zeros(H, dtype=BF16),
+        "heads": H, "head_dim": K,
+    }
+
+
 def ring_decode_inputs(rows=64, hq=16, hkv=4, head_dim=256, window=512, seed=0, pool_rows=None):
     """Config 2: ``rows`` slots x 1 new token, GQA hq/hkv, ring [pool_rows, hkv, window+1, D].
 

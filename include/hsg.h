@@ -75,6 +75,20 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
                             const void* norm_w, float eps, void* out, void* stream);
 
 /*
+ * Chunked gated-delta-rule prefill: the same recurrence and contract as hsg_gdn_slot_step, evaluated
+ * 64 tokens at a time in the WY/UT chunk form on MFMA, for rows of any length (initial contexts).
+ * Replaces FLA's chunk_gated_delta_rule with initial_state = rec[slots] and output_final_state
+ * (call sites src/hs_guard/runtime.py:80-89, src/hs_guard/engine/bucketed_engine.py:109-111).
+ * Arguments as hsg_gdn_slot_step; lens[n] is unbounded. o must not alias qkv.
+ */
+int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
+                          const void* a, const void* b, int64_t ab_stride, const void* A_log,
+                          const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
+                          const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
+                          int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
+                          float* sq, void* stream);
+
+/*
  * Window-W GQA attention of this tick's queries over the slot's ring plus this tick's new keys.
  * Replaces ring_attention_v8 (src/hs_guard/engine/fused_kernels.py:358-376; kernel :288-356),
  * ring_attention (src/hs_guard/engine/ring_attention_kernel.py:91-105) and the Lb > 1 ring scatter

@@ -125,24 +125,28 @@ def gdn_chunk(q, k, v, g, beta, S0, chunk=64, scale=None, normalize=True):
     if normalize:
         q, k = l2norm(q), l2norm(k)
     q = q * scale
-    S = np.array(S0, dtype=np.float64, copy=True)
+    S = np.array(S0, dtype=np.float64, copy=True)          # [H, K, V]
     out = np.zeros(v.shape)
     for c0 in range(0, T, chunk):
         c1 = min(T, c0 + chunk)
         C = c1 - c0
-        for h in range(H):
-            Q, Kc, Vc = q[c0:c1, h], k[c0:c1, h], v[c0:c1, h]
-            G = np.cumsum(g[c0:c1, h])
-            bt = beta[c0:c1, h]
-            diff = G[:, None] - G[None, :]
-            lower = np.tril(np.ones((C, C), dtype=bool), -1)
-            A = np.where(lower, bt[:, None] * (Kc @ Kc.T) * np.exp(np.where(lower, diff, 0.0)), 0.0)
-            Tm = np.linalg.inv(np.eye(C) + A)
-            Wm = Tm @ ((bt * np.exp(G))[:, None] * Kc)
-            Um = Tm @ (bt[:, None] * Vc)
-            Vn = Um - Wm @ S[h]
-            causal = np.tril(np.ones((C, C), dtype=bool))
-            P = np.where(causal, (Q @ Kc.T) * np.exp(np.where(causal, diff, 0.0)), 0.0)
-            out[c0:c1, h] = (Q * np.exp(G)[:, None]) @ S[h] + P @ Vn
-            S[h] = np.exp(G[-1]) * S[h] + (Kc * np.exp(G[-1] - G)[:, None]).T @ Vn
+        Q = np.ascontiguousarray(q[c0:c1].transpose(1, 0, 2))      # [H, C, K]
+        Kc = np.ascontiguousarray(k[c0:c1].transpose(1, 0, 2))
+        Vc = np.ascontiguousarray(v[c0:c1].transpose(1, 0, 2))     # [H, C, V]
+        G = np.cumsum(g[c0:c1].T, axis=1)                   # [H, C]
+        bt = beta[c0:c1].T                                  # [H, C]
+        diff = G[:, :, None] - G[:, None, :]                # [H, C, C]
+        lower = np.tril(np.ones((C, C), dtype=bool), -1)
+        causal = np.tril(np.ones((C, C), dtype=bool))
+        KT = np.ascontiguousarray(Kc.transpose(0, 2, 1))
+        KK = Kc @ KT
+        A = np.where(lower, bt[:, :, None] * KK * np.exp(np.where(lower, diff, 0.0)), 0.0)
+        Tm = np.linalg.inv(np.eye(C) + A)
+        Wm = Tm @ ((bt * np.exp(G))[:, :, None] * Kc)
+        Um = Tm @ (bt[:, :, None] * Vc)
+        Vn = Um - Wm @ S
+        P = np.where(causal, (Q @ KT) * np.exp(np.where(causal, diff, 0.0)), 0.0)
+        out[c0:c1] = ((Q * np.exp(G)[:, :, None]) @ S + P @ Vn).transpose(1, 0, 2)
+        Kd = np.ascontiguousarray((Kc * np.exp(G[:, -1:] - G)[:, :, None]).transpose(0, 2, 1))
+        S = np.exp(G[:, -1])[:, None, None] * S + Kd @ Vn
     return out, S
