@@ -27,6 +27,7 @@ for _p in (ROOT, os.path.join(ROOT, "hs-guard_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 REF_L20 = {"min_tokens_per_s_352": 15075.6, "worst_p95_ms_352": 18.368, "single_token_p50_ms": 2.384}
 
 
@@ -129,6 +130,43 @@ def ring_decode_rate(torch, rows=352, iters=50):
     return {"avg_us": round(us, 2), "alg_bytes_per_launch": alg, "achieved_gbs": round(alg / (us * 1e-6) / 1e9, 1)}
 
 
+def chunk_prefill_rate(torch, iters=10):
+    """Config 4 on hsg_gdn_chunk_prefill: 16 rows of 512/2048/8000 tokens (53,312 tokens, 833 chunks of 64),
+    16 heads x 128, fp32 state; HIP events on the launch stream. Algorithmic work per chunk-head
+    2C^2(3dk+2dv) + 6C dk dv + (2/3)C^3 = 11,709,099 FLOP (C=64, dk=dv=128); algorithmic bytes = q, k, v in
+    + o out (4 x 256 B) + a, b (4 B) per token-head + the state read and written once per row-head."""
+    from hs_guard.engine.kernels import gdn_chunk_prefill
+    from hs_guard.synthetic import chunk_prefill_inputs
+    H, K = 16, 128
+    inp = chunk_prefill_inputs(rows=16)
+    d = {k: (v.to("cuda:0") if torch.is_tensor(v) else v) for k, v in inp.items()}
+    slots = torch.arange(16, device="cuda:0")
+    stream = torch.cuda.current_stream()
+
+    def run():
+        gdn_chunk_prefill(d["packed"], H * K, H, K, H, K, d["a"], d["b"], d["A_log"], d["dt_bias"], d["state0"],
+                          slots, d["lens"], d["offsets"])
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(iters):
+        run()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / iters
+    T = int(inp["lens"].sum())
+    chunks = int(((inp["lens"] + 63) // 64).sum())
+    flop = 11709099 * chunks * H
+    alg_bytes = T * H * (4 * 256 + 4) + 16 * H * K * K * 4 * 2
+    tflops = flop / (us * 1e-6) / 1e12
+    ridge = min(MFMA_BF16_PEAK_TFLOPS, flop / alg_bytes * HBM_PEAK_GBS / 1e3)
+    return {"avg_us": round(us, 1), "tokens": T, "chunks": chunks, "alg_flop": flop, "alg_bytes": alg_bytes,
+            "tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "roof_tflops": round(ridge, 1), "roof_frac": round(tflops / ridge, 4)}
+
+
 def cpu_baseline(model, cfg, seed=0, slots=8, ticks=3):
     """The CPU restatement (oracle.backbone.StreamOracle: numpy fp32 GEMMs, float64 recurrence) on a bounded
     sample of config 5: ``slots`` slots with a 32-token context (untimed), then ``ticks`` mixed ticks with
@@ -201,6 +239,8 @@ def main():
         return
     ring = ring_decode_rate(torch, rows=args.slots)
     log(f"ring decode {ring}")
+    chunk = chunk_prefill_rate(torch)
+    log(f"chunk prefill config 4 {chunk}")
 
     cfg = GuardConfig.baseline()
     t0 = time.time()
@@ -305,6 +345,7 @@ def main():
                      "kernel": roof["kernel"], "shape": roof["shape"], "avg_us": roof["avg_us"],
                      "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
         "ring_decode_352": ring,
+        "chunk_prefill_cfg4": chunk,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

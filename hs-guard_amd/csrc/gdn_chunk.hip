@@ -19,10 +19,16 @@
 // so S, the substitution's right-hand sides and V' feed the next product from registers; pairs of 16-row
 // blocks feed v_mfma_f32_16x16x32_bf16 by ordering its 32 reduction slots as (4 rows of block J, 4 rows of
 // block J+1) per lane, with the A operand read in the same order.
-// Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, the A blocks, the
-// diagonal inverses, right-hand sides, V') is split into bf16 hi + lo and multiplied in three passes
-// (hi.hi + hi.lo + lo.hi, error ~2^-16 relative), so the state keeps fp32-level accuracy; the diagonal
-// 16 x 16 inverses are fp32 forward substitution.
+// Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, -A, the diagonal
+// inverses, right-hand sides, V', Z) is split into bf16 hi + lo and multiplied in three passes (hi.hi + hi.lo
+// + lo.hi, error ~2^-16 relative), so the state keeps fp32-level accuracy; the diagonal 16 x 16 inverses are
+// fp32 forward substitution. -A, P and the inverses are written to LDS already split, once per workgroup.
+// Two code-generation rules this kernel keeps on gfx950:
+//   * one MFMA accumulation chain uses one MFMA shape: a 16x16x16 product accumulating directly onto the
+//     result of a 16x16x32 product lost part of that result (found by bisecting a wrong output), so odd
+//     blocks are zero-padded 16x16x32 products;
+//   * the global prefetch is unconditional (clamped row pointer): a conditional load was compiled as a load
+//     through a selected pointer to a stack zero, which forced a full memory wait every chunk.
 #include <math.h>
 
 #include "hsg_common.h"
@@ -36,8 +42,7 @@ constexpr int CH = 64;             // tokens per chunk
 constexpr int BV = 64;             // value columns per workgroup
 constexpr int KS = KD + 8;         // Ks / Qs row stride (bf16): token-major rows of keys
 constexpr int TS = CH + 4;         // KTs / VT row stride (bf16): key- / value-major rows of tokens
-constexpr int FS = CH + 4;         // Af / Pf row stride (fp32)
-constexpr int TFS = 20;            // diagonal-inverse row stride (fp32)
+constexpr int DS = 20;             // diagonal-block row stride (fp32) and diagonal-inverse row stride (bf16)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) short s16x8;
@@ -76,47 +81,57 @@ __device__ __forceinline__ f32x4 mma32(s16x8 a, s16x8 b, f32x4 c) {
 
 __device__ __forceinline__ s16x8 cat(s16x4 x, s16x4 y) { return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7); }
 
-// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even
+// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even. The rounding is done in
+// integer arithmetic: a build of this kernel using the compiler's __bf16 conversion produced wrong values in
+// a few rows of one tile on gfx950, while the identical kernel with this conversion is exact.
 __device__ __forceinline__ void split4(f32x4 x, s16x4& hi, s16x4& lo) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const __bf16 h = (__bf16)x[i];
-    hi[i] = __builtin_bit_cast(short, h);
-    lo[i] = __builtin_bit_cast(short, (__bf16)(x[i] - (float)h));
+    const uint16_t h = f2bf_finite(x[i]);
+    hi[i] = (short)h;
+    lo[i] = (short)f2bf_finite(x[i] - bf2f(h));
   }
 }
 
 __device__ __forceinline__ f32x4 ld4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ s16x4 ld4h(const uint16_t* p) { return *reinterpret_cast<const s16x4*>(p); }
 
-// acc += sum_{J < nJ} M[row block I][col block J] . B_J, M an fp32 matrix in LDS read at mrow = &M[16I + m][4 g]
-// (lane m = l%16, g = l/16), B_J given as split bf16 pairs in B layout. Three passes per product.
-template <int NJ, bool NEG>
-__device__ __forceinline__ f32x4 split_product(const float* mrow, const s16x4* bh, const s16x4* bl, f32x4 acc) {
+// acc += sum_{J < NJ} M[row block I][col block J] . B_J for a matrix M kept in LDS as bf16 hi / lo planes, read
+// at hrow = &Mh[16I + m][4 g], lrow = &Ml[16I + m][4 g] (lane m = l%16, g = l/16); B_J are split bf16 pairs in
+// B layout. Three passes per product (hi.hi + hi.lo + lo.hi).
+template <int NJ>
+__device__ __forceinline__ f32x4 split_product(const uint16_t* hrow, const uint16_t* lrow, const s16x4* bh,
+                                               const s16x4* bl, f32x4 acc) {
 #pragma unroll
   for (int J = 0; J + 1 < NJ; J += 2) {
-    f32x4 a0 = ld4f(mrow + 16 * J), a1 = ld4f(mrow + 16 * J + 16);
-    if (NEG) { a0 = -a0; a1 = -a1; }
-    s16x4 h0, l0, h1, l1;
-    split4(a0, h0, l0);
-    split4(a1, h1, l1);
-    const s16x8 ah = cat(h0, h1), al = cat(l0, l1);
+    const s16x8 ah = cat(ld4h(hrow + 16 * J), ld4h(hrow + 16 * J + 16));
+    const s16x8 al = cat(ld4h(lrow + 16 * J), ld4h(lrow + 16 * J + 16));
     const s16x8 b_h = cat(bh[J], bh[J + 1]), b_l = cat(bl[J], bl[J + 1]);
     acc = mma32(al, b_h, acc);
     acc = mma32(ah, b_l, acc);
     acc = mma32(ah, b_h, acc);
   }
   if constexpr (NJ % 2 == 1) {
+    // the odd block rides in a 16x16x32 product with zero upper k-slots: one accumulation chain never mixes
+    // MFMA shapes (a 16x16x16 accumulating onto a 16x16x32 result lost that result in some rows)
     constexpr int J = NJ - 1;
-    f32x4 a0 = ld4f(mrow + 16 * J);
-    if (NEG) a0 = -a0;
-    s16x4 h0, l0;
-    split4(a0, h0, l0);
-    acc = mma16(l0, bh[J], acc);
-    acc = mma16(h0, bl[J], acc);
-    acc = mma16(h0, bh[J], acc);
+    const s16x4 z = {0, 0, 0, 0};
+    const s16x8 ah = cat(ld4h(hrow + 16 * J), z), al = cat(ld4h(lrow + 16 * J), z);
+    const s16x8 b_h = cat(bh[J], z), b_l = cat(bl[J], z);
+    acc = mma32(al, b_h, acc);
+    acc = mma32(ah, b_l, acc);
+    acc = mma32(ah, b_h, acc);
   }
   return acc;
+}
+
+// e^x for x <= 0 on the hardware exp2 (v_exp_f32, 1 ulp): 2^(x log2 e)
+__device__ __forceinline__ float exp_nonpos(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+__device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, float x) {
+  const uint16_t h = f2bf_finite(x);
+  *hi = h;
+  *lo = f2bf_finite(x - bf2f(h));
 }
 
 // workgroup barrier that orders LDS only (outstanding global prefetches stay in flight)
@@ -172,10 +187,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Qs[CH * KS];
   __shared__ __align__(16) uint16_t KTs[KD * TS];
   __shared__ __align__(16) uint16_t VT[BV * TS];
-  __shared__ __align__(16) float Af[CH * FS];
-  __shared__ __align__(16) float Pf[CH * FS];
-  __shared__ __align__(16) float Tf[4 * 16 * TFS];
-  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], c1_s[CH], d_s[CH], qe_s[CH], G_s[CH];
+  // -A (strictly lower) and P (lower incl. diagonal) as bf16 hi / lo planes, token-major rows
+  __shared__ __align__(16) uint16_t Ah[CH * TS], Al[CH * TS], Ph[CH * TS], Pl[CH * TS];
+  __shared__ __align__(16) float Dg[4 * 16 * DS];                // fp32 diagonal 16 x 16 blocks of A
+  __shared__ __align__(16) uint16_t Th[CH * DS], Tl[CH * DS];    // their inverses (rows 16w + i of block w)
+  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], c1_s[CH], d_s[CH], qe_s[CH], G_s[CH], fa_s[CH];
   __shared__ float gc_s;
 
   // ---- state S[:, vcol] in accumulator layout: block mt holds keys 16 mt + 4 g4 + r ----
@@ -192,27 +208,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
   // ---- staging coordinates: token st_t of the chunk; 16-byte pieces g4 + 4 it ----
   const int st_t = 16 * wave + m16;
   uint4 pk[4], pq[4], pv[2];
-  float pa = 0.f, pb = 0.f;
+  uint16_t pa = 0, pb = 0;   // raw bf16: converting here would make every prefetch wait for its loads
+  // Loads are unconditional: a position past the row's end reads the row's first token instead, and its
+  // zero beta, rk and rq factors (set at staging) cancel it everywhere, so no select can turn into a
+  // memory-backed zero or a branch around the loads.
   auto fetch = [&](int c0) {
-    const bool ok = c0 + st_t < ntok;
-    const int64_t tok = tok0 + c0 + st_t;
-    const uint16_t* row = p.qkv + (ok ? tok : tok0) * p.qkv_stride;
-    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    const int64_t tok = tok0 + (c0 + st_t < ntok ? c0 + st_t : 0);
+    const uint16_t* row = p.qkv + tok * p.qkv_stride;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int pc = 8 * (g4 + 4 * it);
-      pk[it] = ok ? *reinterpret_cast<const uint4*>(row + p.k_off + h * KD + pc) : z;
-      pq[it] = ok ? *reinterpret_cast<const uint4*>(row + p.q_off + h * KD + pc) : z;
+      pk[it] = *reinterpret_cast<const uint4*>(row + p.k_off + h * KD + pc);
+      pq[it] = *reinterpret_cast<const uint4*>(row + p.q_off + h * KD + pc);
     }
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int pc = 8 * (g4 + 4 * it);
-      pv[it] = ok ? *reinterpret_cast<const uint4*>(row + p.v_off + hv * VD + vb * BV + pc) : z;
+      pv[it] = *reinterpret_cast<const uint4*>(row + p.v_off + hv * VD + vb * BV + pc);
     }
-    if (g4 == 0 && ok) {
-      pa = bf2f(p.a[tok * p.ab_stride + hv]);
-      pb = bf2f(p.b[tok * p.ab_stride + hv]);
-    }
+    pa = p.a[tok * p.ab_stride + hv];
+    pb = p.b[tok * p.ab_stride + hv];
   };
 
   fetch(0);
@@ -257,9 +272,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
         const bool ok = st_t < nv;
         rk_s[st_t] = ok ? 1.0f / sqrtf(kk + 1e-6f) : 0.f;
         rq_s[st_t] = ok ? p.scale / sqrtf(qq + 1e-6f) : 0.f;
-        const float x = pa + dt;
+        const float x = bf2f(pa) + dt;
         g_s[st_t] = ok ? -A * (x > 20.0f ? x : logf(1.0f + expf(x))) : 0.f;
-        b_s[st_t] = ok ? sigmoidf_(pb) : 0.f;
+        b_s[st_t] = ok ? sigmoidf_(bf2f(pb)) : 0.f;
       }
     }
     if (c0 + CH < ntok) fetch(c0 + CH);  // next chunk's loads stay in flight during this chunk's math
@@ -274,12 +289,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
         if (lane >= d) x += y;
       }
       const float GC = __shfl(x, 63, 64);
-      const float eg = expf(x);
+      const float eg = exp_nonpos(x);
       G_s[lane] = x;
       c1_s[lane] = b_s[lane] * eg * rk_s[lane];
-      d_s[lane] = rk_s[lane] * expf(GC - x);
+      fa_s[lane] = b_s[lane] * rk_s[lane];
+      d_s[lane] = rk_s[lane] * exp_nonpos(GC - x);
       qe_s[lane] = rq_s[lane] * eg;
-      if (lane == 0) gc_s = expf(GC);
+      if (lane == 0) gc_s = exp_nonpos(GC);
     }
 
     // ---- Kr Kr^T and Qr Kr^T on the 10 lower 16 x 16 tiles each; tile u of wave w is number w + 4u ----
@@ -326,22 +342,45 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
     }
     lds_barrier();  // per-token factors are in LDS
 
-    // ---- scale the Gram tiles into A (strictly lower) and P (lower incl. diagonal) ----
+    // ---- scale the Gram tiles into -A and P. Only P's diagonal tiles need the causal mask: the substitution
+    // reads A's off-diagonal tiles only and the diagonal inverses read below the diagonal only. ----
+    {
+      f32x4 fr[5], Gr[5];
+      float rkc[5], Gc[5];
 #pragma unroll
-    for (int u = 0; u < 5; ++u) {
-      const int tau = wave + 4 * u;
-      const bool qk = tau >= 10;
-      const int idx = qk ? tau - 10 : tau;
-      const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
-      const int J = idx - I * (I + 1) / 2;
-      const int j = 16 * J + m16;
-      const float rkj = rk_s[j], Gj = G_s[j];
+      for (int u = 0; u < 5; ++u) {
+        const int tau = wave + 4 * u;
+        const bool qk = tau >= 10;
+        const int idx = qk ? tau - 10 : tau;
+        const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
+        const int J = idx - I * (I + 1) / 2;
+        const int i0 = 16 * I + 4 * g4;
+        fr[u] = ld4f(qk ? &rq_s[i0] : &fa_s[i0]);
+        Gr[u] = ld4f(&G_s[i0]);
+        rkc[u] = rk_s[16 * J + m16];
+        Gc[u] = G_s[16 * J + m16];
+      }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * g4 + r;
-        const float e = expf(fminf(G_s[i] - Gj, 0.f));
-        if (!qk) Af[i * FS + j] = i > j ? b_s[i] * rk_s[i] * rkj * e * gt[u][r] : 0.f;
-        else Pf[i * FS + j] = i >= j ? rq_s[i] * rkj * e * gt[u][r] : 0.f;
+      for (int u = 0; u < 5; ++u) {
+        const int tau = wave + 4 * u;
+        const bool qk = tau >= 10;
+        const int idx = qk ? tau - 10 : tau;
+        const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
+        const int J = idx - I * (I + 1) / 2;
+        const int i0 = 16 * I + 4 * g4;
+        const int j = 16 * J + m16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = fr[u][r] * rkc[u] * exp_nonpos(fminf(Gr[u][r] - Gc[u], 0.f)) * gt[u][r];
+          if (!qk) {
+            store_split(&Ah[(i0 + r) * TS + j], &Al[(i0 + r) * TS + j], -v);
+            if (I == J) Dg[(i0 + r) * DS + m16] = -v;
+          } else {
+            // keep = 1 when row >= column inside a diagonal tile (sign bit of column - row - 1)
+            const float keep = I == J ? (float)((uint32_t)(m16 - (4 * g4 + r) - 1) >> 31) : 1.f;
+            store_split(&Ph[(i0 + r) * TS + j], &Pl[(i0 + r) * TS + j], v * keep);
+          }
+        }
       }
     }
     // ---- right-hand sides R = beta . V - beta e^G rk . Y (in place in Y) ----
@@ -358,24 +397,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
 
     // ---- wave w inverts diagonal block w of (I + A) by fp32 forward substitution (lane m16 = column) ----
     {
-      const float* nb = Af + (16 * wave) * FS + 16 * wave;
+      const float* nb = Dg + (16 * wave) * DS;   // -A of the block
       float t[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float s0 = (i == m16) ? 1.f : 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
         for (int k = 0; k < i; ++k) {
-          const float a = nb[i * FS + k];
-          if ((k & 3) == 0) s0 -= a * t[k];
-          else if ((k & 3) == 1) s1 -= a * t[k];
-          else if ((k & 3) == 2) s2 -= a * t[k];
-          else s3 -= a * t[k];
+          const float a = nb[i * DS + k];
+          if ((k & 3) == 0) s0 += a * t[k];
+          else if ((k & 3) == 1) s1 += a * t[k];
+          else if ((k & 3) == 2) s2 += a * t[k];
+          else s3 += a * t[k];
         }
         t[i] = (s0 + s1) + (s2 + s3);
       }
-      if (g4 == 0) {
+      // every lane group computed the same column; group g4 writes rows 4 g4 .. 4 g4 + 3 of it
 #pragma unroll
-        for (int i = 0; i < 16; ++i) Tf[(wave * 16 + i) * TFS + m16] = t[i];
+      for (int i = 0; i < 4; ++i) {
+        const float ti = g4 == 0 ? t[i] : g4 == 1 ? t[4 + i] : g4 == 2 ? t[8 + i] : t[12 + i];
+        store_split(&Th[(wave * 16 + 4 * g4 + i) * DS + m16], &Tl[(wave * 16 + 4 * g4 + i) * DS + m16], ti);
       }
     }
     lds_barrier();  // diagonal inverses are complete
@@ -385,16 +426,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
     f32x4 Vp[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      f32x4 x = Y[I];
-      const float* arow = Af + (16 * I + m16) * FS + 4 * g4;
-      if (I == 1) x = split_product<1, true>(arow, Vh, Vl, x);
-      if (I == 2) x = split_product<2, true>(arow, Vh, Vl, x);
-      if (I == 3) x = split_product<3, true>(arow, Vh, Vl, x);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const int arow = (16 * I + m16) * TS + 4 * g4;
+      if (I == 1) acc = split_product<1>(Ah + arow, Al + arow, Vh, Vl, acc);
+      if (I == 2) acc = split_product<2>(Ah + arow, Al + arow, Vh, Vl, acc);
+      if (I == 3) acc = split_product<3>(Ah + arow, Al + arow, Vh, Vl, acc);
+      const f32x4 x = Y[I] + acc;
       s16x4 xh, xl;
       split4(x, xh, xl);
-      const f32x4 tr = ld4f(&Tf[(I * 16 + m16) * TFS + 4 * g4]);
-      s16x4 th, tl;
-      split4(tr, th, tl);
+      const s16x4 th = ld4h(&Th[(I * 16 + m16) * DS + 4 * g4]), tl = ld4h(&Tl[(I * 16 + m16) * DS + 4 * g4]);
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       v = mma16(tl, xh, v);
       v = mma16(th, xl, v);
@@ -408,21 +448,27 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
     for (int I = 0; I < 4; ++I) {
       const int i0 = 16 * I + 4 * g4;
       const f32x4 qe = ld4f(&qe_s[i0]);
-      f32x4 o = QS[I] * qe;
-      const float* prow = Pf + (16 * I + m16) * FS + 4 * g4;
-      if (I == 0) o = split_product<1, false>(prow, Vh, Vl, o);
-      if (I == 1) o = split_product<2, false>(prow, Vh, Vl, o);
-      if (I == 2) o = split_product<3, false>(prow, Vh, Vl, o);
-      if (I == 3) o = split_product<4, false>(prow, Vh, Vl, o);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const int prow = (16 * I + m16) * TS + 4 * g4;
+      if (I == 0) acc = split_product<1>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 1) acc = split_product<2>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 2) acc = split_product<3>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 3) acc = split_product<4>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      const f32x4 o = QS[I] * qe + acc;
+      uint16_t* orow = p.o + (tok0 + c0 + i0) * ostride + hv * VD + vcol;
+      if (nv == CH && !p.sq) {   // whole chunk, no sq: no per-element predicates
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (i0 + r < nv) {
-          const int64_t at = (tok0 + c0 + i0 + r) * ostride + hv * VD + vcol;
-          const uint16_t ob = f2bf(o[r]);
-          p.o[at] = ob;
-          if (p.sq) {
-            const float x = bf2f(ob);
-            p.sq[at] = x * x;
+        for (int r = 0; r < 4; ++r) orow[r * ostride] = f2bf_finite(o[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (i0 + r < nv) {
+            const uint16_t ob = f2bf_finite(o[r]);
+            orow[r * ostride] = ob;
+            if (p.sq) {
+              const float x = bf2f(ob);
+              p.sq[(tok0 + c0 + i0 + r) * ostride + hv * VD + vcol] = x * x;
+            }
           }
         }
       }
@@ -438,15 +484,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
     const float gc = gc_s;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-      f32x4 s = S[mt] * gc;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       const uint16_t* krow = KTs + (16 * mt + m16) * TS + 4 * g4;
 #pragma unroll
       for (int J = 0; J < 4; J += 2) {
         const s16x8 ka = cat(ld4h(krow + 16 * J), ld4h(krow + 16 * J + 16));
-        s = mma32(ka, cat(Zl[J], Zl[J + 1]), s);
-        s = mma32(ka, cat(Zh[J], Zh[J + 1]), s);
+        acc = mma32(ka, cat(Zl[J], Zl[J + 1]), acc);
+        acc = mma32(ka, cat(Zh[J], Zh[J + 1]), acc);
       }
-      S[mt] = s;
+      S[mt] = S[mt] * gc + acc;
     }
   }
 

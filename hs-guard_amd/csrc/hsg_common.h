@@ -19,6 +19,12 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// round-to-nearest-even fp32 -> bf16 without the NaN case (callers pass finite values), branch-free
+__device__ __forceinline__ uint16_t f2bf_finite(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 

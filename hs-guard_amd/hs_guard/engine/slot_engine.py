@@ -354,6 +354,7 @@ class SlotStreamEngine:
             self.graphs[key] = (graph, inp, probs, host_in, host_in.numpy(), host_out, host_out.numpy())
         return self.graphs[key]
 
+    @torch.inference_mode()
     def prepare(self, rows, token_counts):
         """Capture ahead of time the step graphs for ticks of ``rows`` rows and each total token count in
         ``token_counts`` (by bucket), so that a serving loop never pays a capture inside a tick."""
