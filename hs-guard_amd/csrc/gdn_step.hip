@@ -12,8 +12,9 @@
 // 128-byte row segment, so every load instruction reads 8 full 128-byte lines. The k.S and q.S
 // reductions over the 128 key rows are in-lane (16 rows) plus a 3-step butterfly over rg (lane xor 8,
 // 16, 32). exp(g) is folded in as (exp(g) S)^T k = exp(g) (S^T k), and the decay and rank-1 update share
-// one pass over the registers. The state streams in and out with nontemporal accesses (it is touched once
-// per tick, so it should not displace cached weights and activations).
+// one pass over the registers. The state is read with ordinary loads and written back with nontemporal
+// stores (it is touched once per tick, so the write should not displace cached weights and activations);
+// measured on MI355X this pairing streams faster than nontemporal loads (6.0 vs 5.4 TB/s at 352 x 16).
 // Token inputs (q, k of the key head; v, z of the value head; a, b) are staged in LDS 16 tokens at a time
 // by one cooperative burst of 16-byte loads, so a 64-token tick pays the global-memory latency 4 times
 // instead of 64 and the sequential token loop only touches LDS.
@@ -62,7 +63,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 template <>
 struct StateIO<float> {
   static __device__ __forceinline__ void load(const float* p, float* v) {
-    const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(p);
     v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
   }
   static __device__ __forceinline__ void store(float* p, const float* v) {
@@ -74,7 +75,7 @@ struct StateIO<float> {
 template <>
 struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
   static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
-    const u32x2_t w = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(p);
     v[0] = h2f((uint16_t)(w[0] & 0xffffu)); v[1] = h2f((uint16_t)(w[0] >> 16));
     v[2] = h2f((uint16_t)(w[1] & 0xffffu)); v[3] = h2f((uint16_t)(w[1] >> 16));
   }
