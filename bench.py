@@ -106,28 +106,46 @@ def measured_traffic(rows, state_dtype):
 
 
 def ring_decode_rate(torch, rows=352, iters=50):
-    """Achieved algorithmic GB/s of hsg_ring_attention at the 352 x 1-token decode shape with full rings."""
+    """Split-K ring attention (hsg_ring_decode, three launches) at the 352 x 1-token decode shape, HIP events
+    on the launch stream: config 2's ring fills (uniform in [1, 512]) scaled to 352 rows, and full rings (the
+    steady state of a live session). Algorithmic bytes: the visible keys and values (n 256 dims x 2 B x 2),
+    their positions (8 B each), q, gate and out (3 x 16 heads x 512 B), the new key and value read and
+    written to the ring (4 kv heads x 512 B x 4)."""
     from hs_guard.engine.kernels import ring_attention_v8
     from hs_guard.synthetic import ring_decode_inputs
-    r = ring_decode_inputs(rows=rows)
-    d = {k: v.to("cuda:0") for k, v in r.items() if torch.is_tensor(v)}
+    out = {}
+    for name in ("config2_fills", "full_rings"):
+        r = ring_decode_inputs(rows=rows)
+        if name == "full_rings":
+            W = 512
+            r["fill"] = torch.full_like(r["fill"], W)
+            rp = torch.full_like(r["ring_pos"], -1)
+            for i in range(rows):
+                st = int(r["starts"][i])
+                cols = torch.arange(st - W, st)
+                rp[i, cols % W] = cols
+            r["ring_pos"] = rp
+        d = {k: v.to("cuda:0") for k, v in r.items() if torch.is_tensor(v)}
+        stream = torch.cuda.current_stream()
 
-    def run():
-        ring_attention_v8(d["q"], d["ring_k"], d["ring_v"], d["new_k"], d["value"], d["gate"], d["ring_pos"],
-                          d["slots"], d["starts"], d["lens"], 1 / 16, 512, False)
-    for _ in range(5):
-        run()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(iters):
-        run()
-    t1.record()
-    torch.cuda.synchronize()
-    us = t0.elapsed_time(t1) * 1e3 / iters
-    valid = sum(min(int(f), 511) for f in r["fill"])
-    alg = valid * 4 * 256 * 2 * 2 + rows * 16 * 256 * 2 * 3 + rows * 4 * 256 * 2 * 2 + valid * 8
-    return {"avg_us": round(us, 2), "alg_bytes_per_launch": alg, "achieved_gbs": round(alg / (us * 1e-6) / 1e9, 1)}
+        def run():
+            ring_attention_v8(d["q"], d["ring_k"], d["ring_v"], d["new_k"], d["value"], d["gate"], d["ring_pos"],
+                              d["slots"], d["starts"], d["lens"], 1 / 16, 512, False)
+        for _ in range(5):
+            run()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(iters):
+            run()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / iters
+        valid = sum(min(int(f), 511) for f in r["fill"])
+        alg = valid * 4 * 256 * 2 * 2 + rows * 16 * 256 * 2 * 3 + rows * 4 * 256 * 2 * 2 + valid * 8
+        out[name] = {"avg_us": round(us, 2), "alg_bytes_per_launch": alg,
+                     "achieved_gbs": round(alg / (us * 1e-6) / 1e9, 1)}
+    return out
 
 
 def chunk_prefill_rate(torch, iters=10):

@@ -48,6 +48,7 @@ struct RingParams {
   int lb, hkv, G;
   float scale;
   int write_ring;
+  int min_len;
   uint16_t* out; int64_t o_sn, o_sl, o_sh, o_sg;
 };
 
@@ -73,6 +74,7 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
   const bool padded = p.offsets == nullptr;
   if (slot < 0 || slot >= p.ring_rows || len < 0 || len > LB_MAX) len = 0;  // > LB_MAX: rejected row
   if (padded && len > p.lb) len = p.lb;
+  if (!padded && len < p.min_len) return;              // left to another kernel (single-step rows: split-K)
   const int steps = padded ? p.lb : (int)len;          // output steps written for this row
   const int64_t base_tok = padded ? 0 : p.offsets[n];
   const int64_t q_row = padded ? n * p.q_sn : base_tok * p.q_sl;
@@ -295,8 +297,8 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
                                   int64_t g_off, const int64_t* ring_pos, const int64_t* slots,
                                   const int64_t* starts, const int64_t* lens, const int64_t* offsets,
                                   int32_t n_rows, int32_t lb, int32_t hkv, int32_t groups, int32_t head_dim,
-                                  float scale, int32_t write_ring, void* out, int64_t o_sn, int64_t o_sl,
-                                  int64_t o_sh, int64_t o_sg, void* stream) {
+                                  float scale, int32_t write_ring, int32_t min_len, void* out, int64_t o_sn,
+                                  int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream) {
   using namespace hsg;
   if (n_rows < 0 || lb <= 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
@@ -322,7 +324,7 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
   p.gate = static_cast<const uint16_t*>(gate);
   p.g_sn = g_sn; p.g_sl = g_sl; p.g_sh = g_sh; p.g_sg = g_sg; p.g_off = g_off;
   p.ring_pos = ring_pos; p.slots = slots; p.starts = starts; p.lens = lens; p.offsets = offsets;
-  p.lb = lb; p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring;
+  p.lb = lb; p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring; p.min_len = min_len;
   p.out = static_cast<uint16_t*>(out); p.o_sn = o_sn; p.o_sl = o_sl; p.o_sh = o_sh; p.o_sg = o_sg;
   hipLaunchKernelGGL(ring_attn_mfma_kernel, dim3((unsigned)(n_rows * hkv)), dim3(NW * 64), 0,
                      reinterpret_cast<hipStream_t>(stream), p);

@@ -1,0 +1,449 @@
+// Split-K window-W GQA ring attention for decode steps (one query position per row) on gfx950.
+//
+// Contract and numerics: those of hsg_ring_attention (src/hs_guard/engine/fused_kernels.py:288-376 and the
+// torch reference src/hs_guard/engine/ring_attention_kernel.py:7-26) for rows with lens[n] == 1: keys in
+// blocks of 32 (ring columns in order, then the step's own key), a running max m_b over the blocks,
+// probabilities p = exp(s - m_b) rounded to bf16 in the P.V product and summed unrounded, output / sum
+// rounded to bf16, times bf16(sigmoid(gate)). The running max of block b is the prefix maximum of the block
+// maxima, and the reference's rescaling chain multiplies block b's P.V and sum by exp(m_b - m_final), so the
+// key range can be split across workgroups without changing where any bf16 rounding happens:
+//   A (scores):  (row, kv head, split) -> s = scale * q.k for the split's ring blocks (masked -inf) and each
+//                block's maximum per query head, into the workspace; the last split adds the step's own key.
+//   B (values):  (row, kv head, split) -> prefix maxima from all block maxima, then for each of its blocks
+//                exp(m_b - m_final) * sum_k bf16(exp(s_k - m_b)) v_k and the matching unrounded sum.
+//   C (combine): (row, kv head) -> sum over splits, divide, gate, store; then the in-place ring write of the
+//                step's key and value (every read of this ring finished in B).
+// Blocks with no visible key are skipped in A and B (no K or V traffic). The split is over the 512 ring
+// columns: 4 splits of 4 blocks, one block per wave, so a decode step of R rows runs 16 R workgroups per
+// launch instead of R (latency hidden across workgroups, not inside one).
+#include <math.h>
+
+#include "hsg_common.h"
+
+namespace hsg {
+namespace {
+
+constexpr int D = 256;
+constexpr int KB = 32;             // keys per softmax block
+constexpr int NS = 4;              // splits of the ring columns
+constexpr int W_MAX = 512;
+constexpr int G_MAX = 16;          // query heads per kv head
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+struct DecParams {
+  const uint16_t* q; int64_t q_sn, q_sl, q_sh, q_sg;
+  uint16_t* ring_k; uint16_t* ring_v; int64_t ring_rows; int W;
+  const uint16_t* new_k; int64_t nk_sn, nk_sl, nk_sh;
+  const uint16_t* new_v; int64_t nv_sn, nv_sl, nv_sh;
+  const uint16_t* gate; int64_t g_sn, g_sl, g_sh, g_sg, g_off;
+  const int64_t* ring_pos; const int64_t* slots; const int64_t* starts; const int64_t* lens;
+  const int64_t* offsets;
+  int hkv, G;
+  float scale;
+  int write_ring;
+  uint16_t* out; int64_t o_sn, o_sl, o_sh, o_sg;
+  float* ws;
+  int64_t unit;     // floats of workspace per (row, kv head)
+  int sc_stride;    // floats per query head in the score area (W + KB)
+};
+
+// Workspace of one (row, kv head): scores [G][W + KB] | block maxima [G][KB] | partial sums [NS][G][D] |
+// partial normalisers [NS][G] (padded).
+__host__ __device__ inline int64_t unit_floats(int G, int W) {
+  const int64_t f = (int64_t)G * (W + KB) + (int64_t)G * KB + (int64_t)NS * G * D + (int64_t)NS * G_MAX;
+  return (f + 63) / 64 * 64;
+}
+
+struct RowInfo {
+  bool live;          // lens == 1 and a valid slot
+  int64_t slot, start, tok;
+};
+
+__device__ __forceinline__ RowInfo row_info(const DecParams& p, int n) {
+  RowInfo r;
+  r.slot = p.slots[n];
+  r.start = p.starts[n];
+  r.live = p.lens[n] == 1 && r.slot >= 0 && r.slot < p.ring_rows;
+  r.tok = p.offsets ? p.offsets[n] : n;
+  return r;
+}
+
+__device__ __forceinline__ int64_t row_base(const DecParams& p, int64_t sn, int64_t sl, int n, int64_t tok) {
+  return p.offsets ? tok * sl : (int64_t)n * sn;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m16 = lane & 15, g4 = lane >> 4;
+  const int s = blockIdx.x % NS;
+  const int u = blockIdx.x / NS;
+  const int n = u / p.hkv, h = u - n * p.hkv;
+  const RowInfo ri = row_info(p, n);
+  if (!ri.live) return;
+  const int W = p.W, G = p.G, RB = W / KB;
+  const int bps = (RB + NS - 1) / NS;
+  const int b = s * bps + wave;
+  float* sc = p.ws + u * p.unit;
+  float* bm = sc + (int64_t)G * p.sc_stride;
+  const int64_t qpos = ri.start;
+  const uint16_t* qrow = p.q + row_base(p, p.q_sn, p.q_sl, n, ri.tok) + h * p.q_sh;
+
+  if (wave < bps && b < RB) {
+    // Two memory round trips: the block's positions (and the queries), then its keys only if one of them
+    // is visible (a partly filled ring costs no key traffic for its empty blocks).
+    const int64_t* rpos = p.ring_pos + ri.slot * (int64_t)(W + 1) + b * KB;
+    int64_t kp8[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) kp8[t][r] = rpos[16 * t + 4 * g4 + r];
+    // B operand: query head m16 (zero for m16 >= G), dims 32 ks + 8 g4 ..
+    bf16x8 qb[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (m16 < G) w = *reinterpret_cast<const uint4*>(qrow + m16 * p.q_sg + 32 * ks + 8 * g4);
+      qb[ks] = __builtin_bit_cast(bf16x8, w);
+    }
+    bool vis = false;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vis |= kp8[t][r] >= 0 && kp8[t][r] <= qpos && kp8[t][r] > qpos - W;
+    if (__ballot(vis) == 0) {
+      if (lane < G) bm[lane * KB + b] = -INFINITY;
+    } else {
+      const uint16_t* kbase = p.ring_k + ((ri.slot * p.hkv + h) * (int64_t)(W + 1) + b * KB) * D;
+      uint4 ka[2][D / 32];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks)
+          ka[t][ks] = *reinterpret_cast<const uint4*>(kbase + (16 * t + m16) * D + 32 * ks + 8 * g4);
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[t][ks]), qb[ks], acc, 0, 0, 0);
+        // lane (query m16, keys 16 t + 4 g4 + r)
+        f32x4 sv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t kp = kp8[t][r];
+          const bool ok = kp >= 0 && kp <= qpos && kp > qpos - W;
+          sv[r] = ok ? acc[r] * p.scale : -INFINITY;
+          bmax = fmaxf(bmax, sv[r]);
+        }
+        if (m16 < G) *reinterpret_cast<f32x4*>(sc + m16 * p.sc_stride + b * KB + 16 * t + 4 * g4) = sv;
+      }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+      if (g4 == 0 && m16 < G) bm[m16 * KB + b] = bmax;
+    }
+  }
+
+  // the step's own key: block RB, one key, always visible to its own query
+  if (s == NS - 1 && wave == 0) {
+    const uint16_t* kn = p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh;
+    float k4[4];
+    load4_bf16(kn + 4 * lane, k4);
+    for (int g = 0; g < G; ++g) {
+      float q4[4];
+      load4_bf16(qrow + g * p.q_sg + 4 * lane, q4);
+      const float part = q4[0] * k4[0] + q4[1] * k4[1] + q4[2] * k4[2] + q4[3] * k4[3];
+      const float v = wave_sum(part) * p.scale;
+      if (lane == 0) {
+        sc[g * p.sc_stride + W] = v;
+        bm[g * KB + RB] = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+template <int GT>
+__global__ __launch_bounds__(256) void decode_values_kernel(const DecParams p) {
+  __shared__ __align__(16) float pb_s[4][GT][KB];
+  __shared__ __align__(16) float red[4][GT * D / 4][4];
+  __shared__ float lsum_s[4][GT];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s = blockIdx.x % NS;
+  const int u = blockIdx.x / NS;
+  const int n = u / p.hkv, h = u - n * p.hkv;
+  const RowInfo ri = row_info(p, n);
+  if (!ri.live) return;
+  const int W = p.W, G = p.G, RB = W / KB, NB = RB + 1;
+  const int bps = (RB + NS - 1) / NS;
+  const int b = s * bps + wave;
+  float* sc = p.ws + u * p.unit;
+  const float* bm = sc + (int64_t)G * p.sc_stride;
+  float* pacc = const_cast<float*>(bm) + (int64_t)G * KB;
+  float* pl = pacc + (int64_t)NS * G * D;
+
+  // Two memory round trips: every block maximum of the lane's head (lanes g < G) and the block's scores
+  // (lane: head g0 + lane / 16, keys 2 (lane % 16), +1) together, then the block's values (lane: dims
+  // 8 (lane % 32) .., keys 2 j + lane / 32) only if one of its keys is visible.
+  const bool ring_block = wave < bps && b < RB;
+  const int dl = 8 * (lane & 31), kh = lane >> 5;
+  float bmv[W_MAX / KB + 1];
+#pragma unroll
+  for (int j = 0; j <= W_MAX / KB; ++j) bmv[j] = (lane < G && j < NB) ? bm[lane * KB + j] : -INFINITY;
+  constexpr int GR = (GT + 3) / 4;   // rounds of 4 heads for the probabilities
+  float sv[GR][2];
+#pragma unroll
+  for (int gr = 0; gr < GR; ++gr) {
+    const int g = 4 * gr + (lane >> 4);
+    const int key = 2 * (lane & 15);
+    sv[gr][0] = sv[gr][1] = -INFINITY;
+    if (ring_block && g < G) {
+      const float2 x = *reinterpret_cast<const float2*>(sc + g * p.sc_stride + b * KB + key);
+      sv[gr][0] = x.x;
+      sv[gr][1] = x.y;
+    }
+  }
+  // lane g < G: running max through block b (m_b) and over all blocks (m_final)
+  float mb = -INFINITY, mf = -INFINITY;
+#pragma unroll
+  for (int j = 0; j <= W_MAX / KB; ++j) {
+    mf = fmaxf(mf, bmv[j]);
+    if (j == b) mb = mf;
+  }
+  float acc[GT][8];
+#pragma unroll
+  for (int g = 0; g < GT; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  float lpart = 0.f;   // lane g < G: this wave's weighted normaliser for head g
+
+  // a block without any visible key has no scores written (every head shares the step's visibility)
+  const bool has_block = ring_block && __shfl(bmv[b < NB ? b : 0], 0, 64) != -INFINITY;
+  if (has_block) {
+    const float mb_l = mb;
+    uint4 vr[KB / 2];
+    const uint16_t* vbase = p.ring_v + ((ri.slot * p.hkv + h) * (int64_t)(W + 1) + b * KB) * D + dl;
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) vr[j] = *reinterpret_cast<const uint4*>(vbase + (2 * j + kh) * D);
+#pragma unroll
+    for (int gr = 0; gr < GR; ++gr) {
+      const int g0 = 4 * gr;
+      const int g = g0 + (lane >> 4);
+      const int key = 2 * (lane & 15);
+      const float m_g = __shfl(mb_l, g < G ? g : 0, 64);
+      float p0 = 0.f, p1 = 0.f;
+      if (g < G && m_g != -INFINITY) {
+        p0 = sv[gr][0] == -INFINITY ? 0.f : expf(sv[gr][0] - m_g);
+        p1 = sv[gr][1] == -INFINITY ? 0.f : expf(sv[gr][1] - m_g);
+      }
+      if (g < G) {
+        pb_s[wave][g][key] = rbf(p0);
+        pb_s[wave][g][key + 1] = rbf(p1);
+      }
+      float ps = p0 + p1;   // unrounded, as the reference's row sum
+      ps += __shfl_xor(ps, 1, 64);
+      ps += __shfl_xor(ps, 2, 64);
+      ps += __shfl_xor(ps, 4, 64);
+      ps += __shfl_xor(ps, 8, 64);
+      // lane 16 j holds the sum for head g0 + j; move it to lane g0 + j
+      const float got = __shfl(ps, 16 * ((lane - g0) & 3), 64);
+      if (lane >= g0 && lane < g0 + 4 && lane < G) lpart = got;
+    }
+    // block weight exp(m_b - m_final) per head (lane g < G)
+    float wgt = 0.f;
+    if (lane < G && mb_l != -INFINITY) wgt = expf(mb_l - mf);
+    lpart *= wgt;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) {
+      const int k = 2 * j + kh;
+      float v[8];
+      unpack2(vr[j].x, v[0], v[1]);
+      unpack2(vr[j].y, v[2], v[3]);
+      unpack2(vr[j].z, v[4], v[5]);
+      unpack2(vr[j].w, v[6], v[7]);
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        if (g < G) {
+          const float pk = pb_s[wave][g][k];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] += pk * v[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g < G) {
+        const float wg = __shfl(wgt, g, 64);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = (acc[g][i] + __shfl_xor(acc[g][i], 32, 64)) * wg;  // both key halves
+      }
+    }
+  }
+
+  // the step's own key (block RB): last split, wave 0; its running max is m_final, weight 1
+  if (s == NS - 1 && wave == 0) {
+    const uint16_t* vn = p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) + h * p.nv_sh + dl;
+    float v[8];
+    load4_bf16(vn, v);
+    load4_bf16(vn + 4, v + 4);
+    float pnew = 0.f;
+    if (lane < G) pnew = expf(sc[lane * p.sc_stride + W] - mf);
+    lpart += pnew;
+    if (kh == 0) {
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        if (g < G) {
+          const float pk = rbf(__shfl(pnew, g, 64));
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] += pk * v[i];
+        }
+      }
+    }
+  }
+
+  // ---- reduce the four waves (lanes < 32 hold dims 8 lane .. 8 lane + 7) ----
+  if (kh == 0) {
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g < G) {
+        float* dst = &red[wave][g * (D / 4) + 2 * lane][0];
+        *reinterpret_cast<float4*>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+      }
+    }
+  }
+  if (lane < G) lsum_s[wave][lane] = lpart;
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * (D / 4); e += 256) {
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float4 x = *reinterpret_cast<const float4*>(&red[w][e][0]);
+      t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
+    }
+    *reinterpret_cast<float4*>(pacc + (int64_t)s * G * D + 4 * e) = t;
+  }
+  if (threadIdx.x < G) {
+    pl[s * G_MAX + threadIdx.x] = lsum_s[0][threadIdx.x] + lsum_s[1][threadIdx.x] + lsum_s[2][threadIdx.x] +
+                                  lsum_s[3][threadIdx.x];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void decode_combine_kernel(const DecParams p) {
+  const int u = blockIdx.x;
+  const int n = u / p.hkv, h = u - n * p.hkv;
+  const RowInfo ri = row_info(p, n);
+  const int W = p.W, G = p.G;
+  if (!ri.live) {
+    // padded layout: a row without a live step (lens 0 or a rejected slot) owns an output row of zeros
+    if (p.offsets == nullptr) {
+      for (int e = threadIdx.x; e < G * (D / 4); e += 256) {
+        const int g = e / (D / 4), d = 4 * (e - g * (D / 4));
+        const float z[4] = {0.f, 0.f, 0.f, 0.f};
+        store4_bf16(p.out + (int64_t)n * p.o_sn + h * p.o_sh + g * p.o_sg + d, z);
+      }
+    }
+    return;
+  }
+  const float* sc = p.ws + u * p.unit;
+  const float* pacc = sc + (int64_t)G * p.sc_stride + (int64_t)G * KB;
+  const float* pl = pacc + (int64_t)NS * G * D;
+  uint16_t* orow = p.out + row_base(p, p.o_sn, p.o_sl, n, ri.tok) + h * p.o_sh;
+  const uint16_t* grow = p.gate ? p.gate + row_base(p, p.g_sn, p.g_sl, n, ri.tok) + h * p.g_sh + p.g_off : nullptr;
+  for (int e = threadIdx.x; e < G * (D / 4); e += 256) {
+    const int g = e / (D / 4), d = 4 * (e - g * (D / 4));
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float4 x = *reinterpret_cast<const float4*>(pacc + (int64_t)s * G * D + g * D + d);
+      o[0] += x.x; o[1] += x.y; o[2] += x.z; o[3] += x.w;
+      l += pl[s * G_MAX + g];
+    }
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = l > 0.f ? rbf(o[i] / l) : 0.f;
+    if (grow) {
+      float gt[4];
+      load4_bf16(grow + g * p.g_sg + d, gt);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = y[i] * rbf(1.0f / (1.0f + expf(-gt[i])));
+    }
+    store4_bf16(orow + g * p.o_sg + d, y);
+  }
+  if (p.write_ring) {
+    const int64_t col = ri.start % W;
+    const int64_t dst = ((ri.slot * p.hkv + h) * (int64_t)(W + 1) + col) * D;
+    const uint16_t* kn = p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh;
+    const uint16_t* vn = p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) + h * p.nv_sh;
+    for (int e = threadIdx.x; e < 2 * (D / 4); e += 256) {
+      const int which = e / (D / 4), d = 4 * (e - which * (D / 4));
+      if (which == 0) *reinterpret_cast<uint2*>(p.ring_k + dst + d) = *reinterpret_cast<const uint2*>(kn + d);
+      else *reinterpret_cast<uint2*>(p.ring_v + dst + d) = *reinterpret_cast<const uint2*>(vn + d);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace hsg
+
+extern "C" size_t hsg_ring_decode_workspace_bytes(int32_t n_rows, int32_t hkv, int32_t groups, int32_t window) {
+  if (n_rows <= 0 || hkv <= 0 || groups <= 0 || window <= 0) return 0;
+  return (size_t)n_rows * hkv * (size_t)hsg::unit_floats(groups, window) * sizeof(float);
+}
+
+extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,
+                               void* ring_k, void* ring_v, int64_t ring_rows, int32_t window,
+                               const void* new_k, int64_t nk_sn, int64_t nk_sl, int64_t nk_sh,
+                               const void* new_v, int64_t nv_sn, int64_t nv_sl, int64_t nv_sh,
+                               const void* gate, int64_t g_sn, int64_t g_sl, int64_t g_sh, int64_t g_sg,
+                               int64_t g_off, const int64_t* ring_pos, const int64_t* slots,
+                               const int64_t* starts, const int64_t* lens, const int64_t* offsets,
+                               int32_t n_rows, int32_t hkv, int32_t groups, int32_t head_dim, float scale,
+                               int32_t write_ring, void* out, int64_t o_sn, int64_t o_sl, int64_t o_sh,
+                               int64_t o_sg, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace hsg;
+  if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
+  if (n_rows == 0) return HSG_OK;
+  if (!q || !ring_k || !ring_v || !new_k || !new_v || !ring_pos || !slots || !starts || !lens || !out ||
+      !workspace)
+    return HSG_ERR_ARG;
+  if (head_dim != D || window <= 0 || window > W_MAX || window % KB != 0 || groups > G_MAX) return HSG_ERR_SHAPE;
+  if (workspace_bytes < hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window)) return HSG_ERR_SHAPE;
+  const int64_t s16[] = {q_sn, q_sl, q_sh, q_sg};
+  for (int64_t s : s16)
+    if (s % 8) return HSG_ERR_ALIGN;
+  const int64_t s4[] = {nk_sn, nk_sl, nk_sh, nv_sn, nv_sl, nv_sh, g_sn, g_sl, g_sh, g_sg, g_off, o_sn, o_sl, o_sh, o_sg};
+  for (int64_t s : s4)
+    if (s % 4) return HSG_ERR_ALIGN;
+  if (!aligned(q, 16) || !aligned(ring_k, 16) || !aligned(ring_v, 16) || !aligned(new_k, 8) ||
+      !aligned(new_v, 8) || !aligned(out, 8) || (gate && !aligned(gate, 8)) || !aligned(workspace, 16))
+    return HSG_ERR_ALIGN;
+  DecParams p{};
+  p.q = static_cast<const uint16_t*>(q); p.q_sn = q_sn; p.q_sl = q_sl; p.q_sh = q_sh; p.q_sg = q_sg;
+  p.ring_k = static_cast<uint16_t*>(ring_k); p.ring_v = static_cast<uint16_t*>(ring_v);
+  p.ring_rows = ring_rows; p.W = window;
+  p.new_k = static_cast<const uint16_t*>(new_k); p.nk_sn = nk_sn; p.nk_sl = nk_sl; p.nk_sh = nk_sh;
+  p.new_v = static_cast<const uint16_t*>(new_v); p.nv_sn = nv_sn; p.nv_sl = nv_sl; p.nv_sh = nv_sh;
+  p.gate = static_cast<const uint16_t*>(gate);
+  p.g_sn = g_sn; p.g_sl = g_sl; p.g_sh = g_sh; p.g_sg = g_sg; p.g_off = g_off;
+  p.ring_pos = ring_pos; p.slots = slots; p.starts = starts; p.lens = lens; p.offsets = offsets;
+  p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring;
+  p.out = static_cast<uint16_t*>(out); p.o_sn = o_sn; p.o_sl = o_sl; p.o_sh = o_sh; p.o_sg = o_sg;
+  p.ws = static_cast<float*>(workspace);
+  p.unit = unit_floats(groups, window);
+  p.sc_stride = window + KB;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned units = (unsigned)(n_rows * hkv);
+  hipLaunchKernelGGL(decode_scores_kernel, dim3(units * NS), dim3(256), 0, st, p);
+  if (groups <= 4) hipLaunchKernelGGL(decode_values_kernel<4>, dim3(units * NS), dim3(256), 0, st, p);
+  else if (groups <= 8) hipLaunchKernelGGL(decode_values_kernel<8>, dim3(units * NS), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(decode_values_kernel<16>, dim3(units * NS), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(units), dim3(256), 0, st, p);
+  return launch_status();
+}

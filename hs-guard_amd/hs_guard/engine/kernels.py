@@ -110,11 +110,12 @@ def gdn_chunk_prefill(packed, key_dim, heads, head_k, value_heads, head_v, a, b,
 
 
 def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens, scale, window,
-                      write_ring, block_m=16, block_n=32, num_warps=4, num_stages=1):
+                      write_ring, block_m=16, block_n=32, num_warps=4, num_stages=1, split_k=True):
     """Replaces fused_kernels.py:358-376. q [N, Hkv, G*Lb, D] and new_k [N, Hkv, Lb, D]; value [N, Lb, Hkv*D]
     (v_proj output, strided rows allowed); gate: q_proj output [N, Lb, Hq*2D] (gate = second half of each
     head). Returns out * sigmoid(gate) as [N, Lb, Hq*D] bf16. write_ring (Lb == 1 only, as the
-    reference): also writes this tick's key/value into ring column start % window."""
+    reference): also writes this tick's key/value into ring column start % window. Decode ticks (Lb == 1)
+    run the split-K kernels (hsg_ring_decode) unless split_k is False."""
     n, hkv, m, d = q.shape
     lb = new_k.shape[2]
     groups = m // lb
@@ -124,6 +125,20 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
         _require(tensor.is_contiguous(), "tensors must be contiguous")
     _gpu(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens)
     out = torch.empty(n, lb, hkv * groups * d, dtype=torch.bfloat16, device=q.device)
+    if lb == 1 and split_k:
+        ws_bytes = lib().hsg_ring_decode_workspace_bytes(n, hkv, groups, window)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+        rc = lib().hsg_ring_decode(
+            _ptr(q), hkv * m * d, d, m * d, d,
+            _ptr(ring_k), _ptr(ring_v), ring_k.shape[0], window,
+            _ptr(new_k), hkv * d, d, d,
+            _ptr(value), value.stride(0), value.stride(1), d,
+            _ptr(gate), gate.stride(0), gate.stride(1), groups * 2 * d, 2 * d, d,
+            _ptr(ring_pos), _ptr(slots), _ptr(starts), _ptr(lens), None,
+            n, hkv, groups, d, float(scale), int(bool(write_ring)),
+            _ptr(out), hkv * groups * d, hkv * groups * d, groups * d, d, _ptr(ws), ws.numel(), _stream(q.device))
+        check(rc, "hsg_ring_decode")
+        return out
     rc = lib().hsg_ring_attention(
         _ptr(q), hkv * m * d, d, m * d, lb * d,
         _ptr(ring_k), _ptr(ring_v), ring_k.shape[0], window,
@@ -131,7 +146,7 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
         _ptr(value), value.stride(0), value.stride(1), d,
         _ptr(gate), gate.stride(0), gate.stride(1), groups * 2 * d, 2 * d, d,
         _ptr(ring_pos), _ptr(slots), _ptr(starts), _ptr(lens), None,
-        n, lb, hkv, groups, d, float(scale), int(bool(write_ring)),
+        n, lb, hkv, groups, d, float(scale), int(bool(write_ring)), 0,
         _ptr(out), lb * hkv * groups * d, hkv * groups * d, groups * d, d, _stream(q.device))
     check(rc, "hsg_ring_attention")
     return out
@@ -156,7 +171,7 @@ def ring_attention(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, len
         _ptr(new_v), hkv * lb * d, d, lb * d,
         None, 0, 0, 0, 0, 0,
         _ptr(ring_pos), _ptr(slots), _ptr(starts), _ptr(lens), None,
-        n, lb, hkv, groups, d, float(scale), 0,
+        n, lb, hkv, groups, d, float(scale), 0, 0,
         _ptr(out), hkv * m * d, d, m * d, lb * d, _stream(q.device))
     check(rc, "hsg_ring_attention")
     return out

@@ -193,6 +193,9 @@ class SlotStreamEngine:
             "probs": torch.zeros(len(self.roles) * T * 3, dtype=torch.float32, device=dev),
             "inputs": torch.zeros(2 * T + 4 * self.max_rows, dtype=torch.long, device=dev),
         }
+        # split-K decode scratch (scores, block maxima, partial sums) for the single-step rows of a tick
+        ws = lib().hsg_ring_decode_workspace_bytes(self.max_rows, hkv, hq // hkv, self.window)
+        self.ring_ws = torch.empty(max(int(ws), 16), dtype=torch.uint8, device=dev)
 
     def _view(self, name, *shape):
         n = 1
@@ -296,6 +299,17 @@ class SlotStreamEngine:
                                       k.data_ptr(), hkv * D, D, pos.data_ptr(), self.inv_freq.data_ptr(),
                                       cfg.rotary_dim, tb, D, st), "hsg_norm_rope")
                 att = self._view("mid", tb, hq * D)
+                # single-step rows: split-K decode; rows of two or more steps: the tiled kernel (min_len 2)
+                check(L.hsg_ring_decode(
+                    q.data_ptr(), 0, hq * D, G * D, D,
+                    self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
+                    k.data_ptr(), 0, hkv * D, D,
+                    base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
+                    base, 0, self.att_in, G * 2 * D, 2 * D, D,
+                    self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
+                    nb, hkv, G, D, D ** -0.5, 1,
+                    att.data_ptr(), 0, hq * D, G * D, D, self.ring_ws.data_ptr(), self.ring_ws.numel(), st),
+                    "hsg_ring_decode")
                 check(L.hsg_ring_attention(
                     q.data_ptr(), 0, hq * D, G * D, D,
                     self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
@@ -303,7 +317,7 @@ class SlotStreamEngine:
                     base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
                     base, 0, self.att_in, G * 2 * D, 2 * D, D,
                     self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
-                    nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1,
+                    nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
                     att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
                 torch.mm(att, Lw["w_out"].t(), out=mix)
             check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), Lw["post_w1"].data_ptr(), eps,

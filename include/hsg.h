@@ -20,6 +20,7 @@
 #ifndef HSG_H_
 #define HSG_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -104,6 +105,8 @@ int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, in
  * kpos > qpos - window. Output = softmax-weighted values, rounded to bf16, times bf16(sigmoid(gate)).
  * write_ring != 0: after every read, new key/value of each valid step j go to ring column
  * (start+j) % window. ring_pos itself is not written (see hsg_ring_pos_update).
+ * Packed layout only: rows with lens[n] < min_len are skipped (no output, no ring write), so that a tick's
+ * single-step rows can go to hsg_ring_decode (min_len 2); min_len <= 1 processes every row.
  * Supported: head_dim == 256, window <= 512 and a multiple of 32, lb <= 64 (rows with lens[n] > 64 are
  * treated as empty); write_ring needs lb <= window so that the steps of one tick own distinct columns.
  */
@@ -114,8 +117,31 @@ int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, 
                        int64_t g_sh, int64_t g_sg, int64_t g_off, const int64_t* ring_pos,
                        const int64_t* slots, const int64_t* starts, const int64_t* lens,
                        const int64_t* offsets, int32_t n_rows, int32_t lb, int32_t hkv, int32_t groups,
-                       int32_t head_dim, float scale, int32_t write_ring, void* out, int64_t o_sn,
-                       int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream);
+                       int32_t head_dim, float scale, int32_t write_ring, int32_t min_len, void* out,
+                       int64_t o_sn, int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream);
+
+/*
+ * Split-K ring attention for decode steps: the same contract and numerics as hsg_ring_attention for rows with
+ * lens[n] == 1 (one query position; lb is 1 and the padded layout is [n_rows, 1, ...]). Replaces
+ * ring_attention_v8 at its decode shape (src/hs_guard/engine/fused_kernels.py:358-376 with Lb == 1,
+ * write_ring True, the reference's per-token streaming step). Three launches on `stream`: scores and 32-key
+ * block maxima per (row, kv head, quarter of the ring columns); per-block probabilities with the running
+ * maximum recovered as the prefix maximum of the block maxima, times values; combine, gate, ring write.
+ * Packed layout: rows with lens[n] != 1 are not touched. Padded layout: rows with lens[n] == 0 (or a slot
+ * outside [0, ring_rows)) get zero outputs. workspace: device memory of at least
+ * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes, 16-byte aligned; its contents need
+ * no initialisation and are garbage afterwards. Supported: head_dim == 256, window <= 512 and a multiple of
+ * 32, groups <= 16.
+ */
+size_t hsg_ring_decode_workspace_bytes(int32_t n_rows, int32_t hkv, int32_t groups, int32_t window);
+int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,
+                    void* ring_v, int64_t ring_rows, int32_t window, const void* new_k, int64_t nk_sn,
+                    int64_t nk_sl, int64_t nk_sh, const void* new_v, int64_t nv_sn, int64_t nv_sl,
+                    int64_t nv_sh, const void* gate, int64_t g_sn, int64_t g_sl, int64_t g_sh, int64_t g_sg,
+                    int64_t g_off, const int64_t* ring_pos, const int64_t* slots, const int64_t* starts,
+                    const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t hkv, int32_t groups,
+                    int32_t head_dim, float scale, int32_t write_ring, void* out, int64_t o_sn, int64_t o_sl,
+                    int64_t o_sh, int64_t o_sg, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Embedding gather + RMSNorm of the first layer. Replaces embed_tokens + add_square(hidden) + rms_finish

@@ -48,9 +48,21 @@ def test_argument_errors_are_rejected_before_launch():
                              1.0, 8, None, None)
     assert rc == -3
     rc = L.hsg_ring_attention(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
-                              8, 8, 8, 8, None, 2, 1, 4, 4, 128, 1.0, 0, 16, 0, 0, 0, 0, None)
+                              8, 8, 8, 8, None, 2, 1, 4, 4, 128, 1.0, 0, 0, 16, 0, 0, 0, 0, None)
     assert rc == -3
+    # split-K decode: head_dim 128 and a too-small workspace are rejected, n_rows == 0 is a no-op
+    need = L.hsg_ring_decode_workspace_bytes(2, 4, 4, 512)
+    assert need > 0
+    rc = L.hsg_ring_decode(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
+                           8, 8, 8, 8, None, 2, 4, 4, 128, 1.0, 1, 16, 0, 0, 0, 0, 16, need, None)
+    assert rc == -3
+    rc = L.hsg_ring_decode(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
+                           8, 8, 8, 8, None, 2, 4, 4, 256, 1.0, 1, 16, 0, 0, 0, 0, 16, need - 1, None)
+    assert rc == -3
+    assert L.hsg_ring_decode(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, 0,
+                             0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0, None, 0,
+                             None) == 0
     # n_rows == 0 is a no-op success
     assert L.hsg_ring_attention(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
-                                0, 0, None, None, None, None, None, 0, 1, 4, 4, 256, 1.0, 0, None, 0, 0, 0, 0,
+                                0, 0, None, None, None, None, None, 0, 1, 4, 4, 256, 1.0, 0, 0, None, 0, 0, 0, 0,
                                 None) == 0

@@ -101,3 +101,109 @@ def test_reference_contract_ungated():
                                  slots.numpy(), starts.numpy(), lens.numpy(), D ** -0.5, W)
     from oracle.bf16 import bf16
     _check(_np(out), bf16(ref), rtol=2.0 ** -8)
+
+
+def _decode_case(seed, N, Hkv, G, W, S, fills, lens, D=256):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(N, Hkv, G, D, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    new_k = torch.randn(N, Hkv, 1, D, generator=gen).to(torch.bfloat16)
+    value = torch.randn(N, 1, Hkv * D, generator=gen).to(torch.bfloat16)
+    gate = torch.randn(N, 1, Hkv * G * 2 * D, generator=gen).to(torch.bfloat16)
+    slots = torch.randperm(S - 1, generator=gen)[:N]
+    starts = torch.randint(0, 3 * W, (N,), generator=gen)
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s, st, f in zip(slots.tolist(), starts.tolist(), fills):
+        for p_ in range(max(0, st - f), st):
+            ring_pos[s, p_ % W] = p_
+    return q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, torch.tensor(lens, dtype=torch.long)
+
+
+@pytest.mark.parametrize("G,W", [(4, 512), (1, 64), (2, 128), (8, 512)])
+def test_split_k_decode_matches_oracle_and_tiled_kernel(G, W):
+    """hsg_ring_decode (split-K) against the blockwise oracle and against the tiled kernel on the same decode
+    tick: full, partial and empty rings (only the step's own key visible), a row with lens 0 (zeros), ring
+    write bit-exact."""
+    from hs_guard.engine.kernels import ring_attention_v8
+    print(f"[ring] split-K decode G={G} W={W}", flush=True)
+    N, Hkv, S, D = 6, 2, 8, 256
+    fills = [W, W // 2, 0, 5, W - 1, W]
+    lens = [1, 1, 1, 1, 0, 1]
+    q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens_t = _decode_case(7 + G, N, Hkv, G, W, S,
+                                                                                         fills, lens)
+    dev = torch.device("cuda:0")
+    outs, rings = [], []
+    for split in (True, False):
+        rk, rv = ring_k.to(dev), ring_v.to(dev)
+        out = ring_attention_v8(q.to(dev), rk, rv, new_k.to(dev), value.to(dev), gate.to(dev), ring_pos.to(dev),
+                                slots.to(dev), starts.to(dev), lens_t.to(dev), D ** -0.5, W, True, split_k=split)
+        outs.append(_np(out))
+        rings.append((_np(rk), _np(rv)))
+    ref, _, rk_ref, rv_ref = oring.ring_attention_v8(
+        _np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(value), _np(gate), ring_pos.numpy(), slots.numpy(),
+        starts.numpy(), lens_t.numpy(), D ** -0.5, W, True)
+    _check(outs[0], ref, what="split-K vs oracle")
+    _check(outs[0], outs[1], rtol=2.0 ** -8, what="split-K vs tiled")
+    assert np.count_nonzero(outs[0][4]) == 0            # lens 0 row
+    for rk, rv in rings:
+        np.testing.assert_array_equal(rk, rk_ref)
+        np.testing.assert_array_equal(rv, rv_ref)
+
+
+def test_mixed_packed_tick_split_between_kernels():
+    """A packed tick with single- and multi-step rows: hsg_ring_decode takes the single-step rows and
+    hsg_ring_attention (min_len 2) the rest; the result equals hsg_ring_attention on every row (min_len 0)
+    within one bf16 rounding, and the ring writes are identical."""
+    from hs_guard._lib import lib
+    print("[ring] mixed packed tick, split between kernels", flush=True)
+    gen = torch.Generator().manual_seed(21)
+    Hkv, G, D, W, S = 4, 4, 256, 512, 9
+    lens = torch.tensor([1, 3, 1, 0, 2, 1, 7], dtype=torch.long)
+    N = len(lens)
+    offsets = torch.cumsum(lens, 0) - lens
+    T = int(lens.sum())
+    hq = Hkv * G
+    att_in = hq * 2 * D + 2 * Hkv * D
+    proj = torch.randn(T, att_in, generator=gen).to(torch.bfloat16)       # gate | k | v layout of the engine
+    q = torch.randn(T, hq * D, generator=gen).to(torch.bfloat16)
+    k = torch.randn(T, Hkv * D, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    slots = torch.randperm(S - 1, generator=gen)[:N]
+    starts = torch.randint(0, 2000, (N,), generator=gen)
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s, st in zip(slots.tolist(), starts.tolist()):
+        for p_ in range(max(0, st - 400), st):
+            ring_pos[s, p_ % W] = p_
+    dev = torch.device("cuda:0")
+    d = {n: t.to(dev) for n, t in dict(proj=proj, q=q, k=k, slots=slots, starts=starts, lens=lens,
+                                         offsets=offsets, ring_pos=ring_pos).items()}
+    L = lib()
+    st = torch.cuda.current_stream().cuda_stream
+    base = d["proj"].data_ptr()
+    ws = torch.empty(L.hsg_ring_decode_workspace_bytes(N, Hkv, G, W), dtype=torch.uint8, device=dev)
+
+    def run(split):
+        rk, rv = ring_k.to(dev), ring_v.to(dev)
+        out = torch.zeros(T, hq * D, dtype=torch.bfloat16, device=dev)
+        args_tail = (d["ring_pos"].data_ptr(), d["slots"].data_ptr(), d["starts"].data_ptr(), d["lens"].data_ptr(),
+                     d["offsets"].data_ptr())
+        common = (d["q"].data_ptr(), 0, hq * D, G * D, D, rk.data_ptr(), rv.data_ptr(), S, W,
+                  d["k"].data_ptr(), 0, Hkv * D, D, base + 2 * (hq * 2 * D + Hkv * D), 0, att_in, D,
+                  base, 0, att_in, G * 2 * D, 2 * D, D) + args_tail
+        if split:
+            rc = L.hsg_ring_decode(*common, N, Hkv, G, D, D ** -0.5, 1, out.data_ptr(), 0, hq * D, G * D, D,
+                                   ws.data_ptr(), ws.numel(), st)
+            assert rc == 0, rc
+        rc = L.hsg_ring_attention(*common, N, 8, Hkv, G, D, D ** -0.5, 1, 2 if split else 0, out.data_ptr(), 0,
+                                  hq * D, G * D, D, st)
+        assert rc == 0, rc
+        torch.cuda.synchronize()
+        return _np(out), _np(rk), _np(rv)
+
+    a, rka, rva = run(True)
+    b, rkb, rvb = run(False)
+    _check(a, b, rtol=2.0 ** -8, what="split vs single kernel")
+    np.testing.assert_array_equal(rka, rkb)
+    np.testing.assert_array_equal(rva, rvb)
