@@ -16,6 +16,7 @@ at the 352 x 1-token decode shape, HIP events on its launch stream) and the CPU 
 restatement of the same step timed on this host on a bounded sample).
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -293,21 +294,35 @@ def main():
         eng.step(load.step_requests())
         reprefill(load.resets())
     torch.cuda.synchronize()
+    # the serving loop's own garbage stays collectable; the long-lived objects of the setup (torch, the model,
+    # the engine) are moved out of the collector's scans, as a long-running server process would
+    gc.collect()
+    gc.freeze()
     log("warm-up done")
-    times, tokens = [], 0
+    times, tokens, step_tokens = [], 0, []
     for i in range(args.steps):
         req = load.step_requests()
+        caps = eng.stats["captures"]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         eng.step(req)
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
-        tokens += sum(len(ids) for _, ids in req)
+        step_tokens.append(sum(len(ids) for _, ids in req))
+        tokens += step_tokens[-1]
+        if eng.stats["captures"] != caps or times[-1] > 0.05:
+            log(f"step {i}: {times[-1] * 1e3:.1f} ms, {eng.stats['captures'] - caps} graph captures, "
+                f"{len(req)} rows, max chunk {max(len(ids) for _, ids in req)}")
+        caps = eng.stats["captures"]
         reprefill(load.resets())
+        if eng.stats["captures"] != caps:
+            log(f"after step {i}: re-prefill captured {eng.stats['captures'] - caps} graphs")
         if (i + 1) % 50 == 0:
             log(f"step {i + 1}/{args.steps}: {tokens / sum(times):.0f} tok/s")
     total = sum(times)
     value = tokens / total
+    slow = sorted(range(len(times)), key=lambda i: -times[i])[:3]
+    log("slowest steps: " + ", ".join(f"#{i} {times[i] * 1e3:.1f} ms ({step_tokens[i]} tokens)" for i in slow))
 
     # ---- pure decode: 352 x 1 token, and 1 slot x 1 token (20 warm-up + 200 measured) ----
     def timed(make, n=200, warm=20):
