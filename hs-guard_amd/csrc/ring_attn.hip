@@ -6,9 +6,10 @@
 // in the P.V product and summed in fp32, output / sum rounded to bf16, times bf16(sigmoid(gate)); the
 // tick's keys/values are written into the ring in place after every read.
 //
-// Mapping: one workgroup (4 waves) per (row, kv head), so the workgroup owns that (slot, kv head)'s ring
-// and the ring write at the end cannot race with any read. Query rows r = l*G + g (token l, q group g)
-// form 16-row tiles; wave w takes tile 4*qg + w for query group qg. Per 64 keys the workgroup stages K
+// Mapping: query rows r = l*G + g (token l, q group g) of one (row, kv head) form 16-row tiles; one
+// workgroup (4 waves) per (row, kv head, query group qg), wave w taking tile 4*qg + w, so a 64-step row
+// spreads over several workgroups that stream the same ring in parallel. The in-place ring write is a second
+// launch (ring_write_kernel) after all reads. Per 64 keys the workgroup stages K
 // (row-major) and V (transposed) in LDS with coalesced 16-byte loads, skipping fills whose positions are
 // outside every query's window; then for each of the two 32-key softmax blocks of the fill each wave runs
 // on v_mfma_f32_16x16x32_bf16:
@@ -49,6 +50,7 @@ struct RingParams {
   float scale;
   int write_ring;
   int min_len;
+  int qgroups;      // workgroups per (row, kv head): groups of NW 16-row query tiles
   uint16_t* out; int64_t o_sn, o_sl, o_sh, o_sg;
 };
 
@@ -66,13 +68,18 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int n = blockIdx.x / p.hkv;
-  const int h = blockIdx.x - n * p.hkv;
+  // query group slowest: consecutive workgroups (which the dispatcher deals round-robin over the 8 XCDs)
+  // take consecutive (row, kv head) pairs, so the live workgroups of a short-row tick spread over all XCDs
+  const int n_pairs = gridDim.x / p.qgroups;
+  const int qg = blockIdx.x / n_pairs;
+  const int nh = blockIdx.x - qg * n_pairs;
+  const int n = nh / p.hkv;
+  const int h = nh - n * p.hkv;
   const int64_t slot = p.slots[n];
   const int64_t start = p.starts[n];
   int64_t len = p.lens[n];
   const bool padded = p.offsets == nullptr;
-  if (slot < 0 || slot >= p.ring_rows || len < 0 || len > LB_MAX) len = 0;  // > LB_MAX: rejected row
+  if (slot < 0 || slot >= p.ring_rows || len < 0 || len > (padded ? LB_MAX : p.lb)) len = 0;  // rejected row
   if (padded && len > p.lb) len = p.lb;
   if (!padded && len < p.min_len) return;              // left to another kernel (single-step rows: split-K)
   const int steps = padded ? p.lb : (int)len;          // output steps written for this row
@@ -93,7 +100,7 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
   const int n_ring_blocks = len > 0 ? W / KB : 0;
   const int n_new_blocks = (int)((len + KB - 1) / KB);
 
-  for (int qg = 0; qg * NW < QT; ++qg) {
+  if (qg * NW < QT) {
     const int tile = qg * NW + wave;
     const bool has_tile = tile < QT;
     // ---- this lane's query row ----
@@ -270,19 +277,30 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
     }
   }
 
-  // ---- in-place ring write of this tick's valid keys/values (all reads of this ring are done) ----
-  if (p.write_ring && len > 0) {
-    __syncthreads();
-    for (int e = tid; e < (int)len * (D / 4); e += NW * 64) {
-      const int j = e / (D / 4);
-      const int d = (e - j * (D / 4)) * 4;
-      const int64_t col = (start + j) % W;
-      const int64_t dst = ring_base + col * D + d;
-      *reinterpret_cast<uint2*>(p.ring_k + dst) =
-          *reinterpret_cast<const uint2*>(p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh + d);
-      *reinterpret_cast<uint2*>(p.ring_v + dst) =
-          *reinterpret_cast<const uint2*>(p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh + d);
-    }
+}
+
+// In-place ring write of the tick's valid keys/values, launched after the attention kernel (whose query
+// groups of one row run in different workgroups, so none of them may overwrite a column another still reads).
+__global__ __launch_bounds__(256) void ring_write_kernel(const RingParams p) {
+  const int n = blockIdx.x / p.hkv;
+  const int h = blockIdx.x - n * p.hkv;
+  const int64_t slot = p.slots[n];
+  int64_t len = p.lens[n];
+  const bool padded = p.offsets == nullptr;
+  if (slot < 0 || slot >= p.ring_rows || len < 0 || len > (padded ? LB_MAX : p.lb)) return;
+  if (padded && len > p.lb) len = p.lb;
+  if (!padded && len < p.min_len) return;
+  const int64_t base_tok = padded ? 0 : p.offsets[n];
+  const int64_t nk_row = padded ? n * p.nk_sn : base_tok * p.nk_sl;
+  const int64_t nv_row = padded ? n * p.nv_sn : base_tok * p.nv_sl;
+  const int64_t ring_base = ((slot * p.hkv + h) * (int64_t)(p.W + 1)) * D;
+  for (int e = threadIdx.x; e < (int)len * (D / 4); e += 256) {
+    const int j = e / (D / 4);
+    const int d = (e - j * (D / 4)) * 4;
+    const int64_t col = (p.starts[n] + j) % p.W;
+    const int64_t dst = ring_base + col * D + d;
+    *reinterpret_cast<uint2*>(p.ring_k + dst) = *reinterpret_cast<const uint2*>(p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh + d);
+    *reinterpret_cast<uint2*>(p.ring_v + dst) = *reinterpret_cast<const uint2*>(p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh + d);
   }
 }
 
@@ -326,7 +344,9 @@ extern "C" int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int
   p.ring_pos = ring_pos; p.slots = slots; p.starts = starts; p.lens = lens; p.offsets = offsets;
   p.lb = lb; p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring; p.min_len = min_len;
   p.out = static_cast<uint16_t*>(out); p.o_sn = o_sn; p.o_sl = o_sl; p.o_sh = o_sh; p.o_sg = o_sg;
-  hipLaunchKernelGGL(ring_attn_mfma_kernel, dim3((unsigned)(n_rows * hkv)), dim3(NW * 64), 0,
-                     reinterpret_cast<hipStream_t>(stream), p);
+  p.qgroups = ((groups * lb + 15) / 16 + NW - 1) / NW;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(ring_attn_mfma_kernel, dim3((unsigned)(n_rows * hkv * p.qgroups)), dim3(NW * 64), 0, st, p);
+  if (write_ring) hipLaunchKernelGGL(ring_write_kernel, dim3((unsigned)(n_rows * hkv)), dim3(256), 0, st, p);
   return launch_status();
 }

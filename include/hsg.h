@@ -107,8 +107,10 @@ int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, in
  * (start+j) % window. ring_pos itself is not written (see hsg_ring_pos_update).
  * Packed layout only: rows with lens[n] < min_len are skipped (no output, no ring write), so that a tick's
  * single-step rows can go to hsg_ring_decode (min_len 2); min_len <= 1 processes every row.
- * Supported: head_dim == 256, window <= 512 and a multiple of 32, lb <= 64 (rows with lens[n] > 64 are
- * treated as empty); write_ring needs lb <= window so that the steps of one tick own distinct columns.
+ * Supported: head_dim == 256, window <= 512 and a multiple of 32, lb <= 64. Padded layout: steps past lb are
+ * not computed (rows with lens[n] > 64 are treated as empty); packed layout: lb bounds every row's length and
+ * rows with lens[n] > lb are treated as empty. write_ring needs lb <= window so that the steps of one tick own
+ * distinct columns; with write_ring the call is two launches on `stream` (attention, then the ring write).
  */
 int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,
                        void* ring_k, void* ring_v, int64_t ring_rows, int32_t window, const void* new_k,
