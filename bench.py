@@ -227,6 +227,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel measurement (the command profiled under rocprofv3)")
+    ap.add_argument("--mixed-only", action="store_true",
+                    help="only the prefill and the mixed steps (no kernel legs, decode legs, context sweep or CPU "
+                         "baseline): the command whose kernel statistics give the per-step kernel breakdown")
+    ap.add_argument("--reset-p", type=float, default=0.01, help="per-slot reset probability after each step")
+    ap.add_argument("--sweep-steps", type=int, default=60,
+                    help="timed mixed steps per initial-context length in the per-context latency sweep (0: skip)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -245,8 +251,13 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(0)}")
     state_code = 0 if args.state_dtype == "float32" else 1
-    roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
-    log(f"GDN roofline {roof}")
+    if args.mixed_only:
+        args.sweep_steps = 0
+        args.no_cpu_baseline = True
+        roof = ring = chunk = None
+    else:
+        roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
+        log(f"GDN roofline {roof}")
     if args.roofline_only:
         # calibration for HBM-traffic counters: a plain 512 MiB device-to-device copy (512 MiB read + written)
         src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
@@ -256,10 +267,11 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"roofline_only": roof, "calibration_copy_bytes": 512 << 20}), flush=True)
         return
-    ring = ring_decode_rate(torch, rows=args.slots)
-    log(f"ring decode {ring}")
-    chunk = chunk_prefill_rate(torch)
-    log(f"chunk prefill config 4 {chunk}")
+    if not args.mixed_only:
+        ring = ring_decode_rate(torch, rows=args.slots)
+        log(f"ring decode {ring}")
+        chunk = chunk_prefill_rate(torch)
+        log(f"chunk prefill config 4 {chunk}")
 
     cfg = GuardConfig.baseline()
     t0 = time.time()
@@ -267,7 +279,7 @@ def main():
     log(f"model {model.num_parameters() / 1e6:.1f}M params in {time.time() - t0:.1f}s")
     eng = SlotStreamEngine(model, args.slots, state_dtype=args.state_dtype)
     load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
-                            contexts=tuple(int(x) for x in args.contexts.split(",")))
+                            contexts=tuple(int(x) for x in args.contexts.split(",")), reset_p=args.reset_p)
 
     # ---- untimed initial contexts ----
     t0 = time.time()
@@ -323,6 +335,43 @@ def main():
     value = tokens / total
     slow = sorted(range(len(times)), key=lambda i: -times[i])[:3]
     log("slowest steps: " + ", ".join(f"#{i} {times[i] * 1e3:.1f} ms ({step_tokens[i]} tokens)" for i in slow))
+    step_ms = [t * 1e3 for t in times]
+    if args.mixed_only:
+        print(json.dumps({"mixed_only": True, "value": round(value, 1), "unit": "tokens/s", "steps": args.steps,
+                          "tokens": tokens, "ms_per_step": round(total / args.steps * 1e3, 4),
+                          "latency_ms": {"p50": round(percentile(step_ms, 50), 3),
+                                         "p95": round(percentile(step_ms, 95), 3)}}), flush=True)
+        return
+
+    # ---- per-context latency: every slot restarted with one initial-context length, then timed mixed steps
+    # (resets re-prefilled at that length, untimed) ----
+    by_context = {}
+    if args.sweep_steps > 0:
+        for c in (512, 2048, 8000):
+            t0 = time.time()
+            ctx_load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed + c, contexts=(c,),
+                                        reset_p=args.reset_p)
+            eng.reset()
+            eng.step([(s, ctx_load.context()) for s in range(args.slots)])
+            torch.cuda.synchronize()
+            prefill_s = time.time() - t0
+            ts, toks = [], 0
+            for i in range(args.sweep_steps + 5):
+                req = ctx_load.step_requests()
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                eng.step(req)
+                torch.cuda.synchronize()
+                if i >= 5:
+                    ts.append((time.perf_counter() - t) * 1e3)
+                    toks += sum(len(ids) for _, ids in req)
+                gone = ctx_load.resets()
+                if gone:
+                    eng.reset(gone)
+                    eng.step([(s, ctx_load.context()) for s in gone])
+            by_context[str(c)] = {"steps": len(ts), "tokens_per_s": round(toks / (sum(ts) / 1e3), 1),
+                                  "p50": round(percentile(ts, 50), 3), "p95": round(percentile(ts, 95), 3)}
+            log(f"context {c}: {by_context[str(c)]} (prefill {prefill_s:.1f}s)")
 
     # ---- pure decode: 352 x 1 token, and 1 slot x 1 token (20 warm-up + 200 measured) ----
     def timed(make, n=200, warm=20):
@@ -347,7 +396,6 @@ def main():
         cpu = cpu_baseline(model, cfg, seed=args.seed)
         log(f"cpu baseline {cpu} in {time.time() - t0:.1f}s")
 
-    step_ms = [t * 1e3 for t in times]
     result = {
         "metric": "stream tokens/s @352 slots + p50/p95 single-token step latency (ms)",
         "value": round(value, 1),
@@ -368,6 +416,7 @@ def main():
                                "MLP 3584, vocab 151936", "parallelism": "none (1 GPU)"},
         "latency_ms": {"p50": round(percentile(step_ms, 50), 3), "p95": round(percentile(step_ms, 95), 3),
                        "max": round(max(step_ms), 3)},
+        "latency_by_context_ms": by_context,
         "decode_352x1_ms": {"p50": round(percentile(dec, 50), 3), "p95": round(percentile(dec, 95), 3),
                             "tokens_per_s": round(args.slots / (np.mean(dec) / 1e3), 1)},
         "single_token_ms": {"p50": round(percentile(one, 50), 3), "p95": round(percentile(one, 95), 3)},
