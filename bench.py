@@ -157,14 +157,17 @@ def chunk_prefill_rate(torch, iters=10):
     from hs_guard.engine.kernels import gdn_chunk_prefill
     from hs_guard.synthetic import chunk_prefill_inputs
     H, K = 16, 128
+    from hs_guard._lib import lib
     inp = chunk_prefill_inputs(rows=16)
     d = {k: (v.to("cuda:0") if torch.is_tensor(v) else v) for k, v in inp.items()}
     slots = torch.arange(16, device="cuda:0")
     stream = torch.cuda.current_stream()
+    max_len = int(inp["lens"].max())
+    ws = torch.empty(lib().hsg_gdn_chunk_workspace_bytes(16, max_len, H), dtype=torch.uint8, device="cuda:0")
 
     def run():
         gdn_chunk_prefill(d["packed"], H * K, H, K, H, K, d["a"], d["b"], d["A_log"], d["dt_bias"], d["state0"],
-                          slots, d["lens"], d["offsets"])
+                          slots, d["lens"], d["offsets"], max_len=max_len, workspace=ws)
     for _ in range(2):
         run()
     torch.cuda.synchronize()

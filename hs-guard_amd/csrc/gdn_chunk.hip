@@ -1,4 +1,4 @@
-// Chunked gated-delta-rule prefill for gfx950 (WY/UT chunk form on MFMA).
+// Chunked gated-delta-rule prefill for gfx950 (WY/UT chunk form on MFMA), as two kernels.
 //
 // Same recurrence as the slot step (src/hs_guard/engine/fused_kernels.py:166-188), evaluated 64 tokens at a
 // time in the chunk form behind FLA's chunk_gated_delta_rule (called at src/hs_guard/runtime.py:80-89 and
@@ -6,24 +6,34 @@
 // per chunk, with G_i the in-chunk cumulative log-decay, raw bf16 rows Kr, Qr, Vr and the per-token l2-norm
 // factors rk, rq (rq includes the K^-1/2 scale):
 //   A[i,j]  = beta_i rk_i rk_j e^(G_i-G_j) (Kr Kr^T)[i,j]        j < i
-//   V'      = (I + A)^-1 (beta . Vr - beta e^G rk . (Kr S))       (forward substitution in 16-token blocks)
+//   M'      = (I + A)^-1 diag(beta)
+//   V'      = M' (Vr - e^G rk . (Kr S))                          (= (I + A)^-1 (beta Vr - beta e^G rk Kr S))
 //   O       = rq e^G . (Qr S) + P V',   P[i,j] = rq_i rk_j e^(G_i-G_j) (Qr Kr^T)[i,j]   j <= i
 //   S       <- e^(G_C) S + Kr^T (rk e^(G_C-G) . V')
 // which is the recurrence unrolled over the chunk (v'_t is the rule's beta (v - S^T k) with the decays
 // applied in order).
 //
-// Mapping: one workgroup (4 waves) per (row, value head, 64-column value block); wave w owns value columns
-// [16w, 16w+16) of the block and keeps S[:, those columns] (128 x 16 fp32) in MFMA accumulator layout for the
-// whole sequence, so the state is read once and written once per call. The accumulator layout of a 16-row
-// block (lane l: column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of v_mfma_f32_16x16x16_bf16,
-// so S, the substitution's right-hand sides and V' feed the next product from registers; pairs of 16-row
-// blocks feed v_mfma_f32_16x16x32_bf16 by ordering its 32 reduction slots as (4 rows of block J, 4 rows of
-// block J+1) per lane, with the A operand read in the same order.
-// Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, -A, the diagonal
-// inverses, right-hand sides, V', Z) is split into bf16 hi + lo and multiplied in three passes (hi.hi + hi.lo
-// + lo.hi, error ~2^-16 relative), so the state keeps fp32-level accuracy; the diagonal 16 x 16 inverses are
-// fp32 forward substitution. -A, P and the inverses are written to LDS already split, once per workgroup.
-// Two code-generation rules this kernel keeps on gfx950:
+// Only the last three lines involve the state. gdn_chunk_prep_kernel computes everything else for every
+// (row, chunk, value head) at once, in parallel: M' and P as bf16 hi / lo planes and the per-token factors
+// e^G rk, rq e^G, rk e^(G_C-G) and e^(G_C), into a workspace. gdn_chunk_state_kernel then walks each row's
+// chunks in order with only the state products on its chain: per chunk Y = Kr S and Qr S, Z = Vr - e^G rk . Y,
+// V' = M' Z (no substitution chain: M' is explicit), O, and the state update.
+//
+// Prep mapping: one workgroup (4 waves) per (row, chunk, value head). Kr Kr^T and Qr Kr^T on 16 x 16 tiles,
+// scaled into -A (LDS) and P (workspace); the four diagonal 16 x 16 blocks of I + A are inverted by fp32
+// forward substitution; wave w then solves (I + A) M[:, 16w..16w+16) = I[:, 16w..] block by block, so the
+// inverse is explicit, and scales its columns by beta.
+// State mapping: one workgroup (4 waves) per (row, value head, 64-column value block); wave w owns value
+// columns [16w, 16w+16) of the block and keeps S[:, those columns] (128 x 16 fp32) in MFMA accumulator layout
+// for the whole sequence, so the state is read once and written once per call. The accumulator layout of a
+// 16-row block (lane l: column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of
+// v_mfma_f32_16x16x16_bf16, so S, Z and V' feed the next product from registers; pairs of 16-row blocks feed
+// v_mfma_f32_16x16x32_bf16 by ordering its 32 reduction slots as (4 rows of block J, 4 rows of block J+1) per
+// lane, with the A operand read in the same order.
+// Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, -A, M', P, the
+// diagonal inverses, Z, V') is split into bf16 hi + lo and multiplied in three passes (hi.hi + hi.lo + lo.hi,
+// error ~2^-16 relative), or two when the other operand is exact bf16, so the state keeps fp32-level accuracy.
+// Two code-generation rules these kernels keep on gfx950:
 //   * one MFMA accumulation chain uses one MFMA shape: a 16x16x16 product accumulating directly onto the
 //     result of a 16x16x32 product lost part of that result (found by bisecting a wrong output), so odd
 //     blocks are zero-padded 16x16x32 products;
@@ -41,13 +51,23 @@ constexpr int VD = 128;
 constexpr int CH = 64;             // tokens per chunk
 constexpr int BV = 64;             // value columns per workgroup
 constexpr int KS = KD + 8;         // Ks / Qs row stride (bf16): token-major rows of keys
-constexpr int TS = CH + 4;         // KTs / VT row stride (bf16): key- / value-major rows of tokens
+constexpr int TS = CH + 4;         // row stride (bf16) of the 64-column LDS planes (M', P, -A)
+constexpr int VS = BV + 8;         // Vs row stride (bf16): token-major rows of the block's values
 constexpr int DS = 20;             // diagonal-block row stride (fp32) and diagonal-inverse row stride (bf16)
+constexpr int PL = CH * TS;        // one 64 x 64 bf16 plane of the workspace, rows padded to TS (the LDS layout)
+constexpr int VEC = 256;           // per-token factor floats of a workspace unit: e^G rk, rq e^G, rk e^(G_C-G),
+                                   // then e^(G_C) and padding
+// one workspace unit per (row, chunk, value head): planes M'hi, M'lo, Phi, Plo, then the factors
+constexpr int PLANE_PIECES = 4 * PL * 2 / 16;   // 16-byte pieces of the four planes (2176)
+constexpr int UNIT_BYTES = 4 * PL * 2 + VEC * 4;
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) short s16x8;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+// 16-byte prefetch buffers are native vectors: a HIP uint4 copied whole into LDS is a struct memcpy that the
+// compiler cannot keep in registers (it parked such a buffer in LDS and waited for its loads at issue)
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
 struct ChunkParams {
   const uint16_t* qkv;
@@ -65,9 +85,11 @@ struct ChunkParams {
   const int64_t* offsets;
   int L, H, HV;
   int pairs;                       // n_rows * HV
+  int max_chunks;                  // ceil(L / CH): workspace units per (row, value head)
   float scale;
   uint16_t* o;
   float* sq;
+  uint8_t* ws;
 };
 
 __device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
@@ -98,18 +120,20 @@ __device__ __forceinline__ s16x4 ld4h(const uint16_t* p) { return *reinterpret_c
 
 // acc += sum_{J < NJ} M[row block I][col block J] . B_J for a matrix M kept in LDS as bf16 hi / lo planes, read
 // at hrow = &Mh[16I + m][4 g], lrow = &Ml[16I + m][4 g] (lane m = l%16, g = l/16); B_J are split bf16 pairs in
-// B layout. Three passes per product (hi.hi + hi.lo + lo.hi).
-template <int NJ>
+// B layout. Three passes per product (hi.hi + hi.lo + lo.hi). TR: the same operands with the MFMA operand
+// order swapped, which yields the transposed product (sum_J B_J^T M_IJ^T) in accumulator layout.
+template <int NJ, bool TR = false>
 __device__ __forceinline__ f32x4 split_product(const uint16_t* hrow, const uint16_t* lrow, const s16x4* bh,
                                                const s16x4* bl, f32x4 acc) {
+  auto mm = [](s16x8 m, s16x8 b, f32x4 c) { return TR ? mma32(b, m, c) : mma32(m, b, c); };
 #pragma unroll
   for (int J = 0; J + 1 < NJ; J += 2) {
     const s16x8 ah = cat(ld4h(hrow + 16 * J), ld4h(hrow + 16 * J + 16));
     const s16x8 al = cat(ld4h(lrow + 16 * J), ld4h(lrow + 16 * J + 16));
     const s16x8 b_h = cat(bh[J], bh[J + 1]), b_l = cat(bl[J], bl[J + 1]);
-    acc = mma32(al, b_h, acc);
-    acc = mma32(ah, b_l, acc);
-    acc = mma32(ah, b_h, acc);
+    acc = mm(al, b_h, acc);
+    acc = mm(ah, b_l, acc);
+    acc = mm(ah, b_h, acc);
   }
   if constexpr (NJ % 2 == 1) {
     // the odd block rides in a 16x16x32 product with zero upper k-slots: one accumulation chain never mixes
@@ -118,9 +142,9 @@ __device__ __forceinline__ f32x4 split_product(const uint16_t* hrow, const uint1
     const s16x4 z = {0, 0, 0, 0};
     const s16x8 ah = cat(ld4h(hrow + 16 * J), z), al = cat(ld4h(lrow + 16 * J), z);
     const s16x8 b_h = cat(bh[J], z), b_l = cat(bl[J], z);
-    acc = mma32(al, b_h, acc);
-    acc = mma32(ah, b_l, acc);
-    acc = mma32(ah, b_h, acc);
+    acc = mm(al, b_h, acc);
+    acc = mm(ah, b_l, acc);
+    acc = mm(ah, b_h, acc);
   }
   return acc;
 }
@@ -141,6 +165,14 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// LDS transpose read (ds_read_b64_tr_b16): within each group of 16 lanes, lane 4q + e receives element e of
+// the 4-element (8-byte) vectors addressed by lanes q, q + 4, q + 8, q + 12 of its group. With a row-major
+// tile, lane s of a group addressing row r0 + (s >> 2), columns c0 + 4 (s & 3) .. +3 therefore receives
+// column c0 + s of rows r0 .. r0 + 3: the MFMA operand layout of the transposed tile.
+__device__ __forceinline__ s16x4 ld4h_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
 template <typename ST>
 __device__ __forceinline__ float load_state(const ST* p);
 template <>
@@ -150,14 +182,273 @@ __device__ __forceinline__ float load_state<uint16_t>(const uint16_t* p) { retur
 __device__ __forceinline__ void store_state(float* p, float x) { *p = x; }
 __device__ __forceinline__ void store_state(uint16_t* p, float x) { *p = f2h(x); }
 
+// Tokens of row n (0 for a slot outside the pool or a rejected row) and the row's first token.
+// Padded layout: at most L tokens; packed layout: rows longer than L are rejected (L sizes the workspace).
+__device__ __forceinline__ int row_tokens(const ChunkParams& p, int n, int64_t& slot, int64_t& tok0) {
+  slot = p.slots[n];
+  const int64_t len = p.lens[n];
+  const bool padded = p.offsets == nullptr;
+  tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
+  if (slot < 0 || slot >= p.state_rows || len <= 0) return 0;
+  if (padded) return (int)min(len, (int64_t)p.L);
+  return len > p.L ? 0 : (int)len;
+}
+
+__device__ __forceinline__ uint8_t* unit_ptr(const ChunkParams& p, int n, int c, int hv) {
+  return p.ws + (((int64_t)n * p.max_chunks + c) * p.HV + hv) * (int64_t)UNIT_BYTES;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Prep: M' = (I + A)^-1 diag(beta), P and the per-token factors of one (row, chunk, value head).
+// ---------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int bid = blockIdx.x;
+  const int hv = bid % p.HV;
+  const int nc = bid / p.HV;
+  const int c = nc % p.max_chunks;
+  const int n = nc / p.max_chunks;
+  int64_t slot, tok0;
+  const int ntok = row_tokens(p, n, slot, tok0);
+  const int c0 = c * CH;
+  if (c0 >= ntok) return;
+  const int nv = min(CH, ntok - c0);
+  const int h = hv / (p.HV / p.H);
+  uint8_t* unit = unit_ptr(p, n, c, hv);
+  uint16_t* Mh_g = reinterpret_cast<uint16_t*>(unit);   // M'hi, then M'lo at + PL
+  uint16_t* Ph_g = Mh_g + 2 * PL;
+  uint16_t* Pl_g = Mh_g + 3 * PL;
+  float* vec_g = reinterpret_cast<float*>(unit + 4 * PL * 2);
+
+  // Ks is reused for the M' output planes and Qs for -A once the Gram tiles are done (a barrier apart)
+  __shared__ __align__(16) uint16_t Ks[CH * KS];
+  __shared__ __align__(16) uint16_t Qs[CH * KS];
+  uint16_t* const Ah = Qs;                                       // -A (strictly lower), bf16 hi / lo
+  uint16_t* const Al = Qs + CH * TS;
+  __shared__ __align__(16) float Dg[4 * 16 * DS];                // fp32 diagonal 16 x 16 blocks of -A
+  __shared__ __align__(16) uint16_t Th[CH * DS], Tl[CH * DS];    // their inverses (rows 16w + i of block w)
+  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], G_s[CH], fa_s[CH];
+
+  // ---- stage token st_t: raw K, Q rows into LDS, l2-norm factors, gates. Past the row's end the chunk's
+  // first token is read instead and its zero beta, rk and rq cancel it everywhere. ----
+  const int st_t = 16 * wave + m16;
+  const uint16_t A_raw = p.A_log[hv], dt_raw = p.dt_bias[hv];   // issued with the token loads
+  {
+    const int64_t tok = tok0 + c0 + (st_t < nv ? st_t : 0);
+    const uint16_t* row = p.qkv + tok * p.qkv_stride;
+    uint4 pk[4], pq[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int pc = 8 * (g4 + 4 * it);
+      pk[it] = *reinterpret_cast<const uint4*>(row + p.k_off + h * KD + pc);
+      pq[it] = *reinterpret_cast<const uint4*>(row + p.q_off + h * KD + pc);
+    }
+    const uint16_t pa = p.a[tok * p.ab_stride + hv];
+    const uint16_t pb = p.b[tok * p.ab_stride + hv];
+    float kk = 0.f, qq = 0.f;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int pc = 8 * (g4 + 4 * it);
+      *reinterpret_cast<uint4*>(&Ks[st_t * KS + pc]) = pk[it];
+      *reinterpret_cast<uint4*>(&Qs[st_t * KS + pc]) = pq[it];
+      const uint32_t kw[4] = {pk[it].x, pk[it].y, pk[it].z, pk[it].w};
+      const uint32_t qw[4] = {pq[it].x, pq[it].y, pq[it].z, pq[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x0, x1, y0, y1;
+        unpack2(kw[e], x0, x1);
+        unpack2(qw[e], y0, y1);
+        kk += x0 * x0 + x1 * x1;
+        qq += y0 * y0 + y1 * y1;
+      }
+    }
+    kk = xor_add<16>(kk);
+    kk = xor_add<32>(kk);
+    qq = xor_add<16>(qq);
+    qq = xor_add<32>(qq);
+    if (g4 == 0) {
+      const bool ok = st_t < nv;
+      rk_s[st_t] = ok ? 1.0f / sqrtf(kk + 1e-6f) : 0.f;
+      rq_s[st_t] = ok ? p.scale / sqrtf(qq + 1e-6f) : 0.f;
+      const float A = expf(bf2f(A_raw));
+      const float x = bf2f(pa) + bf2f(dt_raw);
+      g_s[st_t] = ok ? -A * (x > 20.0f ? x : logf(1.0f + expf(x))) : 0.f;
+      b_s[st_t] = ok ? sigmoidf_(bf2f(pb)) : 0.f;
+    }
+  }
+  lds_barrier();
+
+  // ---- in-chunk cumulative decay and the per-token factors (wave 0) ----
+  if (wave == 0) {
+    float x = g_s[lane];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const float y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    const float GC = __shfl(x, 63, 64);
+    const float eg = exp_nonpos(x);
+    G_s[lane] = x;
+    fa_s[lane] = b_s[lane] * rk_s[lane];
+    vec_g[lane] = eg * rk_s[lane];
+    vec_g[CH + lane] = rq_s[lane] * eg;
+    vec_g[2 * CH + lane] = rk_s[lane] * exp_nonpos(GC - x);
+    vec_g[3 * CH + lane] = lane == 0 ? exp_nonpos(GC) : 0.f;
+  }
+
+  // ---- Kr Kr^T and Qr Kr^T on the 10 lower 16 x 16 tiles each; tile u of wave w is number w + 4u. Each
+  // tile is computed transposed (operands swapped), so a lane holds row 16 I + m16, columns 16 J + 4 g4 .. +3 ----
+  f32x4 gt[5];
+#pragma unroll
+  for (int u = 0; u < 5; ++u) {
+    const int tau = wave + 4 * u;
+    const bool qk = tau >= 10;
+    const int idx = qk ? tau - 10 : tau;
+    const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
+    const int J = idx - I * (I + 1) / 2;
+    const uint16_t* arow = (qk ? Qs : Ks) + (16 * I + m16) * KS + 8 * g4;
+    const uint16_t* brow = Ks + (16 * J + m16) * KS + 8 * g4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      acc = mma32(*reinterpret_cast<const s16x8*>(brow + 32 * ks), *reinterpret_cast<const s16x8*>(arow + 32 * ks),
+                  acc);
+    gt[u] = acc;
+  }
+  lds_barrier();  // per-token factors are in LDS; Qs is free for -A
+
+  // ---- scale the Gram tiles into -A (LDS) and P (workspace). Only P's diagonal tiles need the causal mask:
+  // the substitution reads A's off-diagonal tiles only and the diagonal inverses read below the diagonal only;
+  // P's tiles above the diagonal are never read. ----
+  {
+    float fr[5], Gr[5];
+    f32x4 rkc[5], Gc[5];
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+      const int tau = wave + 4 * u;
+      const bool qk = tau >= 10;
+      const int idx = qk ? tau - 10 : tau;
+      const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
+      const int J = idx - I * (I + 1) / 2;
+      const int i = 16 * I + m16;
+      const int j0 = 16 * J + 4 * g4;
+      fr[u] = qk ? rq_s[i] : fa_s[i];
+      Gr[u] = G_s[i];
+      rkc[u] = ld4f(&rk_s[j0]);
+      Gc[u] = ld4f(&G_s[j0]);
+    }
+#pragma unroll
+    for (int u = 0; u < 5; ++u) {
+      const int tau = wave + 4 * u;
+      const bool qk = tau >= 10;
+      const int idx = qk ? tau - 10 : tau;
+      const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
+      const int J = idx - I * (I + 1) / 2;
+      const int i = 16 * I + m16;
+      const int j0 = 16 * J + 4 * g4;
+      f32x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[r] = fr[u] * rkc[u][r] * exp_nonpos(fminf(Gr[u] - Gc[u][r], 0.f)) * gt[u][r];
+        // inside a diagonal tile of P keep row >= column (sign bit of column - row - 1)
+        if (qk && I == J) v[r] *= (float)((uint32_t)((4 * g4 + r) - m16 - 1) >> 31);
+      }
+      s16x4 vh, vl;
+      split4(qk ? v : -v, vh, vl);
+      if (!qk) {
+        *reinterpret_cast<s16x4*>(&Ah[i * TS + j0]) = vh;
+        *reinterpret_cast<s16x4*>(&Al[i * TS + j0]) = vl;
+        if (I == J) *reinterpret_cast<f32x4*>(&Dg[i * DS + 4 * g4]) = -v;
+      } else {
+        *reinterpret_cast<s16x4*>(&Ph_g[i * TS + j0]) = vh;
+        *reinterpret_cast<s16x4*>(&Pl_g[i * TS + j0]) = vl;
+      }
+    }
+  }
+  lds_barrier();  // -A and its diagonal blocks are complete
+
+  // ---- wave w inverts diagonal block w of (I + A) by fp32 forward substitution (lane m16 = column) ----
+  {
+    const float* nb = Dg + (16 * wave) * DS;   // -A of the block
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s0 = (i == m16) ? 1.f : 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+      for (int k = 0; k < i; ++k) {
+        const float a = nb[i * DS + k];
+        if ((k & 3) == 0) s0 += a * t[k];
+        else if ((k & 3) == 1) s1 += a * t[k];
+        else if ((k & 3) == 2) s2 += a * t[k];
+        else s3 += a * t[k];
+      }
+      t[i] = (s0 + s1) + (s2 + s3);
+    }
+    // every lane group computed the same column; group g4 writes rows 4 g4 .. 4 g4 + 3 of it
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ti = g4 == 0 ? t[i] : g4 == 1 ? t[4 + i] : g4 == 2 ? t[8 + i] : t[12 + i];
+      store_split(&Th[(wave * 16 + 4 * g4 + i) * DS + m16], &Tl[(wave * 16 + 4 * g4 + i) * DS + m16], ti);
+    }
+  }
+  lds_barrier();  // diagonal inverses are complete
+
+  // ---- M_I = T_II (E_I - sum_{J<I} A_IJ M_J) for this wave's columns 16w + m16 (E = identity), then
+  // M' = M diag(beta), transposed through LDS (the Ks area) into 16-byte stores to the workspace ----
+  uint16_t* const Mh_s = Ks;
+  uint16_t* const Ml_s = Ks + CH * TS;
+  {
+    const float bcol = b_s[16 * wave + m16];
+    s16x4 Mh[4], Ml[4];
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const int arow = (16 * I + m16) * TS + 4 * g4;
+      if (I == 1) acc = split_product<1>(Ah + arow, Al + arow, Mh, Ml, acc);
+      if (I == 2) acc = split_product<2>(Ah + arow, Al + arow, Mh, Ml, acc);
+      if (I == 3) acc = split_product<3>(Ah + arow, Al + arow, Mh, Ml, acc);
+      f32x4 x;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = acc[r] + ((I == wave && 4 * g4 + r == m16) ? 1.f : 0.f);
+      s16x4 xh, xl;
+      split4(x, xh, xl);
+      const s16x4 th = ld4h(&Th[(I * 16 + m16) * DS + 4 * g4]), tl = ld4h(&Tl[(I * 16 + m16) * DS + 4 * g4]);
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      v = mma16(tl, xh, v);
+      v = mma16(th, xl, v);
+      v = mma16(th, xh, v);
+      split4(v, Mh[I], Ml[I]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int at = (16 * I + 4 * g4 + r) * TS + 16 * wave + m16;
+        store_split(&Mh_s[at], &Ml_s[at], v[r] * bcol);
+      }
+    }
+  }
+  lds_barrier();
+  // the two planes are contiguous in LDS and in the workspace with the same padded rows: a linear copy
+#pragma unroll
+  for (int i = 0; i < (2 * PL * 2 / 16 + 255) / 256; ++i) {
+    const int x = threadIdx.x + 256 * i;
+    if (x < 2 * PL * 2 / 16)
+      reinterpret_cast<u32x4*>(Mh_g)[x] = reinterpret_cast<const u32x4*>(Mh_s)[x];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// State: walks one row's chunks in order for one value head and 64 value columns.
+// ---------------------------------------------------------------------------------------------------------
 template <typename ST>
-__global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(256) void gdn_chunk_state_kernel(const ChunkParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m16 = lane & 15;
   const int g4 = lane >> 4;
   // the two value blocks of one (row, head) are dispatched 8 workgroups apart, i.e. on the same XCD, so
-  // their identical K / Q chunk reads share that XCD's L2
+  // their identical K / Q / workspace reads share that XCD's L2
   const int bid = blockIdx.x;
   const int vb = (bid >> 3) & 1;
   const int pair = ((bid >> 4) << 3) | (bid & 7);
@@ -165,12 +456,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
   const int n = pair / p.HV;
   const int hv = pair - n * p.HV;
   const int h = hv / (p.HV / p.H);
-  const int64_t slot = p.slots[n];
-  int ntok = (int)p.lens[n];
+  int64_t slot, tok0;
+  const int ntok = row_tokens(p, n, slot, tok0);
   const bool padded = p.offsets == nullptr;
-  if (slot < 0 || slot >= p.state_rows || ntok < 0) ntok = 0;
-  if (padded && ntok > p.L) ntok = p.L;
-  const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
   const int vcol = vb * BV + wave * 16 + m16;          // this lane's value column (accumulator layout)
   const int64_t ostride = (int64_t)p.HV * VD;
 
@@ -183,16 +471,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
   }
   if (ntok == 0) return;
 
+  // token-major K, Q and V tiles; K^T and the token-column V fragments are read with transpose reads
   __shared__ __align__(16) uint16_t Ks[CH * KS];
   __shared__ __align__(16) uint16_t Qs[CH * KS];
-  __shared__ __align__(16) uint16_t KTs[KD * TS];
-  __shared__ __align__(16) uint16_t VT[BV * TS];
-  // -A (strictly lower) and P (lower incl. diagonal) as bf16 hi / lo planes, token-major rows
-  __shared__ __align__(16) uint16_t Ah[CH * TS], Al[CH * TS], Ph[CH * TS], Pl[CH * TS];
-  __shared__ __align__(16) float Dg[4 * 16 * DS];                // fp32 diagonal 16 x 16 blocks of A
-  __shared__ __align__(16) uint16_t Th[CH * DS], Tl[CH * DS];    // their inverses (rows 16w + i of block w)
-  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], c1_s[CH], d_s[CH], qe_s[CH], G_s[CH], fa_s[CH];
-  __shared__ float gc_s;
+  __shared__ __align__(16) uint16_t Vs[CH * VS];
+  // M' and P (lower triangles) as bf16 hi / lo planes, token-major rows: plane e at Pn[e * CH * TS]
+  __shared__ __align__(16) uint16_t Pn[4 * CH * TS];
+  __shared__ __align__(16) float vec_s[VEC];
 
   // ---- state S[:, vcol] in accumulator layout: block mt holds keys 16 mt + 4 g4 + r ----
   ST* sbase = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * (int64_t)KD) * VD + vcol;
@@ -202,122 +487,84 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) S[mt][r] = load_state<ST>(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD);
 
-  const float A = expf(bf2f(p.A_log[hv]));
-  const float dt = bf2f(p.dt_bias[hv]);
-
   // ---- staging coordinates: token st_t of the chunk; 16-byte pieces g4 + 4 it ----
   const int st_t = 16 * wave + m16;
-  uint4 pk[4], pq[4], pv[2];
-  uint16_t pa = 0, pb = 0;   // raw bf16: converting here would make every prefetch wait for its loads
+  constexpr int PM = (PLANE_PIECES + 255) / 256;   // plane pieces per thread (the last partly idle)
+  u32x4 pk[4], pq[4], pv[2], pm[PM];
+  float pf;
   // Loads are unconditional: a position past the row's end reads the row's first token instead, and its
-  // zero beta, rk and rq factors (set at staging) cancel it everywhere, so no select can turn into a
-  // memory-backed zero or a branch around the loads.
-  auto fetch = [&](int c0) {
-    const int64_t tok = tok0 + (c0 + st_t < ntok ? c0 + st_t : 0);
-    const uint16_t* row = p.qkv + tok * p.qkv_stride;
+  // zero factors (rk, rq, and the zero columns of M' and P) cancel it everywhere, so no select can turn into
+  // a memory-backed zero or a branch around the loads. The prefetch of the next chunk is issued in four
+  // groups between this chunk's compute phases (pinned there by scheduling barriers): issued at once, its
+  // ~900 cache lines per CU stalled instruction issue for about one memory round trip.
+  auto row_of = [&](int c0) { return p.qkv + (tok0 + (c0 + st_t < ntok ? c0 + st_t : 0)) * p.qkv_stride; };
+  auto fetch_kq = [&](const uint16_t* row) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int pc = 8 * (g4 + 4 * it);
-      pk[it] = *reinterpret_cast<const uint4*>(row + p.k_off + h * KD + pc);
-      pq[it] = *reinterpret_cast<const uint4*>(row + p.q_off + h * KD + pc);
+      pk[it] = *reinterpret_cast<const u32x4*>(row + p.k_off + h * KD + pc);
+      pq[it] = *reinterpret_cast<const u32x4*>(row + p.q_off + h * KD + pc);
     }
+  };
+  auto fetch_v = [&](const uint16_t* row, const uint8_t* unit) {
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
       const int pc = 8 * (g4 + 4 * it);
-      pv[it] = *reinterpret_cast<const uint4*>(row + p.v_off + hv * VD + vb * BV + pc);
+      pv[it] = *reinterpret_cast<const u32x4*>(row + p.v_off + hv * VD + vb * BV + pc);
     }
-    pa = p.a[tok * p.ab_stride + hv];
-    pb = p.b[tok * p.ab_stride + hv];
+    pf = reinterpret_cast<const float*>(unit + 4 * PL * 2)[threadIdx.x];
+  };
+  // piece x = threadIdx.x + 256 i of the planes, clamped to the last piece (re-read, never written twice)
+  auto fetch_planes = [&](const uint8_t* unit, int half) {
+    const u32x4* planes = reinterpret_cast<const u32x4*>(unit);
+#pragma unroll
+    for (int i = half ? PM / 2 : 0; i < (half ? PM : PM / 2); ++i)
+      pm[i] = planes[min((int)threadIdx.x + 256 * i, PLANE_PIECES - 1)];
   };
 
-  fetch(0);
+  {
+    const uint16_t* row = row_of(0);
+    const uint8_t* unit = unit_ptr(p, n, 0, hv);
+    fetch_kq(row);
+    fetch_v(row, unit);
+    fetch_planes(unit, 0);
+    fetch_planes(unit, 1);
+  }
   for (int c0 = 0; c0 < ntok; c0 += CH) {
     const int nv = min(CH, ntok - c0);
     lds_barrier();  // every read of the previous chunk's LDS data is done
     {
-      float kk = 0.f, qq = 0.f;
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int pc = 8 * (g4 + 4 * it);
-        *reinterpret_cast<uint4*>(&Ks[st_t * KS + pc]) = pk[it];
-        *reinterpret_cast<uint4*>(&Qs[st_t * KS + pc]) = pq[it];
-        const uint32_t kw[4] = {pk[it].x, pk[it].y, pk[it].z, pk[it].w};
-        const uint32_t qw[4] = {pq[it].x, pq[it].y, pq[it].z, pq[it].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          KTs[(pc + 2 * e) * TS + st_t] = (uint16_t)(kw[e] & 0xffffu);
-          KTs[(pc + 2 * e + 1) * TS + st_t] = (uint16_t)(kw[e] >> 16);
-          float x0, x1, y0, y1;
-          unpack2(kw[e], x0, x1);
-          unpack2(qw[e], y0, y1);
-          kk += x0 * x0 + x1 * x1;
-          qq += y0 * y0 + y1 * y1;
-        }
+        *reinterpret_cast<u32x4*>(&Ks[st_t * KS + pc]) = pk[it];
+        *reinterpret_cast<u32x4*>(&Qs[st_t * KS + pc]) = pq[it];
       }
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int pc = 8 * (g4 + 4 * it);
-        const uint32_t vw[4] = {pv[it].x, pv[it].y, pv[it].z, pv[it].w};
+      for (int it = 0; it < 2; ++it) *reinterpret_cast<u32x4*>(&Vs[st_t * VS + 8 * (g4 + 4 * it)]) = pv[it];
+      // the workspace planes already have the LDS layout: a linear copy
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          VT[(pc + 2 * e) * TS + st_t] = (uint16_t)(vw[e] & 0xffffu);
-          VT[(pc + 2 * e + 1) * TS + st_t] = (uint16_t)(vw[e] >> 16);
-        }
+      for (int i = 0; i < PM; ++i) {
+        const int x = threadIdx.x + 256 * i;
+        if (x < PLANE_PIECES) reinterpret_cast<u32x4*>(Pn)[x] = pm[i];
       }
-      kk = xor_add<16>(kk);
-      kk = xor_add<32>(kk);
-      qq = xor_add<16>(qq);
-      qq = xor_add<32>(qq);
-      if (g4 == 0) {
-        const bool ok = st_t < nv;
-        rk_s[st_t] = ok ? 1.0f / sqrtf(kk + 1e-6f) : 0.f;
-        rq_s[st_t] = ok ? p.scale / sqrtf(qq + 1e-6f) : 0.f;
-        const float x = bf2f(pa) + dt;
-        g_s[st_t] = ok ? -A * (x > 20.0f ? x : logf(1.0f + expf(x))) : 0.f;
-        b_s[st_t] = ok ? sigmoidf_(bf2f(pb)) : 0.f;
-      }
+      vec_s[threadIdx.x] = pf;
     }
-    if (c0 + CH < ntok) fetch(c0 + CH);  // next chunk's loads stay in flight during this chunk's math
+    // the next chunk (or this one again after the last: harmless loads whose results are never used)
+    const int cn = c0 + CH < ntok ? c0 + CH : c0;
+    const uint16_t* nrow = row_of(cn);
+    const uint8_t* nunit = unit_ptr(p, n, cn / CH, hv);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_kq(nrow);
+    __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
+    const uint16_t* Mh = Pn;
+    const uint16_t* Ml = Pn + CH * TS;
+    const uint16_t* Ph = Pn + 2 * CH * TS;
+    const uint16_t* Pl = Pn + 3 * CH * TS;
 
-    // ---- in-chunk cumulative decay and per-token factors (wave 0) ----
-    if (wave == 0) {
-      float x = g_s[lane];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(x, d, 64);
-        if (lane >= d) x += y;
-      }
-      const float GC = __shfl(x, 63, 64);
-      const float eg = exp_nonpos(x);
-      G_s[lane] = x;
-      c1_s[lane] = b_s[lane] * eg * rk_s[lane];
-      fa_s[lane] = b_s[lane] * rk_s[lane];
-      d_s[lane] = rk_s[lane] * exp_nonpos(GC - x);
-      qe_s[lane] = rq_s[lane] * eg;
-      if (lane == 0) gc_s = exp_nonpos(GC);
-    }
-
-    // ---- Kr Kr^T and Qr Kr^T on the 10 lower 16 x 16 tiles each; tile u of wave w is number w + 4u ----
-    f32x4 gt[5];
-#pragma unroll
-    for (int u = 0; u < 5; ++u) {
-      const int tau = wave + 4 * u;
-      const bool qk = tau >= 10;
-      const int idx = qk ? tau - 10 : tau;
-      const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
-      const int J = idx - I * (I + 1) / 2;
-      const uint16_t* arow = (qk ? Qs : Ks) + (16 * I + m16) * KS + 8 * g4;
-      const uint16_t* brow = Ks + (16 * J + m16) * KS + 8 * g4;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc = mma32(*reinterpret_cast<const s16x8*>(arow + 32 * ks), *reinterpret_cast<const s16x8*>(brow + 32 * ks),
-                    acc);
-      gt[u] = acc;
-    }
-
-    // ---- Y = Kr S and QS = Qr S for this wave's 16 columns (S split hi / lo, key blocks paired) ----
+    // ---- Y = Kr S (token rows) and QS^T = S^T Qr^T (value rows, token columns) for this wave's 16 value
+    // columns: S split hi / lo, key blocks paired; QS^T is the same products with the operands swapped ----
     s16x4 Sh[8], Sl[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) split4(S[mt], Sh[mt], Sl[mt]);
@@ -334,163 +581,94 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
         const s16x8 sh = cat(Sh[2 * q2], Sh[2 * q2 + 1]), sl = cat(Sl[2 * q2], Sl[2 * q2 + 1]);
         y = mma32(ka, sl, y);
         y = mma32(ka, sh, y);
-        qs = mma32(qa, sl, qs);
-        qs = mma32(qa, sh, qs);
+        qs = mma32(sl, qa, qs);
+        qs = mma32(sh, qa, qs);
       }
       Y[I] = y;
       QS[I] = qs;
     }
-    lds_barrier();  // per-token factors are in LDS
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_v(nrow, nunit);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- scale the Gram tiles into -A and P. Only P's diagonal tiles need the causal mask: the substitution
-    // reads A's off-diagonal tiles only and the diagonal inverses read below the diagonal only. ----
-    {
-      f32x4 fr[5], Gr[5];
-      float rkc[5], Gc[5];
-#pragma unroll
-      for (int u = 0; u < 5; ++u) {
-        const int tau = wave + 4 * u;
-        const bool qk = tau >= 10;
-        const int idx = qk ? tau - 10 : tau;
-        const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
-        const int J = idx - I * (I + 1) / 2;
-        const int i0 = 16 * I + 4 * g4;
-        fr[u] = ld4f(qk ? &rq_s[i0] : &fa_s[i0]);
-        Gr[u] = ld4f(&G_s[i0]);
-        rkc[u] = rk_s[16 * J + m16];
-        Gc[u] = G_s[16 * J + m16];
-      }
-#pragma unroll
-      for (int u = 0; u < 5; ++u) {
-        const int tau = wave + 4 * u;
-        const bool qk = tau >= 10;
-        const int idx = qk ? tau - 10 : tau;
-        const int I = idx >= 6 ? 3 : idx >= 3 ? 2 : idx >= 1 ? 1 : 0;
-        const int J = idx - I * (I + 1) / 2;
-        const int i0 = 16 * I + 4 * g4;
-        const int j = 16 * J + m16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = fr[u][r] * rkc[u] * exp_nonpos(fminf(Gr[u][r] - Gc[u], 0.f)) * gt[u][r];
-          if (!qk) {
-            store_split(&Ah[(i0 + r) * TS + j], &Al[(i0 + r) * TS + j], -v);
-            if (I == J) Dg[(i0 + r) * DS + m16] = -v;
-          } else {
-            // keep = 1 when row >= column inside a diagonal tile (sign bit of column - row - 1)
-            const float keep = I == J ? (float)((uint32_t)(m16 - (4 * g4 + r) - 1) >> 31) : 1.f;
-            store_split(&Ph[(i0 + r) * TS + j], &Pl[(i0 + r) * TS + j], v * keep);
-          }
-        }
-      }
-    }
-    // ---- right-hand sides R = beta . V - beta e^G rk . Y (in place in Y) ----
+    // ---- Z = Vr - e^G rk . Y, split (V[16 I + 4 g4 + r][column 16 w + m16] by a transpose read) ----
+    s16x4 Zh[4], Zl[4];
+    const uint16_t* vfrag = Vs + (4 * g4 + (m16 >> 2)) * VS + wave * 16 + 4 * (m16 & 3);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       const int i0 = 16 * I + 4 * g4;
-      const f32x4 bt = ld4f(&b_s[i0]), c1 = ld4f(&c1_s[i0]);
-      float v4[4];
-      load4_bf16(&VT[(wave * 16 + m16) * TS + i0], v4);
+      const f32x4 e1 = ld4f(&vec_s[i0]);
+      const s16x4 v4 = ld4h_tr(vfrag + 16 * I * VS);
+      f32x4 z;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Y[I][r] = bt[r] * v4[r] - c1[r] * Y[I][r];
+      for (int r = 0; r < 4; ++r) z[r] = bf2f((uint16_t)v4[r]) - e1[r] * Y[I][r];
+      split4(z, Zh[I], Zl[I]);
     }
-    lds_barrier();  // A and P are complete
 
-    // ---- wave w inverts diagonal block w of (I + A) by fp32 forward substitution (lane m16 = column) ----
-    {
-      const float* nb = Dg + (16 * wave) * DS;   // -A of the block
-      float t[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s0 = (i == m16) ? 1.f : 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll
-        for (int k = 0; k < i; ++k) {
-          const float a = nb[i * DS + k];
-          if ((k & 3) == 0) s0 += a * t[k];
-          else if ((k & 3) == 1) s1 += a * t[k];
-          else if ((k & 3) == 2) s2 += a * t[k];
-          else s3 += a * t[k];
-        }
-        t[i] = (s0 + s1) + (s2 + s3);
-      }
-      // every lane group computed the same column; group g4 writes rows 4 g4 .. 4 g4 + 3 of it
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ti = g4 == 0 ? t[i] : g4 == 1 ? t[4 + i] : g4 == 2 ? t[8 + i] : t[12 + i];
-        store_split(&Th[(wave * 16 + 4 * g4 + i) * DS + m16], &Tl[(wave * 16 + 4 * g4 + i) * DS + m16], ti);
-      }
-    }
-    lds_barrier();  // diagonal inverses are complete
-
-    // ---- V'_I = T_II (R_I - sum_{J<I} A_IJ V'_J), all in this wave's registers ----
+    // ---- V'_I = sum_{J<=I} M'_IJ Z_J (M' lower triangular) ----
     s16x4 Vh[4], Vl[4];
     f32x4 Vp[4];
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int arow = (16 * I + m16) * TS + 4 * g4;
-      if (I == 1) acc = split_product<1>(Ah + arow, Al + arow, Vh, Vl, acc);
-      if (I == 2) acc = split_product<2>(Ah + arow, Al + arow, Vh, Vl, acc);
-      if (I == 3) acc = split_product<3>(Ah + arow, Al + arow, Vh, Vl, acc);
-      const f32x4 x = Y[I] + acc;
-      s16x4 xh, xl;
-      split4(x, xh, xl);
-      const s16x4 th = ld4h(&Th[(I * 16 + m16) * DS + 4 * g4]), tl = ld4h(&Tl[(I * 16 + m16) * DS + 4 * g4]);
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      v = mma16(tl, xh, v);
-      v = mma16(th, xl, v);
-      v = mma16(th, xh, v);
-      Vp[I] = v;
-      split4(v, Vh[I], Vl[I]);
+      const int mrow = (16 * I + m16) * TS + 4 * g4;
+      if (I == 0) acc = split_product<1>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
+      if (I == 1) acc = split_product<2>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
+      if (I == 2) acc = split_product<3>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
+      if (I == 3) acc = split_product<4>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
+      Vp[I] = acc;
+      split4(acc, Vh[I], Vl[I]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_planes(nunit, 0);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- O = rq e^G . QS + P V' ----
+    // ---- O^T = (QS)^T rq e^G + V'^T P^T: lane holds value columns 4 g4 .. 4 g4 + 3 of token 16 I + m16, so
+    // each lane writes one 8-byte piece per token tile ----
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      const int i0 = 16 * I + 4 * g4;
-      const f32x4 qe = ld4f(&qe_s[i0]);
+      const int t = 16 * I + m16;
+      const float qe = vec_s[CH + t];
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int prow = (16 * I + m16) * TS + 4 * g4;
-      if (I == 0) acc = split_product<1>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 1) acc = split_product<2>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 2) acc = split_product<3>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 3) acc = split_product<4>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      const int prow = t * TS + 4 * g4;
+      if (I == 0) acc = split_product<1, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 1) acc = split_product<2, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 2) acc = split_product<3, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
+      if (I == 3) acc = split_product<4, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
       const f32x4 o = QS[I] * qe + acc;
-      uint16_t* orow = p.o + (tok0 + c0 + i0) * ostride + hv * VD + vcol;
-      if (nv == CH && !p.sq) {   // whole chunk, no sq: no per-element predicates
-#pragma unroll
-        for (int r = 0; r < 4; ++r) orow[r * ostride] = f2bf_finite(o[r]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (i0 + r < nv) {
-            const uint16_t ob = f2bf_finite(o[r]);
-            orow[r * ostride] = ob;
-            if (p.sq) {
-              const float x = bf2f(ob);
-              p.sq[(tok0 + c0 + i0 + r) * ostride + hv * VD + vcol] = x * x;
-            }
-          }
+      if (t < nv) {
+        const int64_t at = (tok0 + c0 + t) * ostride + hv * VD + vb * BV + wave * 16 + 4 * g4;
+        const uint32_t b0 = f2bf_finite(o[0]), b1 = f2bf_finite(o[1]), b2 = f2bf_finite(o[2]), b3 = f2bf_finite(o[3]);
+        *reinterpret_cast<uint2*>(p.o + at) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+        if (p.sq) {
+          const float x0 = bf2f(b0), x1 = bf2f(b1), x2 = bf2f(b2), x3 = bf2f(b3);
+          *reinterpret_cast<f32x4*>(p.sq + at) = (f32x4){x0 * x0, x1 * x1, x2 * x2, x3 * x3};
         }
       }
     }
 
-    // ---- S <- e^(G_C) S + Kr^T Z,  Z = rk e^(G_C - G) . V' (token blocks paired) ----
-    s16x4 Zh[4], Zl[4];
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_planes(nunit, 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- S <- e^(G_C) S + Kr^T W,  W = rk e^(G_C - G) . V' (token blocks paired) ----
+    s16x4 Wh[4], Wl[4];
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
-      const f32x4 d = ld4f(&d_s[16 * J + 4 * g4]);
-      split4(Vp[J] * d, Zh[J], Zl[J]);
+      const f32x4 d = ld4f(&vec_s[2 * CH + 16 * J + 4 * g4]);
+      split4(Vp[J] * d, Wh[J], Wl[J]);
     }
-    const float gc = gc_s;
+    const float gc = vec_s[3 * CH];
+    // K^T operand: lane m16 of group g4 gets key 16 mt + m16 of tokens 16 J + 4 g4 .. +3 (transpose read)
+    const uint16_t* kfrag = Ks + (4 * g4 + (m16 >> 2)) * KS + 4 * (m16 & 3);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = KTs + (16 * mt + m16) * TS + 4 * g4;
 #pragma unroll
       for (int J = 0; J < 4; J += 2) {
-        const s16x8 ka = cat(ld4h(krow + 16 * J), ld4h(krow + 16 * J + 16));
-        acc = mma32(ka, cat(Zl[J], Zl[J + 1]), acc);
-        acc = mma32(ka, cat(Zh[J], Zh[J + 1]), acc);
+        const s16x8 ka = cat(ld4h_tr(kfrag + 16 * J * KS + 16 * mt), ld4h_tr(kfrag + 16 * (J + 1) * KS + 16 * mt));
+        acc = mma32(ka, cat(Wl[J], Wl[J + 1]), acc);
+        acc = mma32(ka, cat(Wh[J], Wh[J + 1]), acc);
       }
       S[mt] = S[mt] * gc + acc;
     }
@@ -507,12 +685,18 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(const ChunkParams p) {
 
 using hsg::ChunkParams;
 
+extern "C" size_t hsg_gdn_chunk_workspace_bytes(int32_t n_rows, int32_t L, int32_t HV) {
+  if (n_rows <= 0 || L <= 0 || HV <= 0) return 0;
+  return (size_t)n_rows * (size_t)((L + hsg::CH - 1) / hsg::CH) * (size_t)HV * (size_t)hsg::UNIT_BYTES;
+}
+
 extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
                                      int32_t v_off, const void* a, const void* b, int64_t ab_stride,
                                      const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
                                      int64_t state_rows, const int64_t* slots, const int64_t* lens,
                                      const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
-                                     int32_t K, int32_t V, float scale, void* o, float* sq, void* stream) {
+                                     int32_t K, int32_t V, float scale, void* o, float* sq, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   ChunkParams p;
   p.qkv = static_cast<const uint16_t*>(qkv);
   p.qkv_stride = qkv_stride;
@@ -535,21 +719,26 @@ extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_
   p.scale = scale;
   p.o = static_cast<uint16_t*>(o);
   p.sq = sq;
-  if (n_rows < 0 || H <= 0 || HV <= 0 || L < 0 || state_rows <= 0) return HSG_ERR_ARG;
+  p.ws = static_cast<uint8_t*>(workspace);
+  if (n_rows < 0 || H <= 0 || HV <= 0 || L <= 0 || state_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
-  if (!qkv || !a || !b || !A_log || !dt_bias || !state || !slots || !lens || !o) return HSG_ERR_ARG;
-  if (offsets == nullptr && L <= 0) return HSG_ERR_ARG;
+  if (!qkv || !a || !b || !A_log || !dt_bias || !state || !slots || !lens || !o || !workspace) return HSG_ERR_ARG;
   if (K != hsg::KD || V != hsg::VD || HV % H != 0) return HSG_ERR_SHAPE;
   if (state_dtype != HSG_STATE_F32 && state_dtype != HSG_STATE_F16) return HSG_ERR_ARG;
   if (!hsg::aligned(qkv, 16) || qkv_stride % 8 || q_off % 8 || k_off % 8 || v_off % 8) return HSG_ERR_ALIGN;
-  if (!hsg::aligned(state, 16) || !hsg::aligned(o, 2) || (sq && !hsg::aligned(sq, 4))) return HSG_ERR_ALIGN;
-  if ((int64_t)n_rows * HV > (int64_t)1 << 26) return HSG_ERR_SHAPE;
+  if (!hsg::aligned(state, 16) || !hsg::aligned(o, 8) || (sq && !hsg::aligned(sq, 16))) return HSG_ERR_ALIGN;
+  if (!hsg::aligned(workspace, 256)) return HSG_ERR_ALIGN;
+  p.max_chunks = (L + hsg::CH - 1) / hsg::CH;
+  const int64_t units = (int64_t)n_rows * p.max_chunks * HV;
+  if ((int64_t)n_rows * HV > (int64_t)1 << 26 || units > (int64_t)0x7fffffff) return HSG_ERR_SHAPE;
+  if (workspace_bytes < hsg_gdn_chunk_workspace_bytes(n_rows, L, HV)) return HSG_ERR_SHAPE;
   p.pairs = n_rows * HV;
-  const dim3 grid((unsigned)(((p.pairs + 7) / 8) * 16));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(hsg::gdn_chunk_prep_kernel, dim3((unsigned)units), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)(((p.pairs + 7) / 8) * 16));
   if (state_dtype == HSG_STATE_F32)
-    hipLaunchKernelGGL((hsg::gdn_chunk_kernel<float>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<float>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((hsg::gdn_chunk_kernel<uint16_t>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<uint16_t>), grid, dim3(256), 0, s, p);
   return hsg::launch_status();
 }

@@ -26,13 +26,14 @@ SIGNATURES = {
         _P, _P, _P, _I32, _I32,              # slots, lens, offsets, n_rows, L
         _I32, _I32, _I32, _I32, _F,          # H, HV, K, V, scale
         _P, _P, _P]),                        # o, sq, stream
+    "hsg_gdn_chunk_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32]),
     "hsg_gdn_chunk_prefill": (ctypes.c_int, [
         _P, _I64, _I32, _I32, _I32,
         _P, _P, _I64, _P, _P,
         _P, _I32, _I64,
         _P, _P, _P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F,
-        _P, _P, _P]),
+        _P, _P, _P, ctypes.c_size_t, _P]),   # o, sq, workspace, workspace_bytes, stream
     "hsg_gdn_slot_step_gated": (ctypes.c_int, [
         _P, _I64, _I32, _I32, _I32,
         _P, _P, _I64, _P, _P,

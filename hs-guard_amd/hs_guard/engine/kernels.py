@@ -77,13 +77,16 @@ def gdn_slot_recurrent(q, k, v, a, b, A_log, dt_bias, state, slots, lens, scale=
 
 
 def gdn_chunk_prefill(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log, dt_bias, state, slots,
-                      lens, offsets=None, scale=None, with_sq=False):
+                      lens, offsets=None, scale=None, with_sq=False, max_len=None, workspace=None):
     """Chunked prefill (replaces FLA chunk_gated_delta_rule with initial_state = state[slots] and
     output_final_state written back, bucketed_engine.py:109-111), with gdn_slot_v8's input contract.
 
     Padded layout (offsets None): packed [N, L, C], a/b [N, L, HV]; returns o [N, L, HV, V] with zeros past
     lens. Packed layout: packed [T, C], a/b [T, HV], row n's tokens at offsets[n] .. offsets[n]+lens[n]-1;
-    returns o [T, HV, V]. State rows slots[n] (lens > 0) are updated in place. Returns (o, sq or None)."""
+    returns o [T, HV, V]; max_len bounds every row's length (default: lens.max(), a device sync).
+    State rows slots[n] (lens > 0) are updated in place. workspace: a uint8 device tensor of at least
+    chunk_workspace_bytes(...) bytes, reused across calls (allocated per call when None).
+    Returns (o, sq or None)."""
     for tensor in (packed, a, b, state):
         _require(tensor.is_contiguous(), "tensors must be contiguous")
     _gpu(packed, a, b, state, slots, lens, offsets)
@@ -95,16 +98,22 @@ def gdn_chunk_prefill(packed, key_dim, heads, head_k, value_heads, head_v, a, b,
         out_shape = (n, length, value_heads, head_v)
     else:
         _require(packed.dim() == 2, "packed layout takes [T, C]")
-        length, c = 0, packed.shape[1]
+        c = packed.shape[1]
         n = slots.shape[0]
+        length = int(lens.max()) if max_len is None else int(max_len)
         out_shape = (packed.shape[0], value_heads, head_v)
     o = torch.empty(out_shape, dtype=packed.dtype, device=packed.device)
     sq = torch.empty(out_shape, dtype=torch.float32, device=packed.device) if with_sq else None
     scale = head_k ** -0.5 if scale is None else scale
+    ws_bytes = lib().hsg_gdn_chunk_workspace_bytes(n, max(length, 1), value_heads)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=packed.device)
+    _require(workspace.numel() >= ws_bytes, f"workspace needs {ws_bytes} bytes")
     rc = lib().hsg_gdn_chunk_prefill(
         _ptr(packed), c, 0, key_dim, 2 * key_dim, _ptr(a), _ptr(b), value_heads, _ptr(A_log), _ptr(dt_bias),
         _ptr(state), _STATE_CODES[state.dtype], state.shape[0], _ptr(slots), _ptr(lens), _ptr(offsets), n,
-        length, heads, value_heads, head_k, head_v, scale, _ptr(o), _ptr(sq), _stream(packed.device))
+        max(length, 1), heads, value_heads, head_k, head_v, scale, _ptr(o), _ptr(sq), _ptr(workspace),
+        workspace.numel(), _stream(packed.device))
     check(rc, "hsg_gdn_chunk_prefill")
     return o, sq
 

@@ -80,14 +80,21 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * 64 tokens at a time in the WY/UT chunk form on MFMA, for rows of any length (initial contexts).
  * Replaces FLA's chunk_gated_delta_rule with initial_state = rec[slots] and output_final_state
  * (call sites src/hs_guard/runtime.py:80-89, src/hs_guard/engine/bucketed_engine.py:109-111).
- * Arguments as hsg_gdn_slot_step; lens[n] is unbounded. o must not alias qkv.
+ * Arguments as hsg_gdn_slot_step, except L: the padded row length, and in the packed layout the bound on
+ * every row's length (rows with lens[n] > L are treated as empty). o must not alias qkv; o 8-byte and sq
+ * 16-byte aligned.
+ * Two launches on `stream`: the state-independent part of every (row, chunk, value head) in parallel, then
+ * the sequential state products per row. workspace: device memory of at least
+ * hsg_gdn_chunk_workspace_bytes(n_rows, L, HV) bytes, 256-byte aligned; no initialisation needed, garbage
+ * afterwards.
  */
+size_t hsg_gdn_chunk_workspace_bytes(int32_t n_rows, int32_t L, int32_t HV);
 int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
                           const void* a, const void* b, int64_t ab_stride, const void* A_log,
                           const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
                           const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
                           int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
-                          float* sq, void* stream);
+                          float* sq, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Window-W GQA attention of this tick's queries over the slot's ring plus this tick's new keys.
