@@ -65,9 +65,6 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) short s16x8;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
-// 16-byte prefetch buffers are native vectors: a HIP uint4 copied whole into LDS is a struct memcpy that the
-// compiler cannot keep in registers (it parked such a buffer in LDS and waited for its loads at issue)
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 
 struct ChunkParams {
   const uint16_t* qkv;

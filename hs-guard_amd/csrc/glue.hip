@@ -86,15 +86,13 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const uint16_t* qkv, int
     e[i] = slot_ok ? pool[(slot * (KS - 1) + i) * (int64_t)C + c] : (uint16_t)0;
     keep[i] = e[i];
   }
-  for (int t = 0; t < steps; ++t) {
-    const int64_t tok = tok0 + t;
-    const uint16_t x = qkv[tok * qkv_stride + c];
+  auto step = [&](int t, uint16_t x) {
     float acc = 0.f;
     acc = fmaf(w[0], bf2f(e[0]), acc);
     acc = fmaf(w[1], bf2f(e[1]), acc);
     acc = fmaf(w[2], bf2f(e[2]), acc);
     acc = fmaf(w[3], bf2f(x), acc);
-    out[tok * out_stride + c] = f2bf(siluf_(rbf(acc)));
+    out[(tok0 + t) * out_stride + c] = f2bf(siluf_(rbf(acc)));
     e[0] = e[1];
     e[1] = e[2];
     e[2] = x;
@@ -103,7 +101,19 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const uint16_t* qkv, int
       keep[1] = e[1];
       keep[2] = e[2];
     }
+  };
+  // Whole batches of TB tokens load together (one memory round trip per batch instead of per token); the
+  // remainder, which is all of a single-token row, goes one load at a time.
+  constexpr int TB = 8;
+  int t = 0;
+  for (; t + TB <= steps; t += TB) {
+    uint16_t xs[TB];
+#pragma unroll
+    for (int i = 0; i < TB; ++i) xs[i] = qkv[(tok0 + t + i) * qkv_stride + c];
+#pragma unroll
+    for (int i = 0; i < TB; ++i) step(t + i, xs[i]);
   }
+  for (; t < steps; ++t) step(t, qkv[(tok0 + t) * qkv_stride + c]);
   if (len > 0) {
     for (int i = 0; i < KS - 1; ++i) pool[(slot * (KS - 1) + i) * (int64_t)C + c] = keep[i];
   }

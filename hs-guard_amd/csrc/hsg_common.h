@@ -7,6 +7,10 @@
 
 namespace hsg {
 
+// 16-byte register vectors are native clang vectors: a HIP uint4 / float4 copied whole is a struct memcpy that
+// the compiler may not keep in registers (it parked such a buffer in LDS, and in another kernel in scratch)
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
 // ---- bf16 / fp16 scalar conversions (bf16 stored as uint16_t; round to nearest even like torch) ----
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 

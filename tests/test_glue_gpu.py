@@ -67,12 +67,12 @@ def test_conv_silu_update(packed):
     from hs_guard._lib import lib
     print(f"[glue] conv packed={packed}", flush=True)
     rng = np.random.default_rng(1)
-    N, L, C, S = 4, 6, 6144, 6
+    N, L, C, S = 4, 21, 6144, 6
     stride = C + 40
     qkv = bf16(rng.standard_normal((N, L, stride)))
     pool = bf16(rng.standard_normal((S, 3, C)))
     w = bf16(rng.standard_normal((C, 4)) * 0.5)
-    slots, lens = np.array([4, 1, 0, 2]), np.array([6, 2, 0, 1])
+    slots, lens = np.array([4, 1, 0, 2]), np.array([21, 2, 0, 9])   # rows span 1-3 load batches of 8 tokens
     ref_out, ref_pool = oglue.conv_silu_update(qkv[..., :C], pool, w, slots, lens)
     pool_d = _bf(pool).to(DEV)
     w_d = _bf(w).to(DEV)
