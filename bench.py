@@ -393,6 +393,19 @@ def main():
     one = timed(lambda: [(0, [int(rng.integers(0, cfg.vocab_size))])])
     log(f"decode 352x1 p50 {percentile(dec, 50):.3f} ms; single-token p50 {percentile(one, 50):.3f} ms")
 
+    # ---- complete-message scorer (one whole forward) on an 8000-token message ----
+    from hs_guard.engine.whole import WholeSequenceScorer
+    scorer = WholeSequenceScorer(model, shared=eng)
+    msg = np.random.default_rng(args.seed + 2).integers(0, cfg.vocab_size, 8000).tolist()
+    scorer.forward(msg)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        scorer.forward(msg)
+    torch.cuda.synchronize()
+    whole_ms = (time.perf_counter() - t0) / 3 * 1e3
+    log(f"complete-message scorer, 8000 tokens: {whole_ms:.1f} ms")
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -431,6 +444,7 @@ def main():
                      "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
         "ring_decode_352": ring,
         "chunk_prefill_cfg4": chunk,
+        "complete_message_8000": {"ms": round(whole_ms, 2), "tokens_per_s": round(8000 / whole_ms * 1e3, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

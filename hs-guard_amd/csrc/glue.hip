@@ -120,6 +120,31 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const uint16_t* qkv, int
 }
 
 // ---------------------------------------------------------------------------------------------------
+// Gated RMSNorm of the GDN output, one wave per (token, head) of width 128 (2 values per lane).
+// gated_finish (src/hs_guard/engine/fused_kernels.py:215-233), as the slot step's fused epilogue computes it:
+// r = rsqrt(mean(o^2) + eps) over the head, out = bf16(bf16(w * bf16(o * r)) * silu(z)), o already bf16.
+// ---------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* x, int64_t x_stride, const uint16_t* z,
+                                                            int64_t z_stride, const uint16_t* w, float eps,
+                                                            uint16_t* out, int64_t out_stride, int tokens,
+                                                            int heads) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= tokens * heads) return;
+  const int t = item / heads;
+  const int c = (item - t * heads) * 128 + 2 * lane;
+  float x0, x1, z0, z1, w0, w1;
+  unpack2(*reinterpret_cast<const uint32_t*>(x + t * x_stride + c), x0, x1);
+  unpack2(*reinterpret_cast<const uint32_t*>(z + t * z_stride + c), z0, z1);
+  unpack2(*reinterpret_cast<const uint32_t*>(w + 2 * lane), w0, w1);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float r = rsqrtf(ss * (1.0f / 128) + eps);
+  const float y0 = rbf(w0 * rbf(x0 * r)) * siluf_(z0);
+  const float y1 = rbf(w1 * rbf(x1 * r)) * siluf_(z1);
+  *reinterpret_cast<uint32_t*>(out + t * out_stride + c) = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+}
+
+// ---------------------------------------------------------------------------------------------------
 // Per-head RMSNorm(1+w) + partial rotate-half RoPE for q and k in one launch, one wave per (token, head).
 // square_rows + norm_rope (src/hs_guard/engine/fused_kernels.py:237-284) with the rotary cos/sin of the
 // Qwen3.5 rotary embedding computed in-kernel: freq = pos * inv_freq[i] (fp32), cos/sin rounded to bf16.
@@ -308,6 +333,24 @@ extern "C" int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* p
                      static_cast<const uint16_t*>(qkv), qkv_stride, static_cast<uint16_t*>(pool), pool_rows,
                      static_cast<const uint16_t*>(weight), slots, lens, offsets, L, channels,
                      static_cast<uint16_t*>(out), out_stride);
+  return launch_status();
+}
+
+extern "C" int hsg_gated_rmsnorm(const void* x, int64_t x_stride, const void* z, int64_t z_stride, const void* w,
+                                 float eps, void* out, int64_t out_stride, int32_t tokens, int32_t heads,
+                                 int32_t width, void* stream) {
+  if (tokens < 0 || heads < 0) return HSG_ERR_ARG;
+  if (width != 128) return HSG_ERR_SHAPE;
+  if (tokens == 0 || heads == 0) return HSG_OK;
+  if (!x || !z || !w || !out) return HSG_ERR_ARG;
+  if (x_stride % 2 || z_stride % 2 || out_stride % 2 || !aligned(x, 4) || !aligned(z, 4) || !aligned(w, 4) ||
+      !aligned(out, 4))
+    return HSG_ERR_ALIGN;
+  const int64_t items = (int64_t)tokens * heads;
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), x_stride,
+                     static_cast<const uint16_t*>(z), z_stride, static_cast<const uint16_t*>(w), eps,
+                     static_cast<uint16_t*>(out), out_stride, tokens, heads);
   return launch_status();
 }
 

@@ -1,5 +1,6 @@
-"""HS-Guard streaming slot step on MI355X (gfx950): drop-in ``load_model`` / ``StreamingGuard``."""
-__all__ = ["StreamingGuard", "load_model"]
+"""HS-Guard streaming slot step on MI355X (gfx950): drop-in ``load_model`` / ``StreamingGuard`` and the
+complete-message scorer ``score_messages``."""
+__all__ = ["StreamingGuard", "load_model", "score_messages", "score_ids", "serialize", "encode_messages", "selfcheck"]
 
 
 def __getattr__(name):

@@ -66,6 +66,7 @@ SIGNATURES = {
     "hsg_add_rmsnorm": (ctypes.c_int, [_P, _P, _P, _F, _P, _I32, _I32, _P]),
     "hsg_conv_silu_update": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _P,
                                             _I64, _P]),
+    "hsg_gated_rmsnorm": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _F, _P, _I64, _I32, _I32, _I32, _P]),
     "hsg_norm_rope": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _F, _P, _I64, _I64,
                                      _P, _I64, _I64, _I32, _P, _F, _P, _I64, _I64,
                                      _P, _P, _I32, _I32, _I32, _P]),

@@ -84,7 +84,51 @@ def pack_ticks(chunks, slots, length, nb, tb, max_slots, out):
     return lens, offsets
 
 
-class SlotStreamEngine:
+class PreparedWeights:
+    """The backbone's weights in the kernels' layouts: fused projections (GDN qkv|z|b|a, attention q|k|v, MLP
+    gate|up, both heads' first Linear), RMSNorm gains as fp32 1 + w, rotary inverse frequencies. Needs
+    ``model``, ``cfg``, ``kind``, ``roles`` and ``device`` set."""
+
+    def _prepare_weights(self):
+        m, cfg = self.model, self.cfg
+        f32 = torch.float32
+        self.layers = []
+        for i, (kind, _) in enumerate(self.kind):
+            p = f"backbone.layers.{i}."
+            L = {"in_w1": (1.0 + m[p + "input_layernorm.weight"].float()).contiguous(),
+                 "post_w1": (1.0 + m[p + "post_attention_layernorm.weight"].float()).contiguous(),
+                 "w_gu": torch.cat([m[p + "mlp.gate_proj.weight"], m[p + "mlp.up_proj.weight"]]).contiguous(),
+                 "w_down": m[p + "mlp.down_proj.weight"].contiguous()}
+            if kind == "linear_attention":
+                a = p + "linear_attn."
+                L["w_in"] = torch.cat([m[a + "in_proj_qkv.weight"], m[a + "in_proj_z.weight"],
+                                       m[a + "in_proj_b.weight"], m[a + "in_proj_a.weight"]]).contiguous()
+                L["conv_w"] = m[a + "conv1d.weight"].reshape(cfg.conv_dim, -1).contiguous()
+                L["A_log"] = m[a + "A_log"].contiguous()
+                L["dt_bias"] = m[a + "dt_bias"].contiguous()
+                L["norm_w"] = m[a + "norm.weight"].contiguous()
+                L["w_out"] = m[a + "out_proj.weight"].contiguous()
+            else:
+                a = p + "self_attn."
+                L["w_in"] = torch.cat([m[a + "q_proj.weight"], m[a + "k_proj.weight"],
+                                       m[a + "v_proj.weight"]]).contiguous()
+                L["q_w1"] = (1.0 + m[a + "q_norm.weight"].float()).contiguous()
+                L["k_w1"] = (1.0 + m[a + "k_norm.weight"].float()).contiguous()
+                L["w_out"] = m[a + "o_proj.weight"].contiguous()
+            self.layers.append(L)
+        self.final_w1 = (1.0 + m["backbone.norm.weight"].float()).contiguous()
+        self.emb = m["backbone.embed_tokens.weight"].contiguous()
+        rot = cfg.rotary_dim
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=f32) / rot))).to(self.device)
+        self.head_w1 = torch.cat([m[f"heads.{r}.projection.0.weight"] for r in self.roles]).contiguous()
+        self.head_b1 = torch.cat([m[f"heads.{r}.projection.0.bias"] for r in self.roles]).contiguous()
+        self.head_ln_w = torch.stack([m[f"heads.{r}.projection.1.weight"] for r in self.roles]).contiguous()
+        self.head_ln_b = torch.stack([m[f"heads.{r}.projection.1.bias"] for r in self.roles]).contiguous()
+        self.head_w2 = torch.stack([m[f"heads.{r}.risk.weight"] for r in self.roles]).contiguous()
+        self.head_b2 = torch.stack([m[f"heads.{r}.risk.bias"] for r in self.roles]).contiguous()
+
+
+class SlotStreamEngine(PreparedWeights):
     """Fixed per-slot state for ``max_slots`` live streams (row ``max_slots`` of every pool is the scratch
     slot of padding rows)."""
 
@@ -135,44 +179,6 @@ class SlotStreamEngine:
         self._allocate_buffers()
 
     # ------------------------------------------------------------------------------------------------
-    def _prepare_weights(self):
-        m, cfg = self.model, self.cfg
-        f32 = torch.float32
-        self.layers = []
-        for i, (kind, _) in enumerate(self.kind):
-            p = f"backbone.layers.{i}."
-            L = {"in_w1": (1.0 + m[p + "input_layernorm.weight"].float()).contiguous(),
-                 "post_w1": (1.0 + m[p + "post_attention_layernorm.weight"].float()).contiguous(),
-                 "w_gu": torch.cat([m[p + "mlp.gate_proj.weight"], m[p + "mlp.up_proj.weight"]]).contiguous(),
-                 "w_down": m[p + "mlp.down_proj.weight"].contiguous()}
-            if kind == "linear_attention":
-                a = p + "linear_attn."
-                L["w_in"] = torch.cat([m[a + "in_proj_qkv.weight"], m[a + "in_proj_z.weight"],
-                                       m[a + "in_proj_b.weight"], m[a + "in_proj_a.weight"]]).contiguous()
-                L["conv_w"] = m[a + "conv1d.weight"].reshape(cfg.conv_dim, -1).contiguous()
-                L["A_log"] = m[a + "A_log"].contiguous()
-                L["dt_bias"] = m[a + "dt_bias"].contiguous()
-                L["norm_w"] = m[a + "norm.weight"].contiguous()
-                L["w_out"] = m[a + "out_proj.weight"].contiguous()
-            else:
-                a = p + "self_attn."
-                L["w_in"] = torch.cat([m[a + "q_proj.weight"], m[a + "k_proj.weight"],
-                                       m[a + "v_proj.weight"]]).contiguous()
-                L["q_w1"] = (1.0 + m[a + "q_norm.weight"].float()).contiguous()
-                L["k_w1"] = (1.0 + m[a + "k_norm.weight"].float()).contiguous()
-                L["w_out"] = m[a + "o_proj.weight"].contiguous()
-            self.layers.append(L)
-        self.final_w1 = (1.0 + m["backbone.norm.weight"].float()).contiguous()
-        self.emb = m["backbone.embed_tokens.weight"].contiguous()
-        rot = cfg.rotary_dim
-        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=f32) / rot))).to(self.device)
-        self.head_w1 = torch.cat([m[f"heads.{r}.projection.0.weight"] for r in self.roles]).contiguous()
-        self.head_b1 = torch.cat([m[f"heads.{r}.projection.0.bias"] for r in self.roles]).contiguous()
-        self.head_ln_w = torch.stack([m[f"heads.{r}.projection.1.weight"] for r in self.roles]).contiguous()
-        self.head_ln_b = torch.stack([m[f"heads.{r}.projection.1.bias"] for r in self.roles]).contiguous()
-        self.head_w2 = torch.stack([m[f"heads.{r}.risk.weight"] for r in self.roles]).contiguous()
-        self.head_b2 = torch.stack([m[f"heads.{r}.risk.bias"] for r in self.roles]).contiguous()
-
     def _allocate_buffers(self):
         cfg, T, dev = self.cfg, self.max_tokens, self.device
         bf16 = torch.bfloat16

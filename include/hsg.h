@@ -172,6 +172,17 @@ int hsg_add_rmsnorm(void* hidden, const void* mix, const float* w1, float eps, v
                     int32_t width, void* stream);
 
 /*
+ * Gated RMSNorm of GDN outputs, per (token, head) of `width` values. Replaces gated_finish
+ * (src/hs_guard/engine/fused_kernels.py:215-233) where it is not fused into the slot step (outputs of
+ * hsg_gdn_chunk_prefill):
+ *   out[t, h*width + c] = bf16( bf16(w[c] * bf16(x * rsqrt(mean_c(x^2) + eps))) * silu(z[t, h*width + c]) )
+ *   x [tokens, x_stride], z [tokens, z_stride], out [tokens, out_stride] bf16; w [width] bf16.
+ * Supported: width == 128; strides even, pointers 4-byte aligned.
+ */
+int hsg_gated_rmsnorm(const void* x, int64_t x_stride, const void* z, int64_t z_stride, const void* w, float eps,
+                      void* out, int64_t out_stride, int32_t tokens, int32_t heads, int32_t width, void* stream);
+
+/*
  * Causal depthwise conv + SiLU with the per-slot conv-history update. Replaces conv_silu_update
  * (src/hs_guard/engine/fused_kernels.py:126-136; kernel :94-123):
  *   qkv [tokens, qkv_stride] bf16 (first `channels` columns), pool [pool_rows, kernel_size-1, channels]

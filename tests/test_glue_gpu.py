@@ -62,6 +62,25 @@ def test_embed_and_add_rmsnorm():
     _close(_np(nrm), n_ref, "add rmsnorm")
 
 
+def test_gated_rmsnorm():
+    """hsg_gated_rmsnorm (the chunk path's gated_finish) against the oracle, strided x / z / out."""
+    from hs_guard._lib import lib
+    print("[glue] gated rmsnorm", flush=True)
+    rng = np.random.default_rng(5)
+    T, HV, V = 29, 4, 128
+    x = bf16(rng.standard_normal((T, HV * V)))
+    z = bf16(rng.standard_normal((T, HV * V + 24)))
+    w = bf16(1.0 + rng.standard_normal(V) * 0.1)
+    ref = oglue.gated_rmsnorm(x.reshape(T, HV, V), z[:, :HV * V].reshape(T, HV, V), w, 1e-6).reshape(T, HV * V)
+    x_d, z_d, w_d = _bf(x).to(DEV), _bf(z).to(DEV), _bf(w).to(DEV)
+    out = torch.zeros(T, HV * V + 8, dtype=torch.bfloat16, device=DEV)
+    assert lib().hsg_gated_rmsnorm(x_d.data_ptr(), HV * V, z_d.data_ptr(), HV * V + 24, w_d.data_ptr(), 1e-6,
+                                   out.data_ptr(), HV * V + 8, T, HV, V, _stream()) == 0
+    got = _np(out)
+    _close(got[:, :HV * V], ref, "gated rmsnorm")
+    assert np.count_nonzero(got[:, HV * V:]) == 0
+
+
 @pytest.mark.parametrize("packed", [False, True])
 def test_conv_silu_update(packed):
     from hs_guard._lib import lib

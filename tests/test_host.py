@@ -119,3 +119,33 @@ def test_load_model_offline_behaviour(tmp_path):
     (tmp_path / "hs_guard.json").write_text('{"format": "other"}')
     with pytest.raises(ValueError, match="Unsupported model format"):
         load_model(str(tmp_path))
+
+
+def test_serialize_and_encode_messages():
+    """serialize / encode_messages (src/hs_guard/runtime.py:44-51,128-133): 'ROLE:\\ncontent' blocks joined by a
+    blank line; positions are the tokens ending inside the last message; the reference's ValueErrors."""
+    import pytest
+    from hs_guard.runtime import encode_messages, serialize
+    msgs = [{"role": "system", "content": "be nice"}, {"role": "user", "content": "hi there"},
+            {"role": "assistant", "content": "hello"}]
+    text = serialize(msgs)
+    assert text == "SYSTEM:\nbe nice\n\nUSER:\nhi there\n\nASSISTANT:\nhello"
+
+    class Tok:   # whitespace-and-newline tokenizer with character offsets, like tokenizers.Encoding
+        def encode(self, text, add_special_tokens=False):
+            import re
+            spans = [(m.start(), m.end()) for m in re.finditer(r"\S+", text)]
+            return type("E", (), {"ids": list(range(len(spans))), "offsets": spans})()
+    ids, positions, role = encode_messages(Tok(), msgs)
+    assert role == "assistant" and len(ids) == 8 and positions == [7]      # only "hello" ends after its start
+    ids, positions, role = encode_messages(Tok(), msgs[:2])
+    assert role == "user" and positions == [4, 5]                          # 'hi', 'there'
+    for bad, msg in (([], "The last message must have role user or assistant"),
+                     ([{"role": "system", "content": "x"}], "The last message must have role user or assistant"),
+                     ([{"role": "tool", "content": "x"}, {"role": "user", "content": "y"}],
+                      "Messages require a supported role and string content"),
+                     ([{"role": "user", "content": ""}], "The target message is empty")):
+        with pytest.raises(ValueError, match=msg):
+            serialize(bad)
+    with pytest.raises(ValueError, match="no tokenizer"):
+        encode_messages(None, msgs)
