@@ -230,6 +230,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel measurement (the command profiled under rocprofv3)")
+    ap.add_argument("--chunk-only", action="store_true",
+                    help="only the config-4 chunked-prefill measurement (profiled under rocprofv3)")
+    ap.add_argument("--ring-only", action="store_true",
+                    help="only the 352 x 1-token split-K ring decode measurement (profiled under rocprofv3)")
     ap.add_argument("--mixed-only", action="store_true",
                     help="only the prefill and the mixed steps (no kernel legs, decode legs, context sweep or CPU "
                          "baseline): the command whose kernel statistics give the per-step kernel breakdown")
@@ -254,6 +258,10 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(0)}")
     state_code = 0 if args.state_dtype == "float32" else 1
+    if args.chunk_only or args.ring_only:
+        leg = chunk_prefill_rate(torch) if args.chunk_only else ring_decode_rate(torch, rows=args.slots)
+        print(json.dumps({"chunk_prefill_cfg4" if args.chunk_only else "ring_decode_352": leg}), flush=True)
+        return
     if args.mixed_only:
         args.sweep_steps = 0
         args.no_cpu_baseline = True
