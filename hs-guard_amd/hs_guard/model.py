@@ -50,6 +50,18 @@ class GuardConfig:
                                 for i in range(self.num_hidden_layers)]
 
     @classmethod
+    def from_hf(cls, d: dict, window_tokens: int = 512):
+        """Geometry from a bundle's config.json (transformers' Qwen3_5TextConfig.to_dict(); rope settings under
+        ``rope_parameters`` or, in older files, at top level) and the manifest's window."""
+        rope = d.get("rope_parameters") or {}
+        kw = {f.name: d[f.name] for f in dataclasses.fields(cls)
+              if f.name in d and f.name not in ("window_tokens", "head_hidden", "layer_norm_eps")}
+        kw["rope_theta"] = float(rope.get("rope_theta", d.get("rope_theta", 10000.0)))
+        kw["partial_rotary_factor"] = float(rope.get("partial_rotary_factor", d.get("partial_rotary_factor", 0.25)))
+        kw["window_tokens"] = int(window_tokens)
+        return cls(**kw)
+
+    @classmethod
     def baseline(cls, **kw):
         """The geometry BASELINE.json's configs state: vocab 151,936, 16q/4kv attention."""
         return cls(**kw)
@@ -155,6 +167,32 @@ class GuardModel:
             if name.endswith(_UNIT_GAINS):
                 t = t + 1.0
             weights[name] = t.to(torch.bfloat16).to(device)
+        return cls(config, weights)
+
+    @classmethod
+    def from_state_dict(cls, config: GuardConfig, state: Dict[str, torch.Tensor], head="redline", device="cuda"):
+        """Weights of a classifier checkpoint (the state dict of src/hs_guard/runtime.py:54-74, loaded there with
+        strict=True): every backbone and head tensor this build uses must be present with its shape, and any
+        other key must be one of the checkpoint's classifier tensors this build does not use (category and
+        general heads). head="general" reads the general projection and risk layers in place of the red-line
+        ones (runtime.py:119-121). Tensors are stored as bf16 on ``device``."""
+        shapes = config.parameter_shapes()
+        known_extra = ("category.", "general_projection.", "general.", "general_category.")
+        unexpected = [k for k in state if k not in shapes and
+                      not (k.startswith("heads.") and k.split(".", 2)[2].startswith(known_extra))]
+        if unexpected:
+            raise ValueError(f"Unexpected keys in checkpoint: {sorted(unexpected)[:5]}")
+        weights = {}
+        for name, shape in shapes.items():
+            src = name
+            if head == "general" and name.startswith("heads."):
+                src = name.replace(".projection.", ".general_projection.").replace(".risk.", ".general.")
+            if src not in state:
+                raise ValueError(f"Missing key in checkpoint: {src}")
+            t = state[src]
+            if tuple(t.shape) != tuple(shape):
+                raise ValueError(f"Shape mismatch for {src}: {tuple(t.shape)} != {tuple(shape)}")
+            weights[name] = t.to(torch.bfloat16).to(device).contiguous()
         return cls(config, weights)
 
     def to(self, device):

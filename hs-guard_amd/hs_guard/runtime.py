@@ -9,6 +9,7 @@ forward; ``score_ids`` is the same on token ids (random-init models have no toke
 """
 from __future__ import annotations
 
+import hashlib
 import json
 from pathlib import Path
 
@@ -25,12 +26,64 @@ def random_metadata(head="redline", window_tokens=512):
             "thresholds": dict(DEFAULT_THRESHOLDS[head])}
 
 
+def sha256(path):
+    """Hex SHA-256 of a file, read in 8 MiB blocks."""
+    digest = hashlib.sha256()
+    with Path(path).open("rb") as f:
+        for block in iter(lambda: f.read(8 << 20), b""):
+            digest.update(block)
+    return digest.hexdigest()
+
+
+def verify_model(directory):
+    """The bundle check of src/hs_guard/runtime.py:19-41: hs_guard.json names format hs-guard-v1 and the risk
+    labels in order, lists config.json, tokenizer.json and model.safetensors, and every listed asset is a file
+    inside the bundle (or, for a hub snapshot, in its blob cache) with the listed SHA-256."""
+    root = Path(directory).resolve()
+    manifest = json.loads((root / "hs_guard.json").read_text())
+    if manifest.get("format") != "hs-guard-v1" or manifest.get("risk_labels") != list(LABELS):
+        raise ValueError("Unsupported model format or risk-label order")
+    files = manifest.get("files", {})
+    if not {"config.json", "tokenizer.json", "model.safetensors"}.issubset(files):
+        raise ValueError("Model manifest is missing required assets")
+    blobs = (root.parent.parent / "blobs").resolve() if root.parent.name == "snapshots" else None
+    for name, expected in files.items():
+        rel = Path(name)
+        if rel.is_absolute() or ".." in rel.parts:
+            raise ValueError(f"Invalid model asset: {name}")
+        path = root / rel
+        real = path.resolve()
+        if not path.is_file() or not (real.is_relative_to(root) or (blobs is not None and real.is_relative_to(blobs))):
+            raise ValueError(f"Invalid model asset: {name}")
+        if sha256(path) != expected:
+            raise ValueError(f"Model asset checksum mismatch: {name}")
+    return manifest
+
+
+def load_bundle(root, head="redline", device="cuda"):
+    """(model, tokenizer, metadata) of a verified local bundle: geometry from config.json, weights from
+    model.safetensors (GuardModel.from_state_dict: strict names and shapes), tokenizers.Tokenizer from
+    tokenizer.json, metadata = the manifest with the chosen head's thresholds (runtime.py:92-125)."""
+    if head not in ("redline", "general"):
+        raise ValueError("head must be redline or general")
+    from safetensors.torch import load_file
+    from tokenizers import Tokenizer
+    from .model import GuardConfig, GuardModel
+    root = Path(root)
+    manifest = verify_model(root)
+    cfg = GuardConfig.from_hf(json.loads((root / "config.json").read_text()), manifest.get("window_tokens", 512))
+    model = GuardModel.from_state_dict(cfg, load_file(str(root / "model.safetensors")), head=head, device=device)
+    metadata = dict(manifest, head=head, thresholds=manifest["thresholds"][head])
+    return model, Tokenizer.from_file(str(root / "tokenizer.json")), metadata
+
+
 def load_model(model=MODEL_ID, *, revision=None, head="redline", config=None, seed=0, device="cuda"):
     """Returns (model, tokenizer, metadata) like src/hs_guard/runtime.py:92-125.
 
-    ``model="random"`` (or a GuardConfig passed as ``config``) builds seeded random-init weights of that
-    geometry on ``device`` (tokenizer None). A local bundle directory is not loadable yet, and hub names
-    need a network fetch, which this build does not do: both raise."""
+    A local bundle directory (hs_guard.json, config.json, tokenizer.json, model.safetensors) is verified and
+    loaded (``load_bundle``). ``model="random"`` (or a GuardConfig passed as ``config``) builds seeded
+    random-init weights of that geometry on ``device`` (tokenizer None). Hub names need a network fetch,
+    which this build does not do: they raise."""
     if head not in ("redline", "general"):
         raise ValueError("head must be redline or general")
     import torch
@@ -43,10 +96,10 @@ def load_model(model=MODEL_ID, *, revision=None, head="redline", config=None, se
     root = Path(str(model))
     if not root.is_dir():
         raise RuntimeError(f"{model!r} is not a local model directory and this build does not download models")
-    manifest = json.loads((root / "hs_guard.json").read_text())
-    if manifest.get("format") != "hs-guard-v1" or manifest.get("risk_labels") != list(LABELS):
-        raise ValueError("Unsupported model format or risk-label order")
-    raise NotImplementedError("loading released bundles is not implemented yet; use load_model('random')")
+    verify_model(root)
+    if not torch.cuda.is_available():
+        raise RuntimeError("HS-Guard requires an AMD Instinct GPU (HIP)")
+    return load_bundle(root, head=head, device=device)
 
 
 class StreamingGuard:

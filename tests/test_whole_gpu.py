@@ -109,3 +109,31 @@ def test_selfcheck_full_geometry():
     print(f"[whole] full-geometry selfcheck {res}", flush=True)
     assert res["stream_positions"] == 160
     assert res["max_prob_diff_stream_vs_whole"] <= 0.05
+
+
+def test_local_bundle_end_to_end(tmp_path):
+    """load_model on a synthetic local bundle (tests/conftest.py:write_bundle), then score_messages through its
+    tokenizer and StreamingGuard on the same ids: the loaded model scores exactly like the same weights built
+    directly, and streaming agrees with the whole forward."""
+    from conftest import write_bundle
+    from hs_guard.model import GuardConfig, GuardModel
+    from hs_guard.runtime import StreamingGuard, encode_messages, load_model, score_ids, score_messages
+    print("[whole] local bundle end to end", flush=True)
+    cfg = GuardConfig(vocab_size=64, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    root, state = write_bundle(tmp_path / "b", cfg)
+    model, tok, meta = load_model(str(root))
+    msgs = [{"role": "user", "content": " ".join(f"w{i % 60}" for i in range(40))},
+            {"role": "assistant", "content": " ".join(f"w{(7 * i) % 60}" for i in range(50))}]
+    rec = score_messages(model, tok, meta, msgs)
+    ids, positions, role = encode_messages(tok, msgs)
+    assert role == "assistant" and len(ids) == 92 and positions == list(range(42, 92))   # the 50 content tokens
+    direct = GuardModel(cfg, {k: v.to("cuda:0") for k, v in state.items() if k in cfg.parameter_shapes()})
+    assert rec == score_ids(direct, meta, ids, positions, role)
+    guard = StreamingGuard(model, meta, max_slots=2)
+    cuts = []
+    for a in range(0, len(ids), 7):
+        cuts += guard.step([(1, ids[a:a + 7])], role="assistant")[0]["cut_scores"]
+    streamed = max(cuts[p] for p in positions)
+    assert abs(streamed - rec["score"]) <= PROB_TOL_INDEPENDENT
