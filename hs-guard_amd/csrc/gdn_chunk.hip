@@ -83,10 +83,17 @@ struct ChunkParams {
   int L, H, HV;
   int pairs;                       // n_rows * HV
   int max_chunks;                  // ceil(L / CH): workspace units per (row, value head)
+  int min_len;                     // rows with fewer tokens are left alone
   float scale;
   uint16_t* o;
   float* sq;
   uint8_t* ws;
+  // gated epilogue (hsg_gdn_chunk_prefill_gated): out = gated RMSNorm of o with z
+  const uint16_t* z;
+  int64_t z_stride;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* out;
 };
 
 __device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
@@ -186,7 +193,7 @@ __device__ __forceinline__ int row_tokens(const ChunkParams& p, int n, int64_t& 
   const int64_t len = p.lens[n];
   const bool padded = p.offsets == nullptr;
   tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
-  if (slot < 0 || slot >= p.state_rows || len <= 0) return 0;
+  if (slot < 0 || slot >= p.state_rows || len <= 0 || len < p.min_len) return 0;
   if (padded) return (int)min(len, (int64_t)p.L);
   return len > p.L ? 0 : (int)len;
 }
@@ -677,24 +684,78 @@ __global__ __launch_bounds__(256) void gdn_chunk_state_kernel(const ChunkParams 
     for (int r = 0; r < 4; ++r) store_state(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD, S[mt][r]);
 }
 
+// Gated RMSNorm of the chunk outputs (gated_finish, src/hs_guard/engine/fused_kernels.py:215-233, as the slot
+// step's fused epilogue computes it): one wave per token of a processed row, all value heads (2 values per lane
+// each, loads of every head issued together); out = bf16(bf16(w * bf16(o * rsqrt(mean(o^2) + eps))) * silu(z)).
+__global__ __launch_bounds__(256) void gdn_chunk_gate_kernel(const ChunkParams p) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.y;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  int64_t slot, tok0;
+  const int ntok = row_tokens(p, n, slot, tok0);
+  if (t >= ntok) return;
+  const int64_t tok = tok0 + t;
+  const int64_t ostride = (int64_t)p.HV * VD;
+  float w0, w1;
+  unpack2(*reinterpret_cast<const uint32_t*>(p.norm_w + 2 * lane), w0, w1);
+  for (int hv = 0; hv < p.HV; hv += 4) {
+    float x[4][2], zz[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int h = min(hv + u, p.HV - 1);
+      unpack2(*reinterpret_cast<const uint32_t*>(p.o + tok * ostride + h * VD + 2 * lane), x[u][0], x[u][1]);
+      unpack2(*reinterpret_cast<const uint32_t*>(p.z + tok * p.z_stride + h * VD + 2 * lane), zz[u][0], zz[u][1]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (hv + u >= p.HV) break;
+      const float r = rsqrtf(wave_sum(x[u][0] * x[u][0] + x[u][1] * x[u][1]) * (1.0f / VD) + p.eps);
+      const float y0 = rbf(w0 * rbf(x[u][0] * r)) * siluf_(zz[u][0]);
+      const float y1 = rbf(w1 * rbf(x[u][1] * r)) * siluf_(zz[u][1]);
+      *reinterpret_cast<uint32_t*>(p.out + tok * ostride + (hv + u) * VD + 2 * lane) =
+          (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace hsg
 
 using hsg::ChunkParams;
 
-extern "C" size_t hsg_gdn_chunk_workspace_bytes(int32_t n_rows, int32_t L, int32_t HV) {
-  if (n_rows <= 0 || L <= 0 || HV <= 0) return 0;
-  return (size_t)n_rows * (size_t)((L + hsg::CH - 1) / hsg::CH) * (size_t)HV * (size_t)hsg::UNIT_BYTES;
+namespace {
+
+// Shared argument checks and the two launches (prep, state); returns HSG_OK after launching, or an error code.
+int chunk_launch(ChunkParams& p, int32_t state_dtype, int32_t n_rows, int32_t L, int32_t H, int32_t HV, int32_t K,
+                 int32_t V, size_t workspace_bytes, hipStream_t s) {
+  if (n_rows < 0 || H <= 0 || HV <= 0 || L <= 0 || p.state_rows <= 0) return HSG_ERR_ARG;
+  if (!p.qkv || !p.a || !p.b || !p.A_log || !p.dt_bias || !p.state || !p.slots || !p.lens || !p.o || !p.ws)
+    return HSG_ERR_ARG;
+  if (K != hsg::KD || V != hsg::VD || HV % H != 0) return HSG_ERR_SHAPE;
+  if (state_dtype != HSG_STATE_F32 && state_dtype != HSG_STATE_F16) return HSG_ERR_ARG;
+  if (!hsg::aligned(p.qkv, 16) || p.qkv_stride % 8 || p.q_off % 8 || p.k_off % 8 || p.v_off % 8) return HSG_ERR_ALIGN;
+  if (!hsg::aligned(p.state, 16) || !hsg::aligned(p.o, 8) || (p.sq && !hsg::aligned(p.sq, 16))) return HSG_ERR_ALIGN;
+  if (!hsg::aligned(p.ws, 256)) return HSG_ERR_ALIGN;
+  p.max_chunks = (L + hsg::CH - 1) / hsg::CH;
+  const int64_t units = (int64_t)n_rows * p.max_chunks * HV;
+  if ((int64_t)n_rows * HV > (int64_t)1 << 26 || units > (int64_t)0x7fffffff) return HSG_ERR_SHAPE;
+  if (workspace_bytes < hsg_gdn_chunk_workspace_bytes(n_rows, L, HV)) return HSG_ERR_SHAPE;
+  p.pairs = n_rows * HV;
+  hipLaunchKernelGGL(hsg::gdn_chunk_prep_kernel, dim3((unsigned)units), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)(((p.pairs + 7) / 8) * 16));
+  if (state_dtype == HSG_STATE_F32)
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<float>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<uint16_t>), grid, dim3(256), 0, s, p);
+  return HSG_OK;
 }
 
-extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
-                                     int32_t v_off, const void* a, const void* b, int64_t ab_stride,
-                                     const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
-                                     int64_t state_rows, const int64_t* slots, const int64_t* lens,
-                                     const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
-                                     int32_t K, int32_t V, float scale, void* o, float* sq, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
-  ChunkParams p;
+ChunkParams chunk_params(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
+                         const void* a, const void* b, int64_t ab_stride, const void* A_log, const void* dt_bias,
+                         void* state, int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                         const int64_t* offsets, int32_t L, int32_t H, int32_t HV, float scale, void* o, float* sq,
+                         int32_t min_len, void* workspace) {
+  ChunkParams p{};
   p.qkv = static_cast<const uint16_t*>(qkv);
   p.qkv_stride = qkv_stride;
   p.q_off = q_off;
@@ -716,26 +777,55 @@ extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_
   p.scale = scale;
   p.o = static_cast<uint16_t*>(o);
   p.sq = sq;
+  p.min_len = min_len;
   p.ws = static_cast<uint8_t*>(workspace);
-  if (n_rows < 0 || H <= 0 || HV <= 0 || L <= 0 || state_rows <= 0) return HSG_ERR_ARG;
-  if (n_rows == 0) return HSG_OK;
-  if (!qkv || !a || !b || !A_log || !dt_bias || !state || !slots || !lens || !o || !workspace) return HSG_ERR_ARG;
-  if (K != hsg::KD || V != hsg::VD || HV % H != 0) return HSG_ERR_SHAPE;
-  if (state_dtype != HSG_STATE_F32 && state_dtype != HSG_STATE_F16) return HSG_ERR_ARG;
-  if (!hsg::aligned(qkv, 16) || qkv_stride % 8 || q_off % 8 || k_off % 8 || v_off % 8) return HSG_ERR_ALIGN;
-  if (!hsg::aligned(state, 16) || !hsg::aligned(o, 8) || (sq && !hsg::aligned(sq, 16))) return HSG_ERR_ALIGN;
-  if (!hsg::aligned(workspace, 256)) return HSG_ERR_ALIGN;
-  p.max_chunks = (L + hsg::CH - 1) / hsg::CH;
-  const int64_t units = (int64_t)n_rows * p.max_chunks * HV;
-  if ((int64_t)n_rows * HV > (int64_t)1 << 26 || units > (int64_t)0x7fffffff) return HSG_ERR_SHAPE;
-  if (workspace_bytes < hsg_gdn_chunk_workspace_bytes(n_rows, L, HV)) return HSG_ERR_SHAPE;
-  p.pairs = n_rows * HV;
+  return p;
+}
+
+}  // namespace
+
+extern "C" size_t hsg_gdn_chunk_workspace_bytes(int32_t n_rows, int32_t L, int32_t HV) {
+  if (n_rows <= 0 || L <= 0 || HV <= 0) return 0;
+  return (size_t)n_rows * (size_t)((L + hsg::CH - 1) / hsg::CH) * (size_t)HV * (size_t)hsg::UNIT_BYTES;
+}
+
+extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
+                                     int32_t v_off, const void* a, const void* b, int64_t ab_stride,
+                                     const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
+                                     int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                                     const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
+                                     int32_t K, int32_t V, float scale, void* o, float* sq, int32_t min_len,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (n_rows == 0 && L > 0 && H > 0 && HV > 0 && state_rows > 0) return HSG_OK;
+  ChunkParams p = chunk_params(qkv, qkv_stride, q_off, k_off, v_off, a, b, ab_stride, A_log, dt_bias, state,
+                               state_rows, slots, lens, offsets, L, H, HV, scale, o, sq, min_len, workspace);
+  const int rc = chunk_launch(p, state_dtype, n_rows, L, H, HV, K, V, workspace_bytes,
+                              reinterpret_cast<hipStream_t>(stream));
+  return rc != HSG_OK ? rc : hsg::launch_status();
+}
+
+extern "C" int hsg_gdn_chunk_prefill_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
+                                           int32_t v_off, const void* a, const void* b, int64_t ab_stride,
+                                           const void* A_log, const void* dt_bias, void* state,
+                                           int32_t state_dtype, int64_t state_rows, const int64_t* slots,
+                                           const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t L,
+                                           int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
+                                           const void* z, int64_t z_stride, const void* norm_w, float eps,
+                                           void* out, int32_t min_len, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  if (n_rows == 0 && L > 0 && H > 0 && HV > 0 && state_rows > 0) return HSG_OK;
+  if (!z || !norm_w || !out || offsets == nullptr) return HSG_ERR_ARG;   // packed layout only
+  if (!hsg::aligned(z, 4) || z_stride % 2 || !hsg::aligned(norm_w, 4) || !hsg::aligned(out, 4)) return HSG_ERR_ALIGN;
+  ChunkParams p = chunk_params(qkv, qkv_stride, q_off, k_off, v_off, a, b, ab_stride, A_log, dt_bias, state,
+                               state_rows, slots, lens, offsets, L, H, HV, scale, o, nullptr, min_len, workspace);
+  p.z = static_cast<const uint16_t*>(z);
+  p.z_stride = z_stride;
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
+  p.out = static_cast<uint16_t*>(out);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(hsg::gdn_chunk_prep_kernel, dim3((unsigned)units), dim3(256), 0, s, p);
-  const dim3 grid((unsigned)(((p.pairs + 7) / 8) * 16));
-  if (state_dtype == HSG_STATE_F32)
-    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<float>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<uint16_t>), grid, dim3(256), 0, s, p);
+  const int rc = chunk_launch(p, state_dtype, n_rows, L, H, HV, K, V, workspace_bytes, s);
+  if (rc != HSG_OK) return rc;
+  hipLaunchKernelGGL(hsg::gdn_chunk_gate_kernel, dim3((unsigned)((L + 3) / 4), (unsigned)n_rows), dim3(256), 0, s, p);
   return hsg::launch_status();
 }

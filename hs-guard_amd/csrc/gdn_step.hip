@@ -27,7 +27,7 @@ constexpr int KD = 128;
 constexpr int VD = 128;
 constexpr int TILE_V = 32;
 constexpr int ROWS = 16;
-constexpr int CT = 16;   // tokens staged in LDS per chunk
+constexpr int CT = 8;    // tokens staged in LDS per burst (the next burst is prefetched into registers)
 
 struct GdnParams {
   const uint16_t* qkv;
@@ -52,6 +52,7 @@ struct GdnParams {
   const uint16_t* norm_w;
   float eps;
   uint16_t* out;
+  int skip_rows, skip_min_len;   // packed layout: rows n < skip_rows with lens >= skip_min_len are left alone
 };
 
 template <typename ST>
@@ -117,6 +118,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   const bool padded = p.offsets == nullptr;
   if (slot < 0 || slot >= p.state_rows || ntok < 0) ntok = 0;
   if (padded && ntok > p.L) ntok = p.L;  // a row never reads past its L padded positions
+  if (!padded && n < p.skip_rows && ntok >= p.skip_min_len) ntok = 0;   // routed to the chunk kernels
   const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
   const int col = wave * TILE_V + c * 4;
 
@@ -135,31 +137,62 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   __shared__ __align__(16) uint16_t sz_[GATED ? CT : 1][VD];
   __shared__ float sa_[CT], sb_[CT];
   constexpr int SEGS = GATED ? 64 : 48;   // 16-byte segments per token: q, k, v (, z)
+  constexpr int PF = (CT * SEGS + 255) / 256;   // segments per thread per burst (the last partly idle)
+  // gated-norm weights staged in LDS once (read per token from global memory they were reloaded after every
+  // output store, since `out` may alias them: one global round trip per token)
+  __shared__ __align__(16) uint16_t sw_[GATED ? VD : 1];
+  if (GATED && threadIdx.x < VD / 8)
+    *reinterpret_cast<u32x4*>(&sw_[8 * threadIdx.x]) = *reinterpret_cast<const u32x4*>(p.norm_w + 8 * threadIdx.x);
+
+  // The tokens of a row go through LDS in bursts of CT; the next burst is loaded into registers while the
+  // current one is processed. Segment e = threadIdx.x + 256 i of a burst is token e / SEGS, piece e % SEGS;
+  // positions past the row's end re-read its last token (never stored to LDS).
+  u32x4 pf[PF];
+  uint16_t pa = 0, pb = 0;
+  auto fetch = [&](int t) {
+    const int last = ntok - 1 - t;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      const int u = min(e / SEGS, last);
+      const int sg = e % SEGS;
+      const int which = sg >> 4;
+      const int c = (sg & 15) * 8;
+      const int64_t tok = tok0 + t + u;
+      const uint16_t* row = p.qkv + tok * p.qkv_stride;
+      const uint16_t* src = which == 0 ? row + p.q_off + h * KD + c
+                          : which == 1 ? row + p.k_off + h * KD + c
+                          : which == 2 ? row + p.v_off + hv * VD + c
+                                       : p.z + tok * p.z_stride + hv * VD + c;
+      pf[i] = *reinterpret_cast<const u32x4*>(src);
+    }
+    const int64_t tok = tok0 + t + min((int)threadIdx.x, last);
+    pa = p.a[tok * p.ab_stride + hv];
+    pb = p.b[tok * p.ab_stride + hv];
+  };
+  if (ntok > 0) fetch(0);
 
   for (int t = 0; t < ntok; ++t) {
     const int tt = t % CT;
-    if (tt == 0) {  // stage the next chunk of tokens in LDS with one burst of coalesced loads
+    if (tt == 0) {  // move the prefetched burst into LDS, then start loading the next one
       const int nt = min(CT, ntok - t);
       __syncthreads();
-      for (int e = threadIdx.x; e < nt * SEGS; e += 256) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int e = threadIdx.x + 256 * i;
         const int u = e / SEGS;
-        const int sg = e - u * SEGS;
+        const int sg = e % SEGS;
         const int which = sg >> 4;
         const int c = (sg & 15) * 8;
-        const uint16_t* row = p.qkv + (tok0 + t + u) * p.qkv_stride;
-        uint16_t* dst;
-        const uint16_t* src;
-        if (which == 0) { src = row + p.q_off + h * KD + c; dst = &sq_[u][c]; }
-        else if (which == 1) { src = row + p.k_off + h * KD + c; dst = &sk_[u][c]; }
-        else if (which == 2) { src = row + p.v_off + hv * VD + c; dst = &sv_[u][c]; }
-        else { src = p.z + (tok0 + t + u) * p.z_stride + hv * VD + c; dst = &sz_[GATED ? u : 0][c]; }
-        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+        uint16_t* dst = which == 0 ? &sq_[u][c] : which == 1 ? &sk_[u][c] : which == 2 ? &sv_[u][c]
+                                                                                     : &sz_[GATED ? u : 0][c];
+        if (u < nt) *reinterpret_cast<u32x4*>(dst) = pf[i];
       }
       if (threadIdx.x < nt) {
-        const int64_t tok = tok0 + t + threadIdx.x;
-        sa_[threadIdx.x] = bf2f(p.a[tok * p.ab_stride + hv]);
-        sb_[threadIdx.x] = bf2f(p.b[tok * p.ab_stride + hv]);
+        sa_[threadIdx.x] = bf2f(pa);
+        sb_[threadIdx.x] = bf2f(pb);
       }
+      if (t + CT < ntok) fetch(t + CT);
       __syncthreads();
     }
     const int64_t tok = tok0 + t;
@@ -238,9 +271,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       const float var = (red[t & 1][0] + red[t & 1][1] + red[t & 1][2] + red[t & 1][3]) * (1.0f / VD);
       const float r = rsqrtf(var + p.eps);
       if (rg == 0) {
-        float y[4], w4[4], z4[4];
-        load4_bf16(p.norm_w + col, w4);
+        float y[4], z4[4], w4[4];
         load4_bf16(&sz_[GATED ? tt : 0][col], z4);
+        load4_bf16(&sw_[GATED ? col : 0], w4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float hb = rbf(ob[i] * r);
@@ -335,7 +368,7 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
                                        const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t L,
                                        int32_t H, int32_t HV, int32_t K, int32_t V, float scale,
                                        const void* z, int64_t z_stride, const void* norm_w, float eps,
-                                       void* out, void* stream) {
+                                       void* out, int32_t skip_rows, int32_t skip_min_len, void* stream) {
   GdnParams p{};
   p.qkv = static_cast<const uint16_t*>(qkv);
   p.qkv_stride = qkv_stride;
@@ -354,9 +387,11 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
   p.norm_w = static_cast<const uint16_t*>(norm_w);
   p.eps = eps;
   p.out = static_cast<uint16_t*>(out);
+  p.skip_rows = skip_rows;
+  p.skip_min_len = skip_min_len;
   const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
   if (rc <= 0) return rc;
-  if (!z || !norm_w || !out) return HSG_ERR_ARG;
-  if (!hsg::aligned(z, 16) || z_stride % 8 || !hsg::aligned(norm_w, 8) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
+  if (!z || !norm_w || !out || skip_rows < 0 || (skip_rows > 0 && skip_min_len < 1)) return HSG_ERR_ARG;
+  if (!hsg::aligned(z, 16) || z_stride % 8 || !hsg::aligned(norm_w, 16) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
   return hsg::launch<true>(p, state_dtype, n_rows, stream);
 }

@@ -33,14 +33,22 @@ SIGNATURES = {
         _P, _I32, _I64,
         _P, _P, _P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F,
-        _P, _P, _P, ctypes.c_size_t, _P]),   # o, sq, workspace, workspace_bytes, stream
+        _P, _P, _I32, _P, ctypes.c_size_t, _P]),   # o, sq, min_len, workspace, workspace_bytes, stream
+    "hsg_gdn_chunk_prefill_gated": (ctypes.c_int, [
+        _P, _I64, _I32, _I32, _I32,
+        _P, _P, _I64, _P, _P,
+        _P, _I32, _I64,
+        _P, _P, _P, _I32, _I32,
+        _I32, _I32, _I32, _I32, _F,
+        _P, _P, _I64, _P, _F, _P,            # o, z, z_stride, norm_w, eps, out
+        _I32, _P, ctypes.c_size_t, _P]),     # min_len, workspace, workspace_bytes, stream
     "hsg_gdn_slot_step_gated": (ctypes.c_int, [
         _P, _I64, _I32, _I32, _I32,
         _P, _P, _I64, _P, _P,
         _P, _I32, _I64,
         _P, _P, _P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F,
-        _P, _I64, _P, _F, _P, _P]),          # z, z_stride, norm_w, eps, out, stream
+        _P, _I64, _P, _F, _P, _I32, _I32, _P]),   # z, z_stride, norm_w, eps, out, skip_rows, skip_min_len, stream
     "hsg_ring_attention": (ctypes.c_int, [
         _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
         _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window

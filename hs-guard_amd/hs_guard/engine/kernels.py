@@ -112,7 +112,7 @@ def gdn_chunk_prefill(packed, key_dim, heads, head_k, value_heads, head_v, a, b,
     rc = lib().hsg_gdn_chunk_prefill(
         _ptr(packed), c, 0, key_dim, 2 * key_dim, _ptr(a), _ptr(b), value_heads, _ptr(A_log), _ptr(dt_bias),
         _ptr(state), _STATE_CODES[state.dtype], state.shape[0], _ptr(slots), _ptr(lens), _ptr(offsets), n,
-        max(length, 1), heads, value_heads, head_k, head_v, scale, _ptr(o), _ptr(sq), _ptr(workspace),
+        max(length, 1), heads, value_heads, head_k, head_v, scale, _ptr(o), _ptr(sq), 0, _ptr(workspace),
         workspace.numel(), _stream(packed.device))
     check(rc, "hsg_gdn_chunk_prefill")
     return o, sq

@@ -120,7 +120,7 @@ class WholeSequenceScorer(PreparedWeights):
                     conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
                     base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), gdn_in,
                     Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), state.data_ptr(), 0, 1, row0.data_ptr(),
-                    row_len.data_ptr(), row0.data_ptr(), 1, T, nh, hv, kd, vd, kd ** -0.5, o.data_ptr(), None,
+                    row_len.data_ptr(), row0.data_ptr(), 1, T, nh, hv, kd, vd, kd ** -0.5, o.data_ptr(), None, 0,
                     ws.data_ptr(), ws.numel(), st), "hsg_gdn_chunk_prefill")
                 gated = torch.empty(T, cfg.value_dim, dtype=bf16, device=dev)
                 check(L.hsg_gated_rmsnorm(o.data_ptr(), cfg.value_dim, base + 2 * C, gdn_in, Lw["norm_w"].data_ptr(),

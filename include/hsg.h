@@ -66,6 +66,8 @@ int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_
  * composed at src/hs_guard/engine/slot_engine_v8.py:234-238):
  *   out[tok, hv*V + c] = bf16( bf16(w[c] * bf16(o*rsqrt(mean(bf16(o)^2)+eps))) * silu(z[tok, hv*V + c]) )
  *   z [tokens, z_stride] bf16, norm_w [V] bf16, out [tokens, HV*V] bf16.
+ * Packed layout: rows n < skip_rows with lens[n] >= skip_min_len (>= 1) are left alone (no output, state
+ * untouched), for hsg_gdn_chunk_prefill_gated to take; skip_rows 0 processes every row.
  */
 int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
                             int32_t v_off, const void* a, const void* b, int64_t ab_stride,
@@ -73,7 +75,8 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
                             int64_t state_rows, const int64_t* slots, const int64_t* lens,
                             const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
                             int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
-                            const void* norm_w, float eps, void* out, void* stream);
+                            const void* norm_w, float eps, void* out, int32_t skip_rows, int32_t skip_min_len,
+                            void* stream);
 
 /*
  * Chunked gated-delta-rule prefill: the same recurrence and contract as hsg_gdn_slot_step, evaluated
@@ -83,6 +86,7 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * Arguments as hsg_gdn_slot_step, except L: the padded row length, and in the packed layout the bound on
  * every row's length (rows with lens[n] > L are treated as empty). o must not alias qkv; o 8-byte and sq
  * 16-byte aligned.
+ * Rows with lens[n] < min_len are left alone (min_len <= 1: every row).
  * Two launches on `stream`: the state-independent part of every (row, chunk, value head) in parallel, then
  * the sequential state products per row. workspace: device memory of at least
  * hsg_gdn_chunk_workspace_bytes(n_rows, L, HV) bytes, 256-byte aligned; no initialisation needed, garbage
@@ -94,7 +98,23 @@ int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, in
                           const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
                           const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
                           int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
-                          float* sq, void* workspace, size_t workspace_bytes, void* stream);
+                          float* sq, int32_t min_len, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The same with the gated RMSNorm of hsg_gdn_slot_step_gated applied (packed layout only): o receives the raw
+ * outputs of the processed rows, out[tok, hv*V + c] their gated RMSNorm with z (z [tokens, z_stride] bf16,
+ * norm_w [V] bf16, out [tokens, HV*V] bf16). A third launch. Together with the skip filter of
+ * hsg_gdn_slot_step_gated it splits one tick's rows between the two kernels: rows n < n_rows with
+ * lens >= min_len here, the others in the slot step. No counterpart of its own in the reference (it composes
+ * chunk_gated_delta_rule and gated_finish, src/hs_guard/engine/fused_kernels.py:215-233).
+ */
+int hsg_gdn_chunk_prefill_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
+                                const void* a, const void* b, int64_t ab_stride, const void* A_log,
+                                const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
+                                const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
+                                int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
+                                const void* z, int64_t z_stride, const void* norm_w, float eps, void* out,
+                                int32_t min_len, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Window-W GQA attention of this tick's queries over the slot's ring plus this tick's new keys.

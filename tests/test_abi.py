@@ -71,10 +71,10 @@ def test_argument_errors_are_rejected_before_launch():
     need = L.hsg_gdn_chunk_workspace_bytes(4, 100, 16)
     args = [256, 6144, 0, 2048, 4096, 256, 256, 16, 256, 256, 256, 0, 17, 256, 256, None, 4, 100, 16, 16, 128, 128,
             1.0, 256, None]
-    assert L.hsg_gdn_chunk_prefill(*args, 256, need - 1, None) == -3
-    assert L.hsg_gdn_chunk_prefill(*args, 128, need, None) == -2
+    assert L.hsg_gdn_chunk_prefill(*args, 0, 256, need - 1, None) == -3
+    assert L.hsg_gdn_chunk_prefill(*args, 0, 128, need, None) == -2
     args[17] = 0
-    assert L.hsg_gdn_chunk_prefill(*args, 256, need, None) == -1
+    assert L.hsg_gdn_chunk_prefill(*args, 0, 256, need, None) == -1
     # n_rows == 0 is a no-op success
     assert L.hsg_ring_attention(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
                                 0, 0, None, None, None, None, None, 0, 1, 4, 4, 256, 1.0, 0, 0, None, 0, 0, 0, 0,

@@ -193,3 +193,62 @@ def test_chunk_prefill_equals_streamed_slot_steps():
     assert rel <= STATE_TOL and mx <= STATE_TOL, f"state error norm {rel:.2e} max {mx:.2e}"
     bad, worst = _out_close(_np(o_chunk), _np(torch.cat(outs, 1)), rtol=2.0 ** -7)
     assert bad == 0, f"{bad} outputs differ (max diff {worst:.3e})"
+
+
+def test_tick_split_between_slot_step_and_chunk():
+    """The engine's split of one packed tick: rows n < R with lens >= 9 through hsg_gdn_chunk_prefill_gated (raw
+    outputs, then the gated RMSNorm), every other row through hsg_gdn_slot_step_gated with the matching skip
+    filter. Against the whole tick through the slot step alone: states within 1e-3 relative, gated outputs
+    within two bf16 steps; a row of >= 9 tokens at n >= R stays in the slot step."""
+    from hs_guard._lib import lib
+    print("[chunk] tick split slot step / chunk", flush=True)
+    gen = torch.Generator().manual_seed(21)
+    H, HV, K = 2, 4, 128
+    C = 2 * H * K + HV * K
+    stride = C + HV * K + 2 * HV               # qkv | z | b | a, the engine's fused projection
+    lens = torch.tensor([40, 12, 1, 9, 11, 3, 0], dtype=torch.long)
+    offsets = torch.cat([torch.zeros(1, dtype=torch.long), torch.cumsum(lens, 0)[:-1]])
+    T, R, THR = int(lens.sum()), 4, 9
+    proj = torch.randn(T, stride, generator=gen).to(torch.bfloat16)
+    A_log = (torch.rand(HV, generator=gen) * 2 - 1).to(torch.bfloat16)
+    dt = torch.randn(HV, generator=gen).to(torch.bfloat16)
+    norm_w = (1 + 0.1 * torch.randn(K, generator=gen)).to(torch.bfloat16)
+    state0 = torch.randn(8, HV, K, K, generator=gen) * 0.05
+    slots = torch.tensor([6, 2, 0, 4, 1, 7, 3], dtype=torch.long)
+    dev = torch.device("cuda:0")
+    P, A_d, dt_d, w_d = proj.to(dev), A_log.to(dev), dt.to(dev), norm_w.to(dev)
+    sl, ln, of = slots.to(dev), lens.to(dev), offsets.to(dev)
+    st = torch.cuda.current_stream().cuda_stream
+    base = P.data_ptr()
+    a_ptr, b_ptr, z_ptr = base + 2 * (C + HV * K + HV), base + 2 * (C + HV * K), base + 2 * C
+
+    def slot_step(state, out, skip_rows):
+        assert lib().hsg_gdn_slot_step_gated(base, stride, 0, H * K, 2 * H * K, a_ptr, b_ptr, stride, A_d.data_ptr(),
+                                             dt_d.data_ptr(), state.data_ptr(), 0, 8, sl.data_ptr(), ln.data_ptr(),
+                                             of.data_ptr(), 7, 0, H, HV, K, K, K ** -0.5, z_ptr, stride,
+                                             w_d.data_ptr(), 1e-6, out.data_ptr(), skip_rows, THR, st) == 0
+
+    s_ref, o_ref = state0.to(dev), torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
+    slot_step(s_ref, o_ref, 0)
+    s_split, o_split = state0.to(dev), torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
+    slot_step(s_split, o_split, R)
+    raw = torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(lib().hsg_gdn_chunk_workspace_bytes(R, 64, HV), dtype=torch.uint8, device=dev)
+    assert lib().hsg_gdn_chunk_prefill_gated(base, stride, 0, H * K, 2 * H * K, a_ptr, b_ptr, stride, A_d.data_ptr(),
+                                             dt_d.data_ptr(), s_split.data_ptr(), 0, 8, sl.data_ptr(), ln.data_ptr(),
+                                             of.data_ptr(), R, 64, H, HV, K, K, K ** -0.5, raw.data_ptr(), z_ptr,
+                                             stride, w_d.data_ptr(), 1e-6, o_split.data_ptr(), THR, ws.data_ptr(),
+                                             ws.numel(), st) == 0
+    torch.cuda.synchronize()
+    chunk_rows = [n for n in range(R) if lens[n] >= THR]
+    assert chunk_rows == [0, 1, 3]
+    for n in range(7):   # the skip filter left exactly the chunk rows to the chunk kernels
+        ln_n, off = int(lens[n]), int(offsets[n])
+        if ln_n == 0:
+            continue
+        bad, worst = _out_close(_np(o_split[off:off + ln_n]), _np(o_ref[off:off + ln_n]), rtol=2.0 ** -7)
+        assert bad == 0, f"row {n}: {bad} outputs off (max diff {worst:.3e})"
+    for s in range(8):
+        rel, mx = _state_err(_np(s_split[s]), _np(s_ref[s]))
+        assert rel <= STATE_TOL and mx <= STATE_TOL, f"slot {s}: state error norm {rel:.2e} max {mx:.2e}"
+    np.testing.assert_array_equal(_np(s_split[5]), _np(state0[5]))   # unused slot

@@ -133,7 +133,7 @@ def test_packed_gated_matches_oracle():
         proj_d.data_ptr(), stride, 0, H * K, 2 * H * K, ab_d[:, HV:].data_ptr(), ab_d.data_ptr(), 2 * HV,
         A_d.data_ptr(), dt_d.data_ptr(), state.data_ptr(), 0, 6, slots_d.data_ptr(), lens_d.data_ptr(),
         off_d.data_ptr(), 4, 0, H, HV, K, K, K ** -0.5, proj_d[:, C:].data_ptr(), stride, w_d.data_ptr(), 1e-6,
-        out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        out.data_ptr(), 0, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     # oracle in padded form
     L = int(lens.max())
