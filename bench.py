@@ -71,7 +71,7 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
                                          base + 2 * (C + HV * V), stride, A.data_ptr(), A.data_ptr(), state.data_ptr(),
                                          state_dtype, rows + 1, slots.data_ptr(), lens.data_ptr(), offs.data_ptr(),
                                          rows, 0, H, HV, K, V, K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6,
-                                         out.data_ptr(), stream.cuda_stream)
+                                         out.data_ptr(), 0, 0, stream.cuda_stream)
         assert rc == 0, rc
     for _ in range(10):
         launch()
