@@ -51,15 +51,17 @@ constexpr int VD = 128;
 constexpr int CH = 64;             // tokens per chunk
 constexpr int BV = 64;             // value columns per workgroup
 constexpr int KS = KD + 8;         // Ks / Qs row stride (bf16): token-major rows of keys
-constexpr int TS = CH + 4;         // row stride (bf16) of the 64-column LDS planes (M', P, -A)
-constexpr int VS = BV + 8;         // Vs row stride (bf16): token-major rows of the block's values
+constexpr int TS = CH + 4;         // row stride (bf16) of the prep kernel's -A plane in LDS
+constexpr int VS = BV + 16;        // Vs row stride (bf16): 40 dwords, so the 4 x 4 pieces of a transpose read
+                                   // fall in 16 distinct bank pairs
 constexpr int DS = 20;             // diagonal-block row stride (fp32) and diagonal-inverse row stride (bf16)
-constexpr int PL = CH * TS;        // one 64 x 64 bf16 plane of the workspace, rows padded to TS (the LDS layout)
+constexpr int PW = CH;             // row width (bf16) of the workspace planes M', P (swizzled rows, see swz)
+constexpr int PL = CH * PW;        // one 64 x 64 bf16 plane of the workspace (also the state kernel's LDS layout)
 constexpr int VEC = 256;           // per-token factor floats of a workspace unit: e^G rk, rq e^G, rk e^(G_C-G),
                                    // then e^(G_C) and padding
 // one workspace unit per (row, chunk, value head): planes M'hi, M'lo, Phi, Plo, then the factors
-constexpr int PLANE_PIECES = 4 * PL * 2 / 16;   // 16-byte pieces of the four planes (2176)
 constexpr int UNIT_BYTES = 4 * PL * 2 + VEC * 4;
+constexpr int ORDER_MAX = 4096;    // rows ranked by the order kernel (more rows keep their given order)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) short s16x8;
@@ -88,6 +90,7 @@ struct ChunkParams {
   uint16_t* o;
   float* sq;
   uint8_t* ws;
+  int32_t* order;                  // state kernel row order (in the workspace after the units)
   // gated epilogue (hsg_gdn_chunk_prefill_gated): out = gated RMSNorm of o with z
   const uint16_t* z;
   int64_t z_stride;
@@ -107,16 +110,14 @@ __device__ __forceinline__ f32x4 mma32(s16x8 a, s16x8 b, f32x4 c) {
 
 __device__ __forceinline__ s16x8 cat(s16x4 x, s16x4 y) { return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7); }
 
-// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even. The rounding is done in
-// integer arithmetic: a build of this kernel using the compiler's __bf16 conversion produced wrong values in
-// a few rows of one tile on gfx950, while the identical kernel with this conversion is exact.
+// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even, on the packed hardware
+// conversion (three VALU instructions per element instead of seven for the integer rounding)
 __device__ __forceinline__ void split4(f32x4 x, s16x4& hi, s16x4& lo) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint16_t h = f2bf_finite(x[i]);
-    hi[i] = (short)h;
-    lo[i] = (short)f2bf_finite(x[i] - bf2f(h));
-  }
+  const uint32_t h01 = pack_bf16x2(x[0], x[1]), h23 = pack_bf16x2(x[2], x[3]);
+  const uint32_t l01 = pack_bf16x2(x[0] - __uint_as_float(h01 << 16), x[1] - __uint_as_float(h01 & 0xffff0000u));
+  const uint32_t l23 = pack_bf16x2(x[2] - __uint_as_float(h23 << 16), x[3] - __uint_as_float(h23 & 0xffff0000u));
+  hi = __builtin_bit_cast(s16x4, (uint64_t)h01 | ((uint64_t)h23 << 32));
+  lo = __builtin_bit_cast(s16x4, (uint64_t)l01 | ((uint64_t)l23 << 32));
 }
 
 __device__ __forceinline__ f32x4 ld4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
@@ -157,9 +158,9 @@ __device__ __forceinline__ f32x4 split_product(const uint16_t* hrow, const uint1
 __device__ __forceinline__ float exp_nonpos(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 __device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, float x) {
-  const uint16_t h = f2bf_finite(x);
-  *hi = h;
-  *lo = f2bf_finite(x - bf2f(h));
+  const uint32_t h = pack_bf16x2(x, 0.f);
+  *hi = (uint16_t)h;
+  *lo = (uint16_t)pack_bf16x2(x - __uint_as_float(h << 16), 0.f);
 }
 
 // workgroup barrier that orders LDS only (outstanding global prefetches stay in flight)
@@ -175,6 +176,45 @@ __device__ __forceinline__ void lds_barrier() {
 // column c0 + s of rows r0 .. r0 + 3: the MFMA operand layout of the transposed tile.
 __device__ __forceinline__ s16x4 ld4h_tr(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// The state kernel's K and Q tiles are unpadded 256-byte token rows whose 8-byte pieces are permuted within each
+// row: logical piece c of row r is stored at piece c ^ swz(r). A row read (16 lanes: 16 consecutive rows, one
+// piece) and a transpose read (16 lanes: 4 rows x 4 consecutive pieces) then both touch 16 distinct 8-byte bank
+// pairs, where any padding of the row leaves one of the two patterns with 2- to 4-way bank conflicts.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// offset (bf16) of logical 4-element piece c in swizzled row r
+__device__ __forceinline__ int swz_at(int r, int c) { return r * KD + 4 * (c ^ swz(r)); }
+
+// the same for the 64-column planes M' and P (16 pieces per row; the XOR permutes all of them)
+__device__ __forceinline__ int pw_at(int r, int c) { return r * PW + 4 * (c ^ swz(r)); }
+
+// split_product on a swizzled plane pair: hrow / lrow = row 16 I + m of the hi / lo planes, po[J] = offset of
+// the lane's logical piece 4 J + g in that row (rows 16 I + m share swz(m))
+template <int NJ, bool TR = false>
+__device__ __forceinline__ f32x4 split_product_sw(const uint16_t* hrow, const uint16_t* lrow, const int* po,
+                                                  const s16x4* bh, const s16x4* bl, f32x4 acc) {
+  auto mm = [](s16x8 m, s16x8 b, f32x4 c) { return TR ? mma32(b, m, c) : mma32(m, b, c); };
+#pragma unroll
+  for (int J = 0; J + 1 < NJ; J += 2) {
+    const s16x8 ah = cat(ld4h(hrow + po[J]), ld4h(hrow + po[J + 1]));
+    const s16x8 al = cat(ld4h(lrow + po[J]), ld4h(lrow + po[J + 1]));
+    const s16x8 b_h = cat(bh[J], bh[J + 1]), b_l = cat(bl[J], bl[J + 1]);
+    acc = mm(al, b_h, acc);
+    acc = mm(ah, b_l, acc);
+    acc = mm(ah, b_h, acc);
+  }
+  if constexpr (NJ % 2 == 1) {
+    constexpr int J = NJ - 1;
+    const s16x4 z = {0, 0, 0, 0};
+    const s16x8 ah = cat(ld4h(hrow + po[J]), z), al = cat(ld4h(lrow + po[J]), z);
+    const s16x8 b_h = cat(bh[J], z), b_l = cat(bl[J], z);
+    acc = mm(al, b_h, acc);
+    acc = mm(ah, b_l, acc);
+    acc = mm(ah, b_h, acc);
+  }
+  return acc;
 }
 
 template <typename ST>
@@ -367,8 +407,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
         *reinterpret_cast<s16x4*>(&Al[i * TS + j0]) = vl;
         if (I == J) *reinterpret_cast<f32x4*>(&Dg[i * DS + 4 * g4]) = -v;
       } else {
-        *reinterpret_cast<s16x4*>(&Ph_g[i * TS + j0]) = vh;
-        *reinterpret_cast<s16x4*>(&Pl_g[i * TS + j0]) = vl;
+        *reinterpret_cast<s16x4*>(&Ph_g[pw_at(i, j0 >> 2)]) = vh;
+        *reinterpret_cast<s16x4*>(&Pl_g[pw_at(i, j0 >> 2)]) = vl;
       }
     }
   }
@@ -403,7 +443,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
   // ---- M_I = T_II (E_I - sum_{J<I} A_IJ M_J) for this wave's columns 16w + m16 (E = identity), then
   // M' = M diag(beta), transposed through LDS (the Ks area) into 16-byte stores to the workspace ----
   uint16_t* const Mh_s = Ks;
-  uint16_t* const Ml_s = Ks + CH * TS;
+  uint16_t* const Ml_s = Ks + PL;
   {
     const float bcol = b_s[16 * wave + m16];
     s16x4 Mh[4], Ml[4];
@@ -427,13 +467,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
       split4(v, Mh[I], Ml[I]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int at = (16 * I + 4 * g4 + r) * TS + 16 * wave + m16;
+        const int at = pw_at(16 * I + 4 * g4 + r, 4 * wave + (m16 >> 2)) + (m16 & 3);
         store_split(&Mh_s[at], &Ml_s[at], v[r] * bcol);
       }
     }
   }
   lds_barrier();
-  // the two planes are contiguous in LDS and in the workspace with the same padded rows: a linear copy
+  // the two planes are contiguous in LDS and in the workspace with the same swizzled rows: a linear copy
 #pragma unroll
   for (int i = 0; i < (2 * PL * 2 / 16 + 255) / 256; ++i) {
     const int x = threadIdx.x + 256 * i;
@@ -443,12 +483,53 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// State: walks one row's chunks in order for one value head and 64 value columns.
+// Order: the state kernel runs rows with more chunks first (ties by row index). Its workgroups are dispatched in
+// this order, so when not all of them fit on the GPU at once, the rows with the longest chunk chains, which
+// bound the kernel's duration, start at once instead of after shorter rows.
 // ---------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void gdn_chunk_order_kernel(const ChunkParams p, int n_rows) {
+  __shared__ int nch[ORDER_MAX];
+  if (n_rows > ORDER_MAX) {
+    for (int j = threadIdx.x; j < n_rows; j += 1024) p.order[j] = j;
+    return;
+  }
+  for (int j = threadIdx.x; j < n_rows; j += 1024) {
+    int64_t slot, tok0;
+    nch[j] = (row_tokens(p, j, slot, tok0) + CH - 1) / CH;
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < n_rows; j += 1024) {
+    const int cj = nch[j];
+    int rank = 0;
+    for (int i = 0; i < n_rows; ++i) {
+      const int ci = nch[i];
+      rank += (ci > cj) || (ci == cj && i < j);
+    }
+    p.order[rank] = j;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// State: walks one row's chunks in order for one value head and 64 value columns, with 8 waves in two roles.
+// Chain waves (0-3) own value columns 16 w .. 16 w + 15 of the block (w = wave & 3), keep S[:, those] in
+// accumulator layout and run the products on the state's dependency chain: Y = Kr S, Z, V' = M' Z and the
+// state update. Output waves (4-7) compute Q S and O for the same columns from the chain's split S and V',
+// handed over through LDS, so those products run beside the chain instead of on it. The next chunk is fetched
+// at the top of each chunk (K, M' and the factors by the chain waves, Q, V and P by the output waves) and
+// staged at its end, into second buffers where a tile is still being read then (K, P, the factors). Of the
+// planes only the lower-triangle blocks are copied. Per chunk:
+//   chain:  fetch K M' factors | split S -> Sx | B1 | Y, Z, V' -> Vx      | B2 | W, S update, stage      | B0
+//   output: fetch Q V P                        | B1 | Sx -> Q S (64 x 16) | B2 | Vx -> O, stage, store O | B0
+// ---------------------------------------------------------------------------------------------------------
+constexpr int XP = 64 * 4;         // one handed-over fragment: 64 lanes x 4 bf16
+constexpr int TRI_SLOTS = 320;     // 16-byte slots of a plane's lower-triangle blocks: 16 rows x 2 (I + 1), I < 4
+
 template <typename ST>
-__global__ __launch_bounds__(256) void gdn_chunk_state_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int w = wave & 3;                              // column group of the wave (both roles)
+  const bool chain = __builtin_amdgcn_readfirstlane(wave) < 4;   // wave-uniform role
   const int m16 = lane & 15;
   const int g4 = lane >> 4;
   // the two value blocks of one (row, head) are dispatched 8 workgroups apart, i.e. on the same XCD, so
@@ -457,17 +538,18 @@ __global__ __launch_bounds__(256) void gdn_chunk_state_kernel(const ChunkParams 
   const int vb = (bid >> 3) & 1;
   const int pair = ((bid >> 4) << 3) | (bid & 7);
   if (pair >= p.pairs) return;
-  const int n = pair / p.HV;
-  const int hv = pair - n * p.HV;
+  const int rank = pair / p.HV;
+  const int hv = pair - rank * p.HV;
+  const int n = p.order[rank];
   const int h = hv / (p.HV / p.H);
   int64_t slot, tok0;
   const int ntok = row_tokens(p, n, slot, tok0);
   const bool padded = p.offsets == nullptr;
-  const int vcol = vb * BV + wave * 16 + m16;          // this lane's value column (accumulator layout)
+  const int vcol = vb * BV + w * 16 + m16;             // this lane's value column (accumulator layout)
   const int64_t ostride = (int64_t)p.HV * VD;
 
   if (padded) {  // positions past the row's length are zeros in the padded layout
-    for (int t = ntok + threadIdx.x / BV; t < p.L; t += 256 / BV) {
+    for (int t = ntok + threadIdx.x / BV; t < p.L; t += 512 / BV) {
       const int64_t at = (tok0 + t) * ostride + hv * VD + vb * BV + (threadIdx.x % BV);
       p.o[at] = 0;
       if (p.sq) p.sq[at] = 0.f;
@@ -475,213 +557,291 @@ __global__ __launch_bounds__(256) void gdn_chunk_state_kernel(const ChunkParams 
   }
   if (ntok == 0) return;
 
-  // token-major K, Q and V tiles; K^T and the token-column V fragments are read with transpose reads
-  __shared__ __align__(16) uint16_t Ks[CH * KS];
-  __shared__ __align__(16) uint16_t Qs[CH * KS];
+  // token-major K (two buffers), Q (swizzled rows, see swz) and V tiles; K^T and the token-column V fragments
+  // are read with transpose reads
+  __shared__ __align__(16) uint16_t Ks[2][CH * KD];
+  __shared__ __align__(16) uint16_t Qs[CH * KD];
   __shared__ __align__(16) uint16_t Vs[CH * VS];
-  // M' and P (lower triangles) as bf16 hi / lo planes, token-major rows: plane e at Pn[e * CH * TS]
-  __shared__ __align__(16) uint16_t Pn[4 * CH * TS];
-  __shared__ __align__(16) float vec_s[VEC];
+  // M' and P (two buffers) as bf16 hi / lo planes of swizzled token-major rows (lower triangles used)
+  __shared__ __align__(16) uint16_t Ms[2 * PL];
+  __shared__ __align__(16) uint16_t Ps[2][2 * PL];
+  __shared__ __align__(16) float vec_s[2][VEC];
+  // hand-over from chain to output waves, in the chain lanes' register layout (lane-linear 8-byte pieces):
+  // Sx[w][2 mt + hl] = split S block mt of column group w, Vx[w][2 I + hl] = split V' token block I
+  __shared__ __align__(16) uint16_t Sx[4 * 16 * XP];
+  __shared__ __align__(16) uint16_t Vx[4 * 8 * XP];
 
-  // ---- state S[:, vcol] in accumulator layout: block mt holds keys 16 mt + 4 g4 + r ----
+  // ---- state S[:, vcol] in accumulator layout (chain waves): block mt holds keys 16 mt + 4 g4 + r ----
   ST* sbase = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * (int64_t)KD) * VD + vcol;
   f32x4 S[8];
+  if (chain) {
 #pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[mt][r] = load_state<ST>(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD);
-
-  // ---- staging coordinates: token st_t of the chunk; 16-byte pieces g4 + 4 it ----
-  const int st_t = 16 * wave + m16;
-  constexpr int PM = (PLANE_PIECES + 255) / 256;   // plane pieces per thread (the last partly idle)
-  u32x4 pk[4], pq[4], pv[2], pm[PM];
-  float pf;
-  // Loads are unconditional: a position past the row's end reads the row's first token instead, and its
-  // zero factors (rk, rq, and the zero columns of M' and P) cancel it everywhere, so no select can turn into
-  // a memory-backed zero or a branch around the loads. The prefetch of the next chunk is issued in four
-  // groups between this chunk's compute phases (pinned there by scheduling barriers): issued at once, its
-  // ~900 cache lines per CU stalled instruction issue for about one memory round trip.
-  auto row_of = [&](int c0) { return p.qkv + (tok0 + (c0 + st_t < ntok ? c0 + st_t : 0)) * p.qkv_stride; };
-  auto fetch_kq = [&](const uint16_t* row) {
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int pc = 8 * (g4 + 4 * it);
-      pk[it] = *reinterpret_cast<const u32x4*>(row + p.k_off + h * KD + pc);
-      pq[it] = *reinterpret_cast<const u32x4*>(row + p.q_off + h * KD + pc);
-    }
-  };
-  auto fetch_v = [&](const uint16_t* row, const uint8_t* unit) {
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int pc = 8 * (g4 + 4 * it);
-      pv[it] = *reinterpret_cast<const u32x4*>(row + p.v_off + hv * VD + vb * BV + pc);
-    }
-    pf = reinterpret_cast<const float*>(unit + 4 * PL * 2)[threadIdx.x];
-  };
-  // piece x = threadIdx.x + 256 i of the planes, clamped to the last piece (re-read, never written twice)
-  auto fetch_planes = [&](const uint8_t* unit, int half) {
-    const u32x4* planes = reinterpret_cast<const u32x4*>(unit);
-#pragma unroll
-    for (int i = half ? PM / 2 : 0; i < (half ? PM : PM / 2); ++i)
-      pm[i] = planes[min((int)threadIdx.x + 256 * i, PLANE_PIECES - 1)];
-  };
-
-  {
-    const uint16_t* row = row_of(0);
-    const uint8_t* unit = unit_ptr(p, n, 0, hv);
-    fetch_kq(row);
-    fetch_v(row, unit);
-    fetch_planes(unit, 0);
-    fetch_planes(unit, 1);
+      for (int r = 0; r < 4; ++r) S[mt][r] = load_state<ST>(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD);
   }
-  for (int c0 = 0; c0 < ntok; c0 += CH) {
-    const int nv = min(CH, ntok - c0);
-    lds_barrier();  // every read of the previous chunk's LDS data is done
-    {
+
+  // ---- swizzled K / Q read offsets (bf16), fixed per lane. Logical piece c of row r sits at c ^ swz(r), and
+  // the XOR touches only the low four bits of c, so bit 4 of c (64 bf16) and the row block (16 rows, whose
+  // swz is the same) are plain offsets added at the read.
+  // yo[2 b + h]: row m16, logical piece g4 + 4 h + 8 b (the row reads of Y and Q S);
+  // ko[u]:       row kr = 4 g4 + m16 / 4, logical piece 4 u + m16 % 4 (the transpose reads of K^T). ----
+  // po[J]:       plane row m16, logical piece 4 J + g4 (the row reads of M' and P). ----
+  int yo[4], ko[4], po[4];
+  {
+    const int kr = 4 * g4 + (m16 >> 2);
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int pc = 8 * (g4 + 4 * it);
-        *reinterpret_cast<u32x4*>(&Ks[st_t * KS + pc]) = pk[it];
-        *reinterpret_cast<u32x4*>(&Qs[st_t * KS + pc]) = pq[it];
+    for (int u = 0; u < 4; ++u) {
+      yo[u] = swz_at(m16, g4 + 4 * (u & 1) + 8 * (u >> 1));
+      ko[u] = swz_at(kr, 4 * u + (m16 & 3));
+      po[u] = 4 * ((4 * u + g4) ^ swz(m16));
+    }
+  }
+
+  // ---- staging: thread x of a role (x = threadIdx.x % 256) handles token st_t = x / 4 of the chunk: 16-byte
+  // pieces sp + 4 j of its K (chain) or Q (output) row and pieces sp, sp + 4 of its 64 values (output), the
+  // lower-triangle plane slots x + 256 i of M' (chain) or P (output) and factor x (chain). Loads are
+  // unconditional: a position past the row's end reads the row's first token instead, and its zero factors
+  // (rk, rq, and the zero columns of M' and P) cancel it everywhere, so no select can turn into a
+  // memory-backed zero or a branch around the loads.
+  const int rx = threadIdx.x & 255;
+  const int st_t = rx >> 2;
+  const int sp = rx & 3;
+  // slot q of a plane pair (hi then lo plane, 320 slots each; row block I has 2 (I + 1) slots per row): the
+  // slot holds 16-byte piece k of the row's lower triangle, i.e. logical pieces 4 (k / 2) .. +3, whose
+  // physical 16-byte slot is 2 ((k / 2) ^ (swz(row) >> 2)) + k % 2 (the XOR keeps aligned groups of four)
+  int qoff[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int q = min(rx + 256 * i, 2 * TRI_SLOTS - 1);
+    const int e = q >= TRI_SLOTS;
+    const int qq = q - TRI_SLOTS * e;
+    const int I = qq >= 192 ? 3 : qq >= 96 ? 2 : qq >= 32 ? 1 : 0;
+    const int n2 = 2 * (I + 1);
+    const int q2 = qq - (I == 3 ? 192 : I == 2 ? 96 : I == 1 ? 32 : 0);
+    const int row = 16 * I + q2 / n2;
+    const int k = q2 - (q2 / n2) * n2;
+    qoff[i] = e * PL + row * PW + 8 * (2 * ((k >> 1) ^ (swz(row) >> 2)) + (k & 1));
+  }
+  const bool third = rx + 512 < 2 * TRI_SLOTS;
+  auto row_of = [&](int c0) { return p.qkv + (tok0 + (c0 + st_t < ntok ? c0 + st_t : 0)) * p.qkv_stride; };
+  // 16-byte piece j of a K / Q row holds logical 8-byte pieces 2j, 2j + 1: it lands in 16-byte slot
+  // j ^ (swz >> 1), its halves exchanged when swz is odd
+  auto stage_rows = [&](uint16_t* tile, const u32x4* pr) {
+    const int sg = swz(st_t);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int at = st_t * KD + 8 * ((sp + 4 * j) ^ (sg >> 1));
+      *reinterpret_cast<u32x4*>(&tile[at]) = (sg & 1) ? pr[j].zwxy : pr[j];
+    }
+  };
+  uint16_t* const sx = Sx + w * 16 * XP + 4 * lane;
+  uint16_t* const vx = Vx + w * 8 * XP + 4 * lane;
+  // The two roles run separate loops with the same barriers (three per chunk, after a staging barrier), so
+  // the registers of one role are not held across the other's code.
+  if (chain) {
+    u32x4 pk[4], pm[3];
+    float pf;
+    auto fetch = [&](int c0) {
+      const uint16_t* row = row_of(c0);
+      const uint8_t* unit = unit_ptr(p, n, c0 / CH, hv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pk[j] = *reinterpret_cast<const u32x4*>(row + p.k_off + h * KD + 8 * (sp + 4 * j));
+#pragma unroll
+      for (int i = 0; i < 3; ++i) pm[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(unit) + qoff[i]);
+      pf = reinterpret_cast<const float*>(unit + 4 * PL * 2)[rx];
+    };
+    auto stage = [&](int buf) {
+      stage_rows(Ks[buf], pk);
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (i < 2 || third) *reinterpret_cast<u32x4*>(Ms + qoff[i]) = pm[i];
+      vec_s[buf][rx] = pf;
+    };
+    fetch(0);
+    stage(0);
+    lds_barrier();  // B0: chunk 0 staged
+    int cb = 0;
+    for (int c0 = 0; c0 < ntok; c0 += CH, cb ^= 1) {
+      const uint16_t* const K_ = Ks[cb];
+      const float* const vec = vec_s[cb];
+      // the next chunk (or this one again after the last: staged into idle buffers and never read)
+      fetch(c0 + CH < ntok ? c0 + CH : c0);
+      s16x4 Sh[8], Sl[8];
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        split4(S[mt], Sh[mt], Sl[mt]);
+        *reinterpret_cast<s16x4*>(sx + (2 * mt) * XP) = Sh[mt];
+        *reinterpret_cast<s16x4*>(sx + (2 * mt + 1) * XP) = Sl[mt];
+      }
+      lds_barrier();  // B1: split S handed over
+
+      // ---- Y = Kr S for this wave's 16 value columns: S split hi / lo, key blocks paired ----
+      f32x4 Y[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const int a0 = yo[2 * (q2 & 1)] + 64 * (q2 >> 1) + 16 * I * KD;
+          const int a1 = yo[2 * (q2 & 1) + 1] + 64 * (q2 >> 1) + 16 * I * KD;
+          const s16x8 ka = cat(ld4h(K_ + a0), ld4h(K_ + a1));
+          y = mma32(ka, cat(Sl[2 * q2], Sl[2 * q2 + 1]), y);
+          y = mma32(ka, cat(Sh[2 * q2], Sh[2 * q2 + 1]), y);
+        }
+        Y[I] = y;
+      }
+      // ---- Z = Vr - e^G rk . Y, split (V[16 I + 4 g4 + r][column 16 w + m16] by a transpose read) ----
+      s16x4 Zh[4], Zl[4];
+      const uint16_t* vfrag = Vs + (4 * g4 + (m16 >> 2)) * VS + w * 16 + 4 * (m16 & 3);
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        const f32x4 e1 = ld4f(&vec[16 * I + 4 * g4]);
+        const s16x4 v4 = ld4h_tr(vfrag + 16 * I * VS);
+        f32x4 z;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = bf2f((uint16_t)v4[r]) - e1[r] * Y[I][r];
+        split4(z, Zh[I], Zl[I]);
+      }
+      // ---- V'_I = sum_{J<=I} M'_IJ Z_J (M' lower triangular), handed over split ----
+      f32x4 Vp[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t* mh = Ms + (16 * I + m16) * PW;
+        const uint16_t* ml = mh + PL;
+        if (I == 0) acc = split_product_sw<1>(mh, ml, po, Zh, Zl, acc);
+        if (I == 1) acc = split_product_sw<2>(mh, ml, po, Zh, Zl, acc);
+        if (I == 2) acc = split_product_sw<3>(mh, ml, po, Zh, Zl, acc);
+        if (I == 3) acc = split_product_sw<4>(mh, ml, po, Zh, Zl, acc);
+        Vp[I] = acc;
+        s16x4 vh, vl;
+        split4(acc, vh, vl);
+        *reinterpret_cast<s16x4*>(vx + (2 * I) * XP) = vh;
+        *reinterpret_cast<s16x4*>(vx + (2 * I + 1) * XP) = vl;
+      }
+      lds_barrier();  // B2: split V' handed over; Q, V and M' of this chunk are no longer read
+
+      // ---- S <- e^(G_C) S + Kr^T W,  W = rk e^(G_C - G) . V' (token blocks paired) ----
+      s16x4 Wh[4], Wl[4];
+#pragma unroll
+      for (int J = 0; J < 4; ++J) split4(Vp[J] * ld4f(&vec[2 * CH + 16 * J + 4 * g4]), Wh[J], Wl[J]);
+      const float gc = vec[3 * CH];
+      // K^T operand: lane m16 of group g4 gets key 16 mt + m16 of tokens 16 J + 4 g4 .. +3 (transpose read)
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int ka0 = ko[mt & 3] + 64 * (mt >> 2);
+#pragma unroll
+        for (int J = 0; J < 4; J += 2) {
+          const s16x8 ka = cat(ld4h_tr(K_ + ka0 + 16 * J * KD), ld4h_tr(K_ + ka0 + 16 * (J + 1) * KD));
+          acc = mma32(ka, cat(Wl[J], Wl[J + 1]), acc);
+          acc = mma32(ka, cat(Wh[J], Wh[J + 1]), acc);
+        }
+        S[mt] = S[mt] * gc + acc;
+      }
+      stage(cb ^ 1);
+      lds_barrier();  // B0: the next chunk is staged
+    }
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) store_state(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD, S[mt][r]);
+  } else {
+    u32x4 pq[4], pv[2], pp[3];
+    auto fetch = [&](int c0) {
+      const uint16_t* row = row_of(c0);
+      const uint16_t* unit = reinterpret_cast<const uint16_t*>(unit_ptr(p, n, c0 / CH, hv));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pq[j] = *reinterpret_cast<const u32x4*>(row + p.q_off + h * KD + 8 * (sp + 4 * j));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        pv[j] = *reinterpret_cast<const u32x4*>(row + p.v_off + hv * VD + vb * BV + 8 * (sp + 4 * j));
+#pragma unroll
+      for (int i = 0; i < 3; ++i) pp[i] = *reinterpret_cast<const u32x4*>(unit + 2 * PL + qoff[i]);
+    };
+    auto stage = [&](int buf) {
+      stage_rows(Qs, pq);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(&Vs[st_t * VS + 8 * (sp + 4 * j)]) = pv[j];
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (i < 2 || third) *reinterpret_cast<u32x4*>(Ps[buf] + qoff[i]) = pp[i];
+    };
+    fetch(0);
+    stage(0);
+    lds_barrier();  // B0: chunk 0 staged
+    int cb = 0;
+    for (int c0 = 0; c0 < ntok; c0 += CH, cb ^= 1) {
+      const int nv = min(CH, ntok - c0);
+      const float* const vec = vec_s[cb];
+      fetch(c0 + CH < ntok ? c0 + CH : c0);
+      lds_barrier();  // B1: split S handed over
+
+      // ---- QS^T = S^T Qr^T (value rows, token columns) from the handed-over split S ----
+      s16x4 Sh[8], Sl[8];
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        Sh[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt) * XP);
+        Sl[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt + 1) * XP);
+      }
+      f32x4 X[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        f32x4 qs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const int a0 = yo[2 * (q2 & 1)] + 64 * (q2 >> 1) + 16 * I * KD;
+          const int a1 = yo[2 * (q2 & 1) + 1] + 64 * (q2 >> 1) + 16 * I * KD;
+          const s16x8 qa = cat(ld4h(Qs + a0), ld4h(Qs + a1));
+          qs = mma32(cat(Sl[2 * q2], Sl[2 * q2 + 1]), qa, qs);
+          qs = mma32(cat(Sh[2 * q2], Sh[2 * q2 + 1]), qa, qs);
+        }
+        X[I] = qs;
+      }
+      lds_barrier();  // B2: split V' handed over
+
+      // ---- O^T = (QS)^T rq e^G + V'^T P^T: lane holds value columns 4 g4 .. 4 g4 + 3 of token 16 I + m16, so
+      // each lane writes one 8-byte piece per token tile ----
+      s16x4 Vh[4], Vl[4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+        Vh[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I) * XP);
+        Vl[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I + 1) * XP);
       }
 #pragma unroll
-      for (int it = 0; it < 2; ++it) *reinterpret_cast<u32x4*>(&Vs[st_t * VS + 8 * (g4 + 4 * it)]) = pv[it];
-      // the workspace planes already have the LDS layout: a linear copy
-#pragma unroll
-      for (int i = 0; i < PM; ++i) {
-        const int x = threadIdx.x + 256 * i;
-        if (x < PLANE_PIECES) reinterpret_cast<u32x4*>(Pn)[x] = pm[i];
+      for (int I = 0; I < 4; ++I) {
+        const int t = 16 * I + m16;
+        const float qe = vec[CH + t];
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t* ph = Ps[cb] + t * PW;
+        const uint16_t* pl = ph + PL;
+        if (I == 0) acc = split_product_sw<1, true>(ph, pl, po, Vh, Vl, acc);
+        if (I == 1) acc = split_product_sw<2, true>(ph, pl, po, Vh, Vl, acc);
+        if (I == 2) acc = split_product_sw<3, true>(ph, pl, po, Vh, Vl, acc);
+        if (I == 3) acc = split_product_sw<4, true>(ph, pl, po, Vh, Vl, acc);
+        X[I] = X[I] * qe + acc;
       }
-      vec_s[threadIdx.x] = pf;
-    }
-    // the next chunk (or this one again after the last: harmless loads whose results are never used)
-    const int cn = c0 + CH < ntok ? c0 + CH : c0;
-    const uint16_t* nrow = row_of(cn);
-    const uint8_t* nunit = unit_ptr(p, n, cn / CH, hv);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch_kq(nrow);
-    __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();
-    const uint16_t* Mh = Pn;
-    const uint16_t* Ml = Pn + CH * TS;
-    const uint16_t* Ph = Pn + 2 * CH * TS;
-    const uint16_t* Pl = Pn + 3 * CH * TS;
-
-    // ---- Y = Kr S (token rows) and QS^T = S^T Qr^T (value rows, token columns) for this wave's 16 value
-    // columns: S split hi / lo, key blocks paired; QS^T is the same products with the operands swapped ----
-    s16x4 Sh[8], Sl[8];
+      // stage before storing: waiting for the staged loads would also wait for stores issued before it
+      stage(cb ^ 1);
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) split4(S[mt], Sh[mt], Sl[mt]);
-    f32x4 Y[4], QS[4];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      f32x4 y = {0.f, 0.f, 0.f, 0.f}, qs = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = Ks + (16 * I + m16) * KS + 4 * g4;
-      const uint16_t* qrow = Qs + (16 * I + m16) * KS + 4 * g4;
-#pragma unroll
-      for (int q2 = 0; q2 < 4; ++q2) {
-        const s16x8 ka = cat(ld4h(krow + 32 * q2), ld4h(krow + 32 * q2 + 16));
-        const s16x8 qa = cat(ld4h(qrow + 32 * q2), ld4h(qrow + 32 * q2 + 16));
-        const s16x8 sh = cat(Sh[2 * q2], Sh[2 * q2 + 1]), sl = cat(Sl[2 * q2], Sl[2 * q2 + 1]);
-        y = mma32(ka, sl, y);
-        y = mma32(ka, sh, y);
-        qs = mma32(sl, qa, qs);
-        qs = mma32(sh, qa, qs);
-      }
-      Y[I] = y;
-      QS[I] = qs;
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    fetch_v(nrow, nunit);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- Z = Vr - e^G rk . Y, split (V[16 I + 4 g4 + r][column 16 w + m16] by a transpose read) ----
-    s16x4 Zh[4], Zl[4];
-    const uint16_t* vfrag = Vs + (4 * g4 + (m16 >> 2)) * VS + wave * 16 + 4 * (m16 & 3);
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int i0 = 16 * I + 4 * g4;
-      const f32x4 e1 = ld4f(&vec_s[i0]);
-      const s16x4 v4 = ld4h_tr(vfrag + 16 * I * VS);
-      f32x4 z;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = bf2f((uint16_t)v4[r]) - e1[r] * Y[I][r];
-      split4(z, Zh[I], Zl[I]);
-    }
-
-    // ---- V'_I = sum_{J<=I} M'_IJ Z_J (M' lower triangular) ----
-    s16x4 Vh[4], Vl[4];
-    f32x4 Vp[4];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int mrow = (16 * I + m16) * TS + 4 * g4;
-      if (I == 0) acc = split_product<1>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
-      if (I == 1) acc = split_product<2>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
-      if (I == 2) acc = split_product<3>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
-      if (I == 3) acc = split_product<4>(Mh + mrow, Ml + mrow, Zh, Zl, acc);
-      Vp[I] = acc;
-      split4(acc, Vh[I], Vl[I]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    fetch_planes(nunit, 0);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- O^T = (QS)^T rq e^G + V'^T P^T: lane holds value columns 4 g4 .. 4 g4 + 3 of token 16 I + m16, so
-    // each lane writes one 8-byte piece per token tile ----
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const int t = 16 * I + m16;
-      const float qe = vec_s[CH + t];
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int prow = t * TS + 4 * g4;
-      if (I == 0) acc = split_product<1, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 1) acc = split_product<2, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 2) acc = split_product<3, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      if (I == 3) acc = split_product<4, true>(Ph + prow, Pl + prow, Vh, Vl, acc);
-      const f32x4 o = QS[I] * qe + acc;
-      if (t < nv) {
-        const int64_t at = (tok0 + c0 + t) * ostride + hv * VD + vb * BV + wave * 16 + 4 * g4;
-        const uint32_t b0 = f2bf_finite(o[0]), b1 = f2bf_finite(o[1]), b2 = f2bf_finite(o[2]), b3 = f2bf_finite(o[3]);
-        *reinterpret_cast<uint2*>(p.o + at) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-        if (p.sq) {
-          const float x0 = bf2f(b0), x1 = bf2f(b1), x2 = bf2f(b2), x3 = bf2f(b3);
-          *reinterpret_cast<f32x4*>(p.sq + at) = (f32x4){x0 * x0, x1 * x1, x2 * x2, x3 * x3};
+      for (int I = 0; I < 4; ++I) {
+        const int t = 16 * I + m16;
+        if (t < nv) {
+          const f32x4 o = X[I];
+          const int64_t at = (tok0 + c0 + t) * ostride + hv * VD + vb * BV + w * 16 + 4 * g4;
+          const uint32_t w01 = pack_bf16x2(o[0], o[1]), w23 = pack_bf16x2(o[2], o[3]);
+          *reinterpret_cast<uint2*>(p.o + at) = make_uint2(w01, w23);
+          if (p.sq) {
+            const float x0 = __uint_as_float(w01 << 16), x1 = __uint_as_float(w01 & 0xffff0000u);
+            const float x2 = __uint_as_float(w23 << 16), x3 = __uint_as_float(w23 & 0xffff0000u);
+            *reinterpret_cast<f32x4*>(p.sq + at) = (f32x4){x0 * x0, x1 * x1, x2 * x2, x3 * x3};
+          }
         }
       }
-    }
-
-    __builtin_amdgcn_sched_barrier(0);
-    fetch_planes(nunit, 1);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- S <- e^(G_C) S + Kr^T W,  W = rk e^(G_C - G) . V' (token blocks paired) ----
-    s16x4 Wh[4], Wl[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      const f32x4 d = ld4f(&vec_s[2 * CH + 16 * J + 4 * g4]);
-      split4(Vp[J] * d, Wh[J], Wl[J]);
-    }
-    const float gc = vec_s[3 * CH];
-    // K^T operand: lane m16 of group g4 gets key 16 mt + m16 of tokens 16 J + 4 g4 .. +3 (transpose read)
-    const uint16_t* kfrag = Ks + (4 * g4 + (m16 >> 2)) * KS + 4 * (m16 & 3);
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int J = 0; J < 4; J += 2) {
-        const s16x8 ka = cat(ld4h_tr(kfrag + 16 * J * KS + 16 * mt), ld4h_tr(kfrag + 16 * (J + 1) * KS + 16 * mt));
-        acc = mma32(ka, cat(Wl[J], Wl[J + 1]), acc);
-        acc = mma32(ka, cat(Wh[J], Wh[J + 1]), acc);
-      }
-      S[mt] = S[mt] * gc + acc;
+      lds_barrier();  // B0: the next chunk is staged
     }
   }
-
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) store_state(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD, S[mt][r]);
 }
 
 // Gated RMSNorm of the chunk outputs (gated_finish, src/hs_guard/engine/fused_kernels.py:215-233, as the slot
@@ -741,12 +901,14 @@ int chunk_launch(ChunkParams& p, int32_t state_dtype, int32_t n_rows, int32_t L,
   if ((int64_t)n_rows * HV > (int64_t)1 << 26 || units > (int64_t)0x7fffffff) return HSG_ERR_SHAPE;
   if (workspace_bytes < hsg_gdn_chunk_workspace_bytes(n_rows, L, HV)) return HSG_ERR_SHAPE;
   p.pairs = n_rows * HV;
+  p.order = reinterpret_cast<int32_t*>(p.ws + units * hsg::UNIT_BYTES);
   hipLaunchKernelGGL(hsg::gdn_chunk_prep_kernel, dim3((unsigned)units), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(hsg::gdn_chunk_order_kernel, dim3(1), dim3(1024), 0, s, p, (int)n_rows);
   const dim3 grid((unsigned)(((p.pairs + 7) / 8) * 16));
   if (state_dtype == HSG_STATE_F32)
-    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<float>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<float>), grid, dim3(512), 0, s, p);
   else
-    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<uint16_t>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((hsg::gdn_chunk_state_kernel<uint16_t>), grid, dim3(512), 0, s, p);
   return HSG_OK;
 }
 
@@ -786,7 +948,9 @@ ChunkParams chunk_params(const void* qkv, int64_t qkv_stride, int32_t q_off, int
 
 extern "C" size_t hsg_gdn_chunk_workspace_bytes(int32_t n_rows, int32_t L, int32_t HV) {
   if (n_rows <= 0 || L <= 0 || HV <= 0) return 0;
-  return (size_t)n_rows * (size_t)((L + hsg::CH - 1) / hsg::CH) * (size_t)HV * (size_t)hsg::UNIT_BYTES;
+  // the units, then the state kernel's row order (int32 per row, rounded up to 256 bytes)
+  return (size_t)n_rows * (size_t)((L + hsg::CH - 1) / hsg::CH) * (size_t)HV * (size_t)hsg::UNIT_BYTES +
+         ((size_t)n_rows * 4 + 255) / 256 * 256;
 }
 
 extern "C" int hsg_gdn_chunk_prefill(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,

@@ -62,11 +62,12 @@ def test_argument_errors_are_rejected_before_launch():
     assert L.hsg_ring_decode(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, 0,
                              0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0, None, 0,
                              None) == 0
-    # chunk prefill: workspace size is rows x ceil(L / 64) x HV units; a too-small or unaligned workspace and
-    # L <= 0 are rejected
-    unit = L.hsg_gdn_chunk_workspace_bytes(1, 64, 1)
-    assert unit > 0
-    assert L.hsg_gdn_chunk_workspace_bytes(3, 130, 16) == 3 * 3 * 16 * unit
+    # chunk prefill: workspace size is rows x ceil(L / 64) x HV units plus the row order (4 bytes per row in
+    # 256-byte blocks); a too-small or unaligned workspace and L <= 0 are rejected
+    unit = L.hsg_gdn_chunk_workspace_bytes(1, 64, 1) - 256
+    assert unit > 0 and unit == L.hsg_gdn_chunk_workspace_bytes(1, 128, 1) - unit - 256
+    assert L.hsg_gdn_chunk_workspace_bytes(3, 130, 16) == 3 * 3 * 16 * unit + 256
+    assert L.hsg_gdn_chunk_workspace_bytes(70, 64, 1) == 70 * unit + 512
     assert L.hsg_gdn_chunk_workspace_bytes(0, 64, 16) == 0
     need = L.hsg_gdn_chunk_workspace_bytes(4, 100, 16)
     args = [256, 6144, 0, 2048, 4096, 256, 256, 16, 256, 256, 256, 0, 17, 256, 256, None, 4, 100, 16, 16, 128, 128,
