@@ -23,13 +23,15 @@
 // scaled into -A (LDS) and P (workspace); the four diagonal 16 x 16 blocks of I + A are inverted by fp32
 // forward substitution; wave w then solves (I + A) M[:, 16w..16w+16) = I[:, 16w..] block by block, so the
 // inverse is explicit, and scales its columns by beta.
-// State mapping: one workgroup (4 waves) per (row, value head, 64-column value block); wave w owns value
-// columns [16w, 16w+16) of the block and keeps S[:, those columns] (128 x 16 fp32) in MFMA accumulator layout
-// for the whole sequence, so the state is read once and written once per call. The accumulator layout of a
-// 16-row block (lane l: column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of
-// v_mfma_f32_16x16x16_bf16, so S, Z and V' feed the next product from registers; pairs of 16-row blocks feed
-// v_mfma_f32_16x16x32_bf16 by ordering its 32 reduction slots as (4 rows of block J, 4 rows of block J+1) per
-// lane, with the A operand read in the same order.
+// State mapping: one workgroup (8 waves) per (row, value head, 64-column value block), rows with the most
+// chunks dispatched first (gdn_chunk_order_kernel). Chain wave w (0-3) owns value columns [16w, 16w+16) of the
+// block and keeps S[:, those columns] (128 x 16 fp32) in MFMA accumulator layout for the whole sequence, so the
+// state is read once and written once per call; output wave 4 + w computes Q S and O for the same columns from
+// the split S and V' the chain wave hands over through LDS. The accumulator layout of a 16-row block (lane l:
+// column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of v_mfma_f32_16x16x16_bf16, so S, Z and V'
+// feed the next product from registers; pairs of 16-row blocks feed v_mfma_f32_16x16x32_bf16 by ordering its
+// 32 reduction slots as (4 rows of block J, 4 rows of block J+1) per lane, with the A operand read in the same
+// order.
 // Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, -A, M', P, the
 // diagonal inverses, Z, V') is split into bf16 hi + lo and multiplied in three passes (hi.hi + hi.lo + lo.hi,
 // error ~2^-16 relative), or two when the other operand is exact bf16, so the state keeps fp32-level accuracy.

@@ -87,8 +87,8 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * every row's length (rows with lens[n] > L are treated as empty). o must not alias qkv; o 8-byte and sq
  * 16-byte aligned.
  * Rows with lens[n] < min_len are left alone (min_len <= 1: every row).
- * Two launches on `stream`: the state-independent part of every (row, chunk, value head) in parallel, then
- * the sequential state products per row. workspace: device memory of at least
+ * Three launches on `stream`: the state-independent part of every (row, chunk, value head) in parallel, the
+ * rows' order (most chunks first), then the sequential state products per row in that order. workspace: device memory of at least
  * hsg_gdn_chunk_workspace_bytes(n_rows, L, HV) bytes, 256-byte aligned; no initialisation needed, garbage
  * afterwards.
  */
