@@ -84,6 +84,25 @@ def pack_ticks(chunks, slots, length, nb, tb, max_slots, out):
     return lens, offsets
 
 
+def gdn_proj_width(cfg):
+    """Columns of a GDN layer's fused projection qkv|z|b|a, padded with zero weight rows to a multiple of 256:
+    hipBLASLt serves N = 8,224 (the baseline geometry) with a stream-K kernel at 38-40 us for M ~ 1,500 tokens
+    and N = 8,448 with a regular one at 27-31 us. The padding columns are computed and never read."""
+    n = cfg.conv_dim + cfg.value_dim + 2 * cfg.linear_num_value_heads
+    return -(-n // 256) * 256
+
+
+def request_order(flat, lens, offsets):
+    """Tick outputs [R, T, 3] (row r at positions offsets[r] .. offsets[r] + lens[r] - 1) gathered so that the
+    rows follow one another in request order: row r then starts at sum(lens[:r])."""
+    starts = np.zeros(len(lens), dtype=np.int64)
+    if len(lens) > 1:
+        np.cumsum(lens[:-1], out=starts[1:])
+    gather = np.repeat(np.asarray(offsets, dtype=np.int64) - starts, lens) + np.arange(int(np.sum(lens)),
+                                                                                         dtype=np.int64)
+    return np.ascontiguousarray(flat[:, gather])
+
+
 class PreparedWeights:
     """The backbone's weights in the kernels' layouts: fused projections (GDN qkv|z|b|a, attention q|k|v, MLP
     gate|up, both heads' first Linear), RMSNorm gains as fp32 1 + w, rotary inverse frequencies. Needs
@@ -101,8 +120,10 @@ class PreparedWeights:
                  "w_down": m[p + "mlp.down_proj.weight"].contiguous()}
             if kind == "linear_attention":
                 a = p + "linear_attn."
-                L["w_in"] = torch.cat([m[a + "in_proj_qkv.weight"], m[a + "in_proj_z.weight"],
-                                       m[a + "in_proj_b.weight"], m[a + "in_proj_a.weight"]]).contiguous()
+                w_in = torch.cat([m[a + "in_proj_qkv.weight"], m[a + "in_proj_z.weight"],
+                                  m[a + "in_proj_b.weight"], m[a + "in_proj_a.weight"]])
+                pad = gdn_proj_width(cfg) - w_in.shape[0]
+                L["w_in"] = torch.cat([w_in, w_in.new_zeros(pad, w_in.shape[1])]).contiguous()
                 L["conv_w"] = m[a + "conv1d.weight"].reshape(cfg.conv_dim, -1).contiguous()
                 L["A_log"] = m[a + "A_log"].contiguous()
                 L["dt_bias"] = m[a + "dt_bias"].contiguous()
@@ -190,7 +211,7 @@ class SlotStreamEngine(PreparedWeights):
         cfg, T, dev = self.cfg, self.max_tokens, self.device
         bf16 = torch.bfloat16
         hq, hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-        self.gdn_in = cfg.conv_dim + cfg.value_dim + 2 * cfg.linear_num_value_heads
+        self.gdn_in = gdn_proj_width(cfg)       # row stride of the GDN projection (padded, see gdn_proj_width)
         self.att_in = hq * 2 * D + 2 * hkv * D
         widest = max(self.gdn_in, self.att_in, 2 * cfg.intermediate_size)
         self.buf = {
@@ -422,13 +443,14 @@ class SlotStreamEngine(PreparedWeights):
         """One tick: <= max_rows rows of <= max_tick_tokens tokens. Returns (probs [R, T, 3] numpy, lens,
         offsets) with row r's probabilities at [:, offsets[r] : offsets[r] + lens[r]]."""
         n = len(chunks)
-        total = sum(len(c) for c in chunks)
+        row_lens = np.fromiter(map(len, chunks), dtype=np.int64, count=n)
+        total = int(row_lens.sum())
         nb = bucket(n, self.session_buckets)
         tb = bucket(total, self.token_buckets)
         graph, inp, probs, host_in, host_np, host_out, out_np = self._static(nb, tb)
         # rows go to the device longest first: the per-row kernels then start their longest rows first
         # instead of finishing on them (every kernel treats rows independently, so results do not change)
-        order = sorted(range(n), key=lambda r: -len(chunks[r]))
+        order = np.argsort(-row_lens, kind="stable")
         lens_p, offsets_p = pack_ticks([chunks[r] for r in order], np.asarray(slots)[order], self.length, nb, tb,
                                        self.max_slots, host_np)
         lens = np.empty(n, dtype=np.int64)
@@ -479,6 +501,13 @@ class SlotStreamEngine(PreparedWeights):
         (src/hs_guard/engine/slot_engine_v7.py:147-167)."""
         self._validate(requests)
         largest, rows = self.max_tick_tokens, self.max_rows
+        if len(requests) <= rows and all(len(ids) <= largest for _, ids in requests):
+            # one tick (the serving case): split the request-ordered outputs directly
+            slots = np.fromiter((s for s, _ in requests), dtype=np.int64, count=len(requests))
+            flat, lens, offsets = self._run_arrays([ids for _, ids in requests], slots)
+            probs = torch.from_numpy(request_order(flat, lens, offsets))
+            sizes = lens.tolist()
+            return {role: list(torch.split(probs[r], sizes)) for r, role in enumerate(self.roles)}
         results = {role: [[] for _ in requests] for role in self.roles}
         pending = [(i, s, list(ids)) for i, (s, ids) in enumerate(requests)]
         while pending:
@@ -487,10 +516,13 @@ class SlotStreamEngine(PreparedWeights):
                 part = batch[start:start + rows]
                 slots = np.fromiter((s for _, s, _ in part), dtype=np.int64, count=len(part))
                 flat, lens, offsets = self._run_arrays([c for _, _, c in part], slots)
-                probs = torch.from_numpy(flat)
+                # one gather into request order, then one split per role (per-row slicing in Python cost ~700
+                # tensor constructions per 352-row tick)
+                probs = torch.from_numpy(request_order(flat, lens, offsets))
+                sizes = lens.tolist()
                 for role_index, role in enumerate(self.roles):
-                    for row, (i, _, _) in enumerate(part):
-                        results[role][i].append(probs[role_index, offsets[row]:offsets[row] + lens[row]])
+                    for (i, _, _), piece in zip(part, torch.split(probs[role_index], sizes)):
+                        results[role][i].append(piece)
             pending = [(i, s, ids[largest:]) for i, s, ids in pending if len(ids) > largest]
         return {role: [chunks[0] if len(chunks) == 1 else torch.cat(chunks) for chunks in rows_]
                 for role, rows_ in results.items()}

@@ -27,7 +27,7 @@ import math
 import torch
 
 from .._lib import check, lib
-from .slot_engine import ROLES, PreparedWeights
+from .slot_engine import ROLES, PreparedWeights, gdn_proj_width
 
 SEG = 64                  # tokens per conv / attention segment (the tiled ring kernel's row limit)
 MAX_ATT_SEGMENTS = 128    # segments per attention launch: bounds the gathered rings to ~270 MB at W = 512
@@ -69,7 +69,7 @@ class WholeSequenceScorer(PreparedWeights):
         nh, hv, kd, vd = cfg.linear_num_key_heads, cfg.linear_num_value_heads, cfg.linear_key_head_dim, \
             cfg.linear_value_head_dim
         C = cfg.conv_dim
-        gdn_in = C + cfg.value_dim + 2 * hv
+        gdn_in = gdn_proj_width(cfg)       # row stride of the GDN projection (zero-padded weight rows)
         att_in = hq * 2 * D + 2 * hkv * D
         i64 = dict(dtype=torch.long, device=dev)
 

@@ -57,8 +57,10 @@ def setup():
 def _matched_gemm(eng):
     """The engine's product (torch.mm / addmm into a [tb, N] bf16 buffer, tb the engine's token bucket) applied
     to the oracle's padded [n, lb, K] activations: rows packed in request order, padded positions skipped."""
-    from hs_guard.engine.slot_engine import bucket
+    from hs_guard.engine.slot_engine import bucket, gdn_proj_width
     cache = {}
+    cfg = eng.cfg
+    gdn_n = cfg.conv_dim + cfg.value_dim + 2 * cfg.linear_num_value_heads
 
     def gemm(x, w, bias, lens):
         n, lb, K = x.shape
@@ -69,7 +71,10 @@ def _matched_gemm(eng):
         xp[:total] = np.concatenate([x[r, :lens[r]] for r in range(n)])
         key = (w.shape, float(w.ravel()[0]), float(w.ravel()[-1]), float(w.sum()))
         if key not in cache:
-            cache[key] = torch.from_numpy(np.ascontiguousarray(w)).to(torch.bfloat16).cuda().contiguous()
+            wp = w
+            if w.shape == (gdn_n, cfg.hidden_size):   # the engine's GDN projection carries zero padding rows
+                wp = np.concatenate([w, np.zeros((gdn_proj_width(cfg) - gdn_n, w.shape[1]), w.dtype)])
+            cache[key] = torch.from_numpy(np.ascontiguousarray(wp)).to(torch.bfloat16).cuda().contiguous()
         W = cache[key]
         xd = torch.from_numpy(xp).to(torch.bfloat16).cuda()
         out = torch.empty(tb, W.shape[0], dtype=torch.bfloat16, device="cuda")
@@ -77,8 +82,8 @@ def _matched_gemm(eng):
             torch.mm(xd, W.t(), out=out)
         else:
             torch.addmm(torch.from_numpy(bias).to(torch.bfloat16).cuda(), xd, W.t(), out=out)
-        y = out.float().cpu().numpy()
-        res = np.zeros((n, lb, W.shape[0]), dtype=np.float32)
+        y = out.float().cpu().numpy()[:, :w.shape[0]]
+        res = np.zeros((n, lb, w.shape[0]), dtype=np.float32)
         at = 0
         for r in range(n):
             res[r, :lens[r]] = y[at:at + lens[r]]

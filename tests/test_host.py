@@ -149,3 +149,21 @@ def test_serialize_and_encode_messages():
             serialize(bad)
     with pytest.raises(ValueError, match="no tokenizer"):
         encode_messages(None, msgs)
+
+
+def test_request_order_gathers_rows():
+    """The engine's tick outputs are packed longest row first; request_order puts them back in request order
+    (row r at sum(lens[:r])) exactly as slicing each row out of the packed outputs would."""
+    from hs_guard.engine.slot_engine import request_order
+    rng = np.random.default_rng(5)
+    lens = rng.integers(1, 40, 37)
+    order = np.argsort(-lens, kind="stable")
+    packed_off = np.concatenate([[0], np.cumsum(lens[order])[:-1]])
+    offsets = np.empty(len(lens), dtype=np.int64)
+    offsets[order] = packed_off
+    flat = rng.random((2, int(lens.sum()) + 5, 3)).astype(np.float32)   # 5 padding positions at the end
+    got = request_order(flat, lens, offsets)
+    want = np.concatenate([flat[:, o:o + n] for o, n in zip(offsets, lens)], axis=1)
+    assert got.shape == want.shape and np.array_equal(got, want)
+    one = request_order(flat, lens[:1], offsets[:1])
+    assert np.array_equal(one, flat[:, offsets[0]:offsets[0] + lens[0]])
