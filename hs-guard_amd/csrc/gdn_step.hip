@@ -11,13 +11,18 @@
 // per tick whatever the token count. Each state load is a 16-byte vector; the 8 lanes of one rg cover a
 // 128-byte row segment, so every load instruction reads 8 full 128-byte lines. The k.S and q.S
 // reductions over the 128 key rows are in-lane (16 rows) plus a 3-step butterfly over rg (lane xor 8,
-// 16, 32). exp(g) is folded in as (exp(g) S)^T k = exp(g) (S^T k), and the decay and rank-1 update share
-// one pass over the registers. The state is read with ordinary loads and written back with nontemporal
-// stores (it is touched once per tick, so the write should not displace cached weights and activations);
-// measured on MI355X this pairing streams faster than nontemporal loads (6.0 vs 5.4 TB/s at 352 x 16).
-// Token inputs (q, k of the key head; v, z of the value head; a, b) are staged in LDS 16 tokens at a time
-// by one cooperative burst of 16-byte loads, so a 64-token tick pays the global-memory latency 4 times
-// instead of 64 and the sequential token loop only touches LDS.
+// 16, 32) done with a DPP row rotate and gfx950's permlane16/32 swaps, not the LDS crossbar. The state is
+// read with ordinary loads and written back with nontemporal stores (it is touched once per tick, so the
+// write should not displace cached weights and activations); measured on MI355X this pairing streams
+// faster than nontemporal loads (6.0 vs 5.4 TB/s at 352 x 16).
+// Per-token work is cut to the three 16 x 4 products a token needs (S^T k, the rank-1 update, S^T q):
+//   * the registers hold St with S = D St, so exp(g) scales the scalar D, not 64 registers (D is folded
+//     back before 1 / D could overflow and when the state is stored);
+//   * token inputs (q, k of the key head; v, z of the value head; a, b) arrive in bursts of CT tokens by
+//     one cooperative round of 16-byte loads, prefetched into registers one burst ahead; when a burst
+//     moves into LDS its q and k are L2-normalised once per token (not once per lane) and exp(g) and
+//     beta are computed once per token;
+//   * the gated RMSNorm epilogue runs once per burst on all 256 threads, so the token loop has no barrier.
 #include "hsg_common.h"
 
 namespace hsg {
@@ -88,21 +93,8 @@ struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
   }
 };
 
-// Sum over the 8 lanes sharing (lane & 7): lane xor 8, 16, 32.
-__device__ __forceinline__ float sum_rg(float x) {
-  x = xor_add<8>(x);
-  x = xor_add<16>(x);
-  x = xor_add<32>(x);
-  return x;
-}
-
-// Sum over the 8 lanes sharing (lane >> 3): lane xor 1, 2, 4.
-__device__ __forceinline__ float sum_c(float x) {
-  x = xor_add<1>(x);
-  x = xor_add<2>(x);
-  x = xor_add<4>(x);
-  return x;
-}
+// Sum over the 8 lanes sharing (lane & 7): lane xor 8, 16, 32 (DPP row rotate, then the two permlane swaps).
+__device__ __forceinline__ float sum_rg(float x) { return sum_stride8_dpp(x); }
 
 template <typename ST, bool GATED>
 __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
@@ -122,7 +114,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
   const int col = wave * TILE_V + c * 4;
 
+  // The registers hold St with S = D * St: the per-token decay multiplies the scalar D instead of all 64
+  // registers; D is folded back into St before 1 / D could overflow and when the state is stored.
   float S[ROWS][4];
+  float D = 1.0f;
   ST* sp = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * KD + rg * ROWS) * (int64_t)VD + col;
   if (ntok > 0) {
 #pragma unroll
@@ -130,12 +125,14 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   }
   const float A = expf(bf2f(p.A_log[hv]));
   const float dt = bf2f(p.dt_bias[hv]);
-  __shared__ float red[2][4];
-  __shared__ __align__(16) uint16_t sq_[CT][KD];
-  __shared__ __align__(16) uint16_t sk_[CT][KD];
+  // per burst: normalised q (times scale) and k in fp32, one 16-row piece per lane group (stride 20 floats, so
+  // the 8 pieces a wave reads at once fall on distinct banks); raw v and z; exp(g) and beta per token
+  __shared__ __align__(16) float fq_[CT][KD / ROWS][ROWS + 4];
+  __shared__ __align__(16) float fk_[CT][KD / ROWS][ROWS + 4];
   __shared__ __align__(16) uint16_t sv_[CT][VD];
   __shared__ __align__(16) uint16_t sz_[GATED ? CT : 1][VD];
-  __shared__ float sa_[CT], sb_[CT];
+  __shared__ __align__(16) float so_[GATED ? CT : 1][VD];   // bf16-rounded o of the burst, for the gated norm
+  __shared__ float sdec_[CT], sbe_[CT];
   constexpr int SEGS = GATED ? 64 : 48;   // 16-byte segments per token: q, k, v (, z)
   constexpr int PF = (CT * SEGS + 255) / 256;   // segments per thread per burst (the last partly idle)
   // gated-norm weights staged in LDS once (read per token from global memory they were reloaded after every
@@ -145,7 +142,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
     *reinterpret_cast<u32x4*>(&sw_[8 * threadIdx.x]) = *reinterpret_cast<const u32x4*>(p.norm_w + 8 * threadIdx.x);
 
   // The tokens of a row go through LDS in bursts of CT; the next burst is loaded into registers while the
-  // current one is processed. Segment e = threadIdx.x + 256 i of a burst is token e / SEGS, piece e % SEGS;
+  // current one is processed. Segment e = threadIdx.x + 256 i of a burst is token e / SEGS, piece e % SEGS
+  // (pieces 16j .. 16j+15 are q, k, v, z for j = 0..3: an aligned group of 16 lanes holds one whole vector);
   // positions past the row's end re-read its last token (never stored to LDS).
   u32x4 pf[PF];
   uint16_t pa = 0, pb = 0;
@@ -170,117 +168,160 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
     pa = p.a[tok * p.ab_stride + hv];
     pb = p.b[tok * p.ab_stride + hv];
   };
-  if (ntok > 0) fetch(0);
-
-  for (int t = 0; t < ntok; ++t) {
-    const int tt = t % CT;
-    if (tt == 0) {  // move the prefetched burst into LDS, then start loading the next one
-      const int nt = min(CT, ntok - t);
-      __syncthreads();
+  // prefetched burst -> LDS: q <- q / sqrt(|q|^2 + 1e-6) * scale and k <- k / sqrt(|k|^2 + 1e-6) once per token
+  // (|x|^2 summed over the 16 lanes holding the vector), v and z as loaded, exp(g) and beta by thread u
+  auto stage = [&](int nt) {
 #pragma unroll
-      for (int i = 0; i < PF; ++i) {
-        const int e = threadIdx.x + 256 * i;
-        const int u = e / SEGS;
-        const int sg = e % SEGS;
-        const int which = sg >> 4;
-        const int c = (sg & 15) * 8;
-        uint16_t* dst = which == 0 ? &sq_[u][c] : which == 1 ? &sk_[u][c] : which == 2 ? &sv_[u][c]
-                                                                                     : &sz_[GATED ? u : 0][c];
-        if (u < nt) *reinterpret_cast<u32x4*>(dst) = pf[i];
-      }
-      if (threadIdx.x < nt) {
-        sa_[threadIdx.x] = bf2f(pa);
-        sb_[threadIdx.x] = bf2f(pb);
-      }
-      if (t + CT < ntok) fetch(t + CT);
-      __syncthreads();
-    }
-    const int64_t tok = tok0 + t;
-    float q[ROWS], k[ROWS], v[4];
-    load8_bf16(&sq_[tt][rg * ROWS], q);
-    load8_bf16(&sq_[tt][rg * ROWS + 8], q + 8);
-    load8_bf16(&sk_[tt][rg * ROWS], k);
-    load8_bf16(&sk_[tt][rg * ROWS + 8], k + 8);
-    load4_bf16(&sv_[tt][col], v);
-    float qq = 0.f, kk = 0.f;
+    for (int i = 0; i < PF; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      const int u = e / SEGS;
+      const int sg = e % SEGS;
+      const int which = sg >> 4;
+      const int c = (sg & 15) * 8;
+      float x[8];
+      unpack2(pf[i][0], x[0], x[1]);
+      unpack2(pf[i][1], x[2], x[3]);
+      unpack2(pf[i][2], x[4], x[5]);
+      unpack2(pf[i][3], x[6], x[7]);
+      float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < ROWS; ++j) {
-      qq += q[j] * q[j];
-      kk += k[j] * k[j];
-    }
-    qq = sum_rg(qq);
-    kk = sum_rg(kk);
-    const float rq = 1.0f / sqrtf(qq + 1e-6f);
-    const float rk = 1.0f / sqrtf(kk + 1e-6f);
+      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+      ss = sum16_dpp(ss);
+      if (u < nt) {
+        if (which < 2) {
+          const float r = 1.0f / sqrtf(ss + 1e-6f);
+          f32x4_t y0, y1;
+          if (which == 0) {
 #pragma unroll
-    for (int j = 0; j < ROWS; ++j) {
-      q[j] = q[j] * rq * p.scale;
-      k[j] = k[j] * rk;
-    }
-    const float x = sa_[tt] + dt;
-    const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
-    const float beta = sigmoidf_(sb_[tt]);
-    const float decay = expf(g);
-
-    float kv[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 4; ++j) {
+              y0[j] = x[j] * r * p.scale;
+              y1[j] = x[4 + j] * r * p.scale;
+            }
+          } else {
 #pragma unroll
-    for (int j = 0; j < ROWS; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kv[i] += S[j][i] * k[j];
-    }
-    float vn[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vn[i] = beta * (v[i] - decay * sum_rg(kv[i]));
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < ROWS; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        S[j][i] = S[j][i] * decay + k[j] * vn[i];
-        o[i] += S[j][i] * q[j];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = sum_rg(o[i]);
-
-    if constexpr (!GATED) {
-      if (rg == 0) {
-        const int64_t base = (tok * p.HV + hv) * VD + col;
-        store4_bf16(p.o + base, o);
-        if (p.sq != nullptr) {
-          float s4[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float ob = rbf(o[i]);
-            s4[i] = ob * ob;
+            for (int j = 0; j < 4; ++j) {
+              y0[j] = x[j] * r;
+              y1[j] = x[4 + j] * r;
+            }
           }
-          *reinterpret_cast<float4*>(p.sq + base) = make_float4(s4[0], s4[1], s4[2], s4[3]);
+          float* dst = which == 0 ? &fq_[u][c / ROWS][c % ROWS] : &fk_[u][c / ROWS][c % ROWS];
+          *reinterpret_cast<f32x4_t*>(dst) = y0;
+          *reinterpret_cast<f32x4_t*>(dst + 4) = y1;
+        } else if (which == 2) {
+          *reinterpret_cast<u32x4*>(&sv_[u][c]) = pf[i];
+        } else if (GATED) {
+          *reinterpret_cast<u32x4*>(&sz_[GATED ? u : 0][c]) = pf[i];
         }
       }
-    } else {
-      float ob[4];
+    }
+    if (threadIdx.x < nt) {
+      const float x = bf2f(pa) + dt;
+      const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
+      sdec_[threadIdx.x] = expf(g);
+      sbe_[threadIdx.x] = sigmoidf_(bf2f(pb));
+    }
+  };
+  if (ntok > 0) fetch(0);
+
+  for (int t0 = 0; t0 < ntok; t0 += CT) {
+    const int nt = min(CT, ntok - t0);
+    __syncthreads();   // every read of the previous burst's LDS is done
+    stage(nt);
+    if (t0 + CT < ntok) fetch(t0 + CT);
+    __syncthreads();
+
+    for (int tt = 0; tt < nt; ++tt) {
+      float q[ROWS], k[ROWS], v[4];
+#pragma unroll
+      for (int j = 0; j < ROWS; j += 4) {
+        const f32x4_t a4 = *reinterpret_cast<const f32x4_t*>(&fq_[tt][rg][j]);
+        const f32x4_t b4 = *reinterpret_cast<const f32x4_t*>(&fk_[tt][rg][j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          q[j + i] = a4[i];
+          k[j + i] = b4[i];
+        }
+      }
+      load4_bf16(&sv_[tt][col], v);
+      const float beta = sbe_[tt];
+      float Dn = D * sdec_[tt];
+      if (Dn < 0x1p-40f) {   // uniform over the workgroup (every lane has the same D and decay)
+#pragma unroll
+        for (int j = 0; j < ROWS; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[j][i] *= Dn;
+        Dn = 1.0f;
+      }
+      // S1 = exp(g) S_prev = Dn St;  v' = beta (v - S1^T k);  S2 = S1 + k v'^T = Dn (St + k (v' / Dn)^T);
+      // o = S2^T q = Dn (St'^T q)
+      float kv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < ROWS; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kv[i] += S[j][i] * k[j];
+      }
+      const float rD = __builtin_amdgcn_rcpf(Dn);   // v_rcp_f32 (1 ulp): S2 is Dn * rD * (k v'^T), within 1e-7
+      float w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = beta * (v[i] - Dn * sum_rg(kv[i])) * rD;
+      float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < ROWS; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          S[j][i] += k[j] * w[i];
+          o[i] += S[j][i] * q[j];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = sum_rg(o[i]) * Dn;
+      D = Dn;
+
+      const int64_t tok = tok0 + t0 + tt;
+      if constexpr (!GATED) {
+        if (rg == 0) {
+          const int64_t base = (tok * p.HV + hv) * VD + col;
+          store4_bf16(p.o + base, o);
+          if (p.sq != nullptr) {
+            float s4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float ob = rbf(o[i]);
+              s4[i] = ob * ob;
+            }
+            *reinterpret_cast<float4*>(p.sq + base) = make_float4(s4[0], s4[1], s4[2], s4[3]);
+          }
+        }
+      } else {
+        if (rg == 0) {
+          const f32x4_t ob = {rbf(o[0]), rbf(o[1]), rbf(o[2]), rbf(o[3])};
+          *reinterpret_cast<f32x4_t*>(&so_[GATED ? tt : 0][col]) = ob;
+        }
+      }
+    }
+
+    if constexpr (GATED) {
+      // gated RMSNorm of the burst: 32 threads per token, 4 value columns each
+      __syncthreads();
+      const int u = threadIdx.x >> 5;
+      const int cc = (threadIdx.x & 31) * 4;
+      const f32x4_t ob = *reinterpret_cast<const f32x4_t*>(&so_[GATED ? u : 0][cc]);
       float part = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ob[i] = rbf(o[i]);
-        part += ob[i] * ob[i];
-      }
-      part = sum_c(part);
-      if (lane == 0) red[t & 1][wave] = part;
-      __syncthreads();
-      const float var = (red[t & 1][0] + red[t & 1][1] + red[t & 1][2] + red[t & 1][3]) * (1.0f / VD);
-      const float r = rsqrtf(var + p.eps);
-      if (rg == 0) {
+      for (int i = 0; i < 4; ++i) part += ob[i] * ob[i];
+      part = sum32_dpp(part);
+      const float r = rsqrtf(part * (1.0f / VD) + p.eps);
+      if (u < nt) {
         float y[4], z4[4], w4[4];
-        load4_bf16(&sz_[GATED ? tt : 0][col], z4);
-        load4_bf16(&sw_[GATED ? col : 0], w4);
+        load4_bf16(&sz_[GATED ? u : 0][cc], z4);
+        load4_bf16(&sw_[GATED ? cc : 0], w4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float hb = rbf(ob[i] * r);
           const float tw = rbf(w4[i] * hb);
           y[i] = tw * siluf_(z4[i]);
         }
-        store4_bf16(p.out + tok * (int64_t)(p.HV * VD) + hv * VD + col, y);
+        store4_bf16(p.out + (tok0 + t0 + u) * (int64_t)(p.HV * VD) + hv * VD + cc, y);
       }
     }
   }
@@ -301,7 +342,11 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
 
   if (ntok > 0) {
 #pragma unroll
-    for (int j = 0; j < ROWS; ++j) StateIO<ST>::store(sp + j * VD, S[j]);
+    for (int j = 0; j < ROWS; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[j][i] *= D;
+      StateIO<ST>::store(sp + j * VD, S[j]);
+    }
   }
 }
 

@@ -145,10 +145,12 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* x, i
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Per-head RMSNorm(1+w) + partial rotate-half RoPE for q and k in one launch, one wave per (token, head).
+// Per-head RMSNorm(1+w) + partial rotate-half RoPE for q and k in one launch, one workgroup per token.
 // square_rows + norm_rope (src/hs_guard/engine/fused_kernels.py:237-284) with the rotary cos/sin of the
 // Qwen3.5 rotary embedding computed in-kernel: freq = pos * inv_freq[i] (fp32), cos/sin rounded to bf16.
 // y = bf16(x * rsqrt(mean(x^2)+eps) * w1); for d < rot: out = bf16(bf16(y*cos) + bf16(rot_half(y)*sin)).
+// The token's rot/2 cos/sin pairs are computed once into LDS (every head of the token shares them); wave w
+// then normalises heads w, w+4, ... of q followed by k, 4 dims per lane.
 // ---------------------------------------------------------------------------------------------------
 struct RopeTensor {
   const uint16_t* src; int64_t src_row, src_head; int heads;
@@ -160,61 +162,82 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
                                                         const float* inv_freq, int rot, float eps_a, float eps_b,
                                                         int tokens, int D) {
   const int lane = threadIdx.x & 63;
-  const int heads_total = a.heads + b.heads;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= tokens * heads_total) return;
-  const int tok = item / heads_total;
-  int head = item - tok * heads_total;
-  const bool is_a = head < a.heads;
-  const RopeTensor& t = is_a ? a : b;
-  if (!is_a) head -= a.heads;
-  const float eps = is_a ? eps_a : eps_b;
-  const int per_lane = D / 64;  // 4 for D = 256
-  const int d0 = lane * per_lane;
-  float x[4];
-  load4_bf16(t.src + tok * t.src_row + head * t.src_head + d0, x);
-  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)D + eps);
-  float y[4];
-  for (int i = 0; i < 4; ++i) y[i] = rbf((x[i] * r) * t.w1[d0 + i]);
+  const int wave = threadIdx.x >> 6;
+  const int tok = blockIdx.x;
   const int half = rot / 2;
-  // the partner of dim d (d +- half) sits in lane ^ (half / 4) at the same slot
-  float yp[4];
-  const int pmask = half / 4;
-  for (int i = 0; i < 4; ++i) yp[i] = __shfl_xor(y[i], pmask, 64);
-  float o[4];
-  const float p = (float)pos[tok];
-  for (int i = 0; i < 4; ++i) {
-    const int d = d0 + i;
-    if (d < rot) {
-      const float f = p * inv_freq[d < half ? d : d - half];
-      const float cs = rbf(cosf(f));
-      const float sn = rbf(sinf(f));
-      const float rh = d < half ? -yp[i] : yp[i];
-      o[i] = __fadd_rn(rbf(y[i] * cs), rbf(rh * sn));
-    } else {
-      o[i] = y[i];
-    }
+  __shared__ float cs_[128], sn_[128];   // rot <= D = 256
+  if (threadIdx.x < half) {
+    const float f = (float)pos[tok] * inv_freq[threadIdx.x];
+    cs_[threadIdx.x] = rbf(cosf(f));
+    sn_[threadIdx.x] = rbf(sinf(f));
   }
-  store4_bf16(t.out + tok * t.out_row + head * t.out_head + d0, o);
+  __syncthreads();
+  const int heads_total = a.heads + b.heads;
+  const int d0 = lane * 4;   // D / 64 = 4 dims per lane
+  // the partner of dim d (d +- half) sits in lane ^ (half / 4) at the same slot
+  const int pmask = half / 4;
+  for (int head = wave; head < heads_total; head += 4) {
+    const bool is_a = head < a.heads;
+    const uint16_t* src = is_a ? a.src : b.src;
+    const int64_t src_row = is_a ? a.src_row : b.src_row, src_head = is_a ? a.src_head : b.src_head;
+    const float* w1 = is_a ? a.w1 : b.w1;
+    uint16_t* dst = is_a ? a.out : b.out;
+    const int64_t out_row = is_a ? a.out_row : b.out_row, out_head = is_a ? a.out_head : b.out_head;
+    const int hh = is_a ? head : head - a.heads;
+    const float eps = is_a ? eps_a : eps_b;
+    float x[4];
+    load4_bf16(src + tok * src_row + hh * src_head + d0, x);
+    const float4 w4 = *reinterpret_cast<const float4*>(w1 + d0);
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = rsqrtf(ss / (float)D + eps);
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = rbf((x[i] * r) * wv[i]);
+    float yp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yp[i] = __shfl_xor(y[i], pmask, 64);
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = d0 + i;
+      if (d < rot) {
+        const int fi = d < half ? d : d - half;
+        const float rh = d < half ? -yp[i] : yp[i];
+        o[i] = __fadd_rn(rbf(y[i] * cs_[fi]), rbf(rh * sn_[fi]));
+      } else {
+        o[i] = y[i];
+      }
+    }
+    store4_bf16(dst + tok * out_row + hh * out_head + d0, o);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------
 // SiLU-mul (src/hs_guard/engine/fused_kernels.py:76-90): out = bf16(bf16(silu(gate)) * up); gate and up
 // are the two halves of the fused gate|up projection row.
 // ---------------------------------------------------------------------------------------------------
+__device__ __forceinline__ float lane_bf(const u32x4& v, int j) {   // bf16 element j of 8 packed in 16 bytes
+  const uint32_t w = v[j >> 1];
+  return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64_t gu_stride, int width,
                                                        uint16_t* out, int tokens) {
-  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   const int tok = (int)(idx / width);
   const int c = (int)(idx - (int64_t)tok * width);
   if (tok >= tokens) return;
-  float g[4], u[4], y[4];
-  load4_bf16(gu + tok * gu_stride + c, g);
-  load4_bf16(gu + tok * gu_stride + width + c, u);
-  for (int i = 0; i < 4; ++i) y[i] = rbf(siluf_(g[i])) * u[i];
-  store4_bf16(out + (int64_t)tok * width + c, y);
+  const u32x4 g = *reinterpret_cast<const u32x4*>(gu + tok * gu_stride + c);
+  const u32x4 u = *reinterpret_cast<const u32x4*>(gu + tok * gu_stride + width + c);
+  u32x4 y;
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const float y0 = rbf(siluf_(lane_bf(g, j))) * lane_bf(u, j);
+    const float y1 = rbf(siluf_(lane_bf(g, j + 1))) * lane_bf(u, j + 1);
+    y[j >> 1] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+  }
+  *reinterpret_cast<u32x4*>(out + (int64_t)tok * width + c) = y;
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -368,12 +391,12 @@ extern "C" int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, i
   const int64_t strides[] = {q_row, q_head, q_out_row, q_out_head, k_row, k_head, k_out_row, k_out_head};
   for (int64_t s : strides)
     if (s % 4) return HSG_ERR_ALIGN;
+  if ((q_heads && !aligned(q_w1, 16)) || (k_heads && !aligned(k_w1, 16))) return HSG_ERR_ALIGN;
   RopeTensor a{static_cast<const uint16_t*>(q_src), q_row, q_head, q_heads, q_w1, static_cast<uint16_t*>(q_out),
                q_out_row, q_out_head};
   RopeTensor b{static_cast<const uint16_t*>(k_src), k_row, k_head, k_heads, k_w1, static_cast<uint16_t*>(k_out),
                k_out_row, k_out_head};
-  const int items = tokens * (q_heads + k_heads);
-  hipLaunchKernelGGL(norm_rope_kernel, dim3((items + 3) / 4), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a,
+  hipLaunchKernelGGL(norm_rope_kernel, dim3((unsigned)tokens), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a,
                      b, pos, inv_freq, rot, q_eps, k_eps, tokens, head_dim);
   return launch_status();
 }
@@ -381,10 +404,11 @@ extern "C" int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, i
 extern "C" int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* out, int32_t tokens,
                             void* stream) {
   if (tokens < 0 || width <= 0) return HSG_ERR_ARG;
-  if (width % 4 || row_stride % 4) return HSG_ERR_ALIGN;
+  if (width % 8 || row_stride % 8) return HSG_ERR_ALIGN;
   if (tokens == 0) return HSG_OK;
   if (!gate_up || !out) return HSG_ERR_ARG;
-  const int64_t total = (int64_t)tokens * width / 4;
+  if (!aligned(gate_up, 16) || !aligned(out, 16)) return HSG_ERR_ALIGN;
+  const int64_t total = (int64_t)tokens * width / 8;
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), row_stride, width,
                      static_cast<uint16_t*>(out), tokens);

@@ -76,16 +76,54 @@ __device__ __forceinline__ float xor_add(float x) { return x + __shfl_xor(x, MAS
 template <int MASK>
 __device__ __forceinline__ float xor_max(float x) { return fmaxf(x, __shfl_xor(x, MASK, 64)); }
 
-__device__ __forceinline__ float wave_sum(float x) {
-  x = xor_add<1>(x); x = xor_add<2>(x); x = xor_add<4>(x);
-  x = xor_add<8>(x); x = xor_add<16>(x); x = xor_add<32>(x);
-  return x;
+// ---- lane exchanges without the LDS crossbar: DPP modifiers (folded into the add) and gfx950's
+// v_permlane16/32_swap. Each partial sum is a + b with a, b the two partners' values, so every lane of a
+// group ends with the same bitwise value, as with the xor butterflies above. ----
+template <int CTRL>
+__device__ __forceinline__ float dpp_(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
+__device__ __forceinline__ float add_xor1(float x) { return x + dpp_<0xB1>(x); }    // quad_perm [1,0,3,2]
+__device__ __forceinline__ float add_xor2(float x) { return x + dpp_<0x4E>(x); }    // quad_perm [2,3,0,1]
+__device__ __forceinline__ float add_xor8(float x) { return x + dpp_<0x128>(x); }   // row_ror:8
+// lane i <- lane 7 - i of its group of 8; after the quad sums this is the other quad's sum
+__device__ __forceinline__ float add_halfmirror(float x) { return x + dpp_<0x141>(x); }
+// v_permlane16_swap(x, x) hands each lane, in one of the two results, its own value and in the other the value
+// of lane xor 16; their sum is the pair sum (likewise permlane32 for lane xor 32)
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// sums over aligned lane groups of 8, 16, 32
+__device__ __forceinline__ float sum8_dpp(float x) { return add_halfmirror(add_xor2(add_xor1(x))); }
+__device__ __forceinline__ float sum16_dpp(float x) { return add_xor8(sum8_dpp(x)); }
+__device__ __forceinline__ float sum32_dpp(float x) { return add_xor16(sum16_dpp(x)); }
+// sum over the 8 lanes sharing lane & 7 (lane xor 8, 16, 32)
+__device__ __forceinline__ float sum_stride8_dpp(float x) { return add_xor32(add_xor16(add_xor8(x))); }
 
+// whole-wave sum and max. Every stage combines the same pairs of partial results as the xor butterfly
+// 1, 2, 4, 8, 16, 32 (the half mirror pairs each quad with the other quad of its 8), so the result is
+// bitwise that of the butterfly, on every lane.
+__device__ __forceinline__ float wave_sum(float x) { return add_xor32(sum32_dpp(x)); }
+
+__device__ __forceinline__ float max_pair16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_pair32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float wave_max(float x) {
-  x = xor_max<1>(x); x = xor_max<2>(x); x = xor_max<4>(x);
-  x = xor_max<8>(x); x = xor_max<16>(x); x = xor_max<32>(x);
-  return x;
+  x = fmaxf(x, dpp_<0xB1>(x));
+  x = fmaxf(x, dpp_<0x4E>(x));
+  x = fmaxf(x, dpp_<0x141>(x));
+  x = fmaxf(x, dpp_<0x128>(x));
+  return max_pair32(max_pair16(x));
 }
 
 inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }

@@ -220,7 +220,7 @@ int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* pool, int64_
  * mean + norm_rope x2 (src/hs_guard/engine/fused_kernels.py:237-284; slot_engine_v8.py:246-249) and the
  * rotary cos/sin of the backbone (slot_engine_v8.py:206): cos/sin = bf16(cos/sin(pos[t] * inv_freq[i])).
  *   x[t, h, :] at src + t*row + h*head;  out[t, h, :] at out + t*out_row + h*out_head (bf16).
- *   w1 [head_dim] fp32 per tensor; inv_freq [rot/2] fp32; pos [tokens] int64.
+ *   w1 [head_dim] fp32 per tensor (16-byte aligned); inv_freq [rot/2] fp32; pos [tokens] int64.
  * Supported: head_dim == 256, rot a power of two in [8, 256].
  */
 int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_heads, const float* q_w1,
@@ -232,6 +232,7 @@ int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_he
 /*
  * SiLU-mul of the fused gate|up projection. Replaces silu_mul (src/hs_guard/engine/fused_kernels.py:86-90):
  *   out[t, c] = bf16(bf16(silu(gu[t, c])) * gu[t, width + c]), out [tokens, width] bf16.
+ * Supported: width and row_stride multiples of 8, pointers 16-byte aligned.
  */
 int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* out, int32_t tokens,
                  void* stream);

@@ -104,26 +104,28 @@ def test_multi_token_and_padding():
             np.testing.assert_array_equal(got[s], _np(state0[s]))
 
 
-def test_packed_gated_matches_oracle():
-    """Packed rows (offsets) with the fused gated RMSNorm epilogue, z read from a strided projection."""
+def _check_packed_gated(lens_list, A_log_vals, dt_scale, seed, state_scale=0.02):
+    """Packed rows (offsets) with the fused gated RMSNorm epilogue, z read from a strided projection; gated
+    outputs and states against the oracle, rows of zero length bit-exact."""
     from hs_guard._lib import lib
-    print("[gdn] packed + gated", flush=True)
-    gen = torch.Generator().manual_seed(2)
+    gen = torch.Generator().manual_seed(seed)
     H = HV = 16
     K = 128
-    lens = torch.tensor([3, 1, 0, 4], dtype=torch.long)
-    offsets = torch.tensor([0, 3, 4, 4], dtype=torch.long)
+    N = len(lens_list)
+    lens = torch.tensor(lens_list, dtype=torch.long)
+    offsets = torch.cumsum(lens, 0) - lens
     T = int(lens.sum())
     C = 2 * H * K + HV * K
     stride = C + HV * K + 2 * HV + 8   # fused projection row: qkv | z | b | a | pad
     proj = torch.randn(T, stride, generator=gen).to(torch.bfloat16)
     qkv, z = proj[:, :C], proj[:, C:C + HV * K]
     ab = torch.randn(T, 2 * HV, generator=gen).to(torch.bfloat16)
-    A_log = torch.zeros(HV, dtype=torch.bfloat16)
-    dt = (torch.randn(HV, generator=gen) * 0.5).to(torch.bfloat16)
+    A_log = torch.tensor(A_log_vals, dtype=torch.float32).repeat(HV // len(A_log_vals)).to(torch.bfloat16)
+    dt = (torch.randn(HV, generator=gen) * dt_scale).to(torch.bfloat16)
     norm_w = (1 + 0.1 * torch.randn(K, generator=gen)).to(torch.bfloat16)
-    state0 = torch.randn(6, HV, K, K, generator=gen) * 0.02
-    slots = torch.tensor([1, 3, 0, 5], dtype=torch.long)
+    S = N + 2
+    state0 = torch.randn(S, HV, K, K, generator=gen) * state_scale
+    slots = torch.randperm(S, generator=gen)[:N]
     dev = torch.device("cuda:0")
     proj_d, ab_d, state = proj.to(dev), ab.to(dev), state0.to(dev)
     out = torch.empty(T, HV * K, dtype=torch.bfloat16, device=dev)
@@ -131,17 +133,17 @@ def test_packed_gated_matches_oracle():
     A_d, dt_d, w_d = A_log.to(dev), dt.to(dev), norm_w.to(dev)
     rc = lib().hsg_gdn_slot_step_gated(
         proj_d.data_ptr(), stride, 0, H * K, 2 * H * K, ab_d[:, HV:].data_ptr(), ab_d.data_ptr(), 2 * HV,
-        A_d.data_ptr(), dt_d.data_ptr(), state.data_ptr(), 0, 6, slots_d.data_ptr(), lens_d.data_ptr(),
-        off_d.data_ptr(), 4, 0, H, HV, K, K, K ** -0.5, proj_d[:, C:].data_ptr(), stride, w_d.data_ptr(), 1e-6,
+        A_d.data_ptr(), dt_d.data_ptr(), state.data_ptr(), 0, S, slots_d.data_ptr(), lens_d.data_ptr(),
+        off_d.data_ptr(), N, 0, H, HV, K, K, K ** -0.5, proj_d[:, C:].data_ptr(), stride, w_d.data_ptr(), 1e-6,
         out.data_ptr(), 0, 0, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     # oracle in padded form
     L = int(lens.max())
-    packed_pad = np.zeros((4, L, C))
-    a_pad = np.zeros((4, L, HV))
-    b_pad = np.zeros((4, L, HV))
-    z_pad = np.zeros((4, L, HV, K))
-    for n in range(4):
+    packed_pad = np.zeros((N, L, C))
+    a_pad = np.zeros((N, L, HV))
+    b_pad = np.zeros((N, L, HV))
+    z_pad = np.zeros((N, L, HV, K))
+    for n in range(N):
         o0, ln = int(offsets[n]), int(lens[n])
         packed_pad[n, :ln] = _np(qkv[o0:o0 + ln])
         a_pad[n, :ln] = _np(ab[o0:o0 + ln, HV:])
@@ -152,7 +154,7 @@ def test_packed_gated_matches_oracle():
     from oracle.bf16 import bf16
     gated_ref = oglue.gated_rmsnorm(bf16(o_ref), z_pad, _np(norm_w), 1e-6)
     got = _np(out)
-    for n in range(4):
+    for n in range(N):
         o0, ln = int(offsets[n]), int(lens[n])
         if ln == 0:
             continue
@@ -161,8 +163,29 @@ def test_packed_gated_matches_oracle():
         assert bad == 0, f"row {n}: {bad} gated outputs off (max {worst})"
     torch.cuda.synchronize()
     gs = _np(state)
-    for s in (1, 3, 5):
-        rel, mx = _state_err(gs[s], st_ref[s])
-        assert rel <= STATE_TOL and mx <= STATE_TOL
-    np.testing.assert_array_equal(gs[0], _np(state0[0]))
-    np.testing.assert_array_equal(gs[2], _np(state0[2]))
+    for n in range(N):
+        s = int(slots[n])
+        if int(lens[n]) > 0:
+            rel, mx = _state_err(gs[s], st_ref[s])
+            assert rel <= STATE_TOL and mx <= STATE_TOL, f"row {n} slot {s}: {rel:.2e} {mx:.2e}"
+        else:
+            np.testing.assert_array_equal(gs[s], _np(state0[s]))
+    for s in set(range(S)) - set(slots.tolist()):
+        np.testing.assert_array_equal(gs[s], _np(state0[s]))
+
+
+def test_packed_gated_matches_oracle():
+    """Packed rows with the fused gated RMSNorm epilogue: short rows, one of zero length."""
+    print("[gdn] packed + gated", flush=True)
+    _check_packed_gated([3, 1, 0, 4], [0.0], 0.5, seed=2)
+
+
+@pytest.mark.parametrize("case", ["bursts", "fast_decay", "zero_decay"])
+def test_packed_gated_long_rows_and_decay(case):
+    """Rows spanning several 8-token bursts (full and partial), and heads whose decay is fast enough that the
+    kernel's deferred decay factor is folded back into the state mid-row (exp(A_log) = 20: exp(g) ~ 1e-6 per
+    token, below 2^-40 after two tokens) or underflows to exactly zero in fp32 (exp(A_log) = 403)."""
+    print(f"[gdn] packed + gated, {case}", flush=True)
+    lens = [64, 17, 1, 9, 0, 33, 8, 2]
+    A_log = {"bursts": [0.0, -1.0], "fast_decay": [0.0, 3.0, -2.0, 3.0], "zero_decay": [6.0, 0.0, 3.0, 6.0]}[case]
+    _check_packed_gated(lens, A_log, 1.0, seed=11, state_scale=0.05)
