@@ -9,13 +9,15 @@
 // Mapping: query rows r = l*G + g (token l, q group g) of one (row, kv head) form 16-row tiles; one
 // workgroup (4 waves) per (row, kv head, query group qg), wave w taking tile 4*qg + w, so a 64-step row
 // spreads over several workgroups that stream the same ring in parallel. The in-place ring write is a second
-// launch (ring_write_kernel) after all reads. Per 64 keys the workgroup stages K
-// (row-major) and V (transposed) in LDS with coalesced 16-byte loads, skipping fills whose positions are
-// outside every query's window; then for each of the two 32-key softmax blocks of the fill each wave runs
-// on v_mfma_f32_16x16x32_bf16:
+// launch (ring_write_kernel) after all reads. All key positions of the ring and the tick go to LDS first, and
+// fills (64 keys) whose positions are outside every query's window of the workgroup are skipped. Per fill the
+// workgroup stages K and V row-major in LDS from registers loaded during the previous fill (each load
+// instruction of a wave reads two whole 512-byte key rows); then for each of the fill's two 32-key softmax
+// blocks each wave runs on v_mfma_f32_16x16x32_bf16:
 //   S^T[key, m] = K . Q^T   (A = K rows from LDS, B = Q from registers; 2 key tiles x 8 d-steps)
-//   O^T[d, m] += V^T . P^T  (A = V^T from LDS, B = P straight from the S^T accumulators: the k order of the
-//                            product is the lane's own key order, so P never leaves registers)
+//   O^T[d, m] += V^T . P^T  (A = V^T by LDS transpose reads of the row-major V, B = P straight from the S^T
+//                            accumulators: the k order of the product is the lane's own key order, so P
+//                            never leaves registers)
 // The S^T accumulator layout puts one query row per lane column, so the running max / sum and the O^T
 // rescale are per-lane scalars plus a 2-step butterfly (lane xor 16, 32).
 #include <math.h>
@@ -32,8 +34,7 @@ constexpr int SB = 2;                  // softmax blocks staged per LDS fill
 constexpr int KF = KB * SB;            // keys per LDS fill
 constexpr int W_MAX = 512;
 constexpr int LB_MAX = 64;
-constexpr int KS_STRIDE = D + 8;       // bf16 per K row in LDS (16-byte pad)
-constexpr int VT_STRIDE = KF + 8;      // bf16 per V^T row in LDS
+constexpr int KS_STRIDE = D + 8;       // bf16 per K or V row in LDS (16-byte pad)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
@@ -56,14 +57,33 @@ struct RingParams {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 w) { return __builtin_bit_cast(bf16x8, w); }
 
+constexpr int KP_NONE = -(1 << 30);
+
+// exp of the softmax argument on the hardware exp2 (v_exp_f32): exp(x) = 2^(x log2 e). The reference kernel
+// takes tl.exp, Triton's fast exponential, here too (src/hs_guard/engine/fused_kernels.py:318).
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_;
+
+// LDS transpose read (ds_read_b64_tr_b16): within each group of 16 lanes, lane 4q + e receives element e of
+// the 4-element (8-byte) vectors addressed by lanes q, q + 4, q + 8, q + 12 of its group. With V row-major
+// ([key][dim]), lane s of a group addressing key row r0 + (s >> 2), dims c0 + 4 (s & 3) .. +3 receives dim
+// c0 + s of keys r0 .. r0 + 3: the A operand of O^T += V^T . P^T.
+__device__ __forceinline__ uint2 ld_tr4(const uint16_t* p) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_*)(p)));
+}
+
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-__global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParams p) {
+__global__ __launch_bounds__(NW * 64, 2) void ring_attn_mfma_kernel(const RingParams p) {
   __shared__ __align__(16) uint16_t Ks[KF * KS_STRIDE];
-  __shared__ __align__(16) uint16_t Vt[D * VT_STRIDE];
-  __shared__ int64_t kp_s[KF];
+  __shared__ __align__(16) uint16_t Vs[KF * KS_STRIDE];
+  // key position - start (the row's first new position), clamped to [-2W-1, 2W+1]; KP_NONE for an empty
+  // column: ring columns [0, W), then the tick's new keys
+  __shared__ int kp_all[W_MAX + LB_MAX];
+  __shared__ uint32_t wave_mask[NW];           // per wave: bit f set if fill f has a key visible to the group
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -109,7 +129,6 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
     const int gq = r - l_tok * G;
     const bool row_ok = has_tile && r < M;
     const bool q_valid = row_ok && l_tok < len;
-    const int64_t qpos = start + l_tok;
     bf16x8 qb[D / 32];
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
@@ -128,69 +147,87 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) O[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    for (int blk = 0; blk < n_ring_blocks + n_new_blocks;) {
-      // a fill holds up to SB consecutive softmax blocks of one kind (ring columns or new keys)
-      const bool is_ring = blk < n_ring_blocks;
-      const int nb = is_ring ? min(SB, n_ring_blocks - blk) : min(SB, n_ring_blocks + n_new_blocks - blk);
+    // Fills: n_ring_fills of up to SB ring blocks, then the new-key blocks in fills of up to SB. Every key
+    // position goes to LDS in one round trip and the fills no query of this group sees are skipped; the
+    // next visible fill's K and V are loaded into registers while the current one is computed.
+    const int n_ring_fills = (n_ring_blocks + SB - 1) / SB;
+    const int n_fills = n_ring_fills + (n_new_blocks + SB - 1) / SB;
+    uint32_t my_mask = 0u;
+    for (int c = tid; c < W + n_new_blocks * KB; c += NW * 64) {
+      int64_t kpos;
+      int f;
+      if (c < W) {
+        kpos = c < n_ring_blocks * KB ? rpos[c] : -1;
+        f = c / KF;
+      } else {
+        const int j = c - W;
+        kpos = j < len ? start + j : -1;
+        f = n_ring_fills + j / KF;
+      }
+      const int64_t rel = kpos - start;
+      kp_all[c] = kpos < 0 ? KP_NONE : (int)(rel < -2 * W - 1 ? -2 * W - 1 : rel > 2 * W + 1 ? 2 * W + 1 : rel);
+      if (kpos >= 0 && kpos <= qpos_hi && kpos > qpos_lo - W) my_mask |= 1u << f;
+    }
+    // OR over the workgroup: wave butterfly, then one word per wave through LDS
+    for (int o = 1; o < 64; o <<= 1) my_mask |= (uint32_t)__shfl_xor((int)my_mask, o, 64);
+    if (lane == 0) wave_mask[wave] = my_mask;
+    __syncthreads();
+    const uint32_t fmask = wave_mask[0] | wave_mask[1] | wave_mask[2] | wave_mask[3];
+    auto fill_geom = [&](int f, bool& is_ring, int& c0, int& nb) {
+      is_ring = f < n_ring_fills;
+      const int b0 = is_ring ? f * SB : (f - n_ring_fills) * SB;
+      nb = is_ring ? min(SB, n_ring_blocks - b0) : min(SB, n_new_blocks - b0);
+      c0 = b0 * KB;   // ring column or new-key index of the fill's first key
+    };
+    // Thread t holds dims 8 (t % 32) .. +7 of keys t / 32 + 8 i (i < 8) of K and of V: every load instruction
+    // of a wave reads two whole 512-byte key rows. Keys past the fill's valid ones load a clamped valid row
+    // and are zeroed when staged.
+    u32x4 kr[8], vr[8];
+    auto prefetch = [&](int f) {
+      bool is_ring; int c0, nb;
+      fill_geom(f, is_ring, c0, nb);
       const int nkeys = nb * KB;
-      const int c0 = is_ring ? blk * KB : (blk - n_ring_blocks) * KB;   // ring column or new-key index
-      blk += nb;
-      __syncthreads();  // the previous fill's LDS reads are done
-      int vis = 0;
-      if (tid < KF) {
-        int64_t kpos = -1;
-        if (tid < nkeys) kpos = is_ring ? rpos[c0 + tid] : ((c0 + tid < len) ? start + c0 + tid : -1);
-        kp_s[tid] = kpos;
-        vis = kpos >= 0 && kpos <= qpos_hi && kpos > qpos_lo - W;
-      }
-      if (!__syncthreads_or(vis)) continue;  // no query of this group sees these keys
-      // ---- stage K (row-major): 4 threads per 512-byte row, 128 bytes each ----
-      {
-        const int row = tid >> 2, seg = tid & 3;
-        const uint16_t* src;
-        bool live;
-        if (is_ring) { src = p.ring_k + ring_base + (int64_t)(c0 + row) * D; live = row < nkeys; }
-        else { src = p.new_k + nk_row + (int64_t)(c0 + row) * p.nk_sl + h * p.nk_sh; live = row < nkeys && c0 + row < len; }
-        uint4 w[8];
+      const int dcol = 8 * (tid & 31);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          w[i] = live ? *reinterpret_cast<const uint4*>(src + seg * 64 + 8 * i) : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&Ks[row * KS_STRIDE + seg * 64 + 8 * i]) = w[i];
-      }
-      // ---- stage V transposed: a key pair x 32 dims per thread ----
-      {
-        const int kp2 = tid & 31, chunk = tid >> 5;
-        const int k0 = 2 * kp2, d0 = chunk * 32;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int dd = d0 + 16 * half;
-          uint4 a[2], b[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int key = k0 + e;
-            const uint16_t* src;
-            bool live;
-            if (is_ring) { src = p.ring_v + ring_base + (int64_t)(c0 + key) * D; live = key < nkeys; }
-            else { src = p.new_v + nv_row + (int64_t)(c0 + key) * p.nv_sl + h * p.nv_sh; live = key < nkeys && c0 + key < len; }
-            uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0;
-            if (live) {
-              x0 = *reinterpret_cast<const uint4*>(src + dd);
-              x1 = *reinterpret_cast<const uint4*>(src + dd + 8);
-            }
-            if (e == 0) { a[0] = x0; a[1] = x1; } else { b[0] = x0; b[1] = x1; }
-          }
-          const uint32_t* va = reinterpret_cast<const uint32_t*>(a);
-          const uint32_t* vb = reinterpret_cast<const uint32_t*>(b);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {   // dims dd + 2i, dd + 2i + 1
-            const uint32_t lo = (va[i] & 0xffffu) | (vb[i] << 16);
-            const uint32_t hi = (va[i] >> 16) | (vb[i] & 0xffff0000u);
-            *reinterpret_cast<uint32_t*>(&Vt[(dd + 2 * i) * VT_STRIDE + k0]) = lo;
-            *reinterpret_cast<uint32_t*>(&Vt[(dd + 2 * i + 1) * VT_STRIDE + k0]) = hi;
-          }
+      for (int i = 0; i < 8; ++i) {
+        const int key = (tid >> 5) + 8 * i;
+        const uint16_t* ksrc;
+        const uint16_t* vsrc;
+        if (is_ring) {
+          const int64_t off = ring_base + (int64_t)(c0 + min(key, nkeys - 1)) * D + dcol;
+          ksrc = p.ring_k + off;
+          vsrc = p.ring_v + off;
+        } else {
+          const int64_t j = min(c0 + key, (int)len - 1);
+          ksrc = p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh + dcol;
+          vsrc = p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh + dcol;
         }
+        kr[i] = *reinterpret_cast<const u32x4*>(ksrc);
+        vr[i] = *reinterpret_cast<const u32x4*>(vsrc);
       }
+    };
+    auto next_fill = [&](int f) {   // first visible fill after f (n_fills if none)
+      const uint32_t rest = f + 1 < 32 ? (fmask >> (f + 1)) : 0u;
+      return rest ? f + 1 + __builtin_ctz(rest) : n_fills;
+    };
+    int fcur = next_fill(-1);
+    if (fcur < n_fills) prefetch(fcur);
+    for (; fcur < n_fills; fcur = next_fill(fcur)) {
+      bool is_ring; int c0, nb;
+      fill_geom(fcur, is_ring, c0, nb);
+      const int nkeys = nb * KB;
+      const int kbase = is_ring ? c0 : W + c0;   // the fill's first key in kp_all
+      __syncthreads();  // the previous fill's LDS reads are done
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int key = (tid >> 5) + 8 * i;
+        const bool live = key < nkeys && (is_ring || c0 + key < len);
+        const int o = key * KS_STRIDE + 8 * (tid & 31);
+        *reinterpret_cast<u32x4*>(&Ks[o]) = live ? kr[i] : (u32x4){0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(&Vs[o]) = live ? vr[i] : (u32x4){0u, 0u, 0u, 0u};
+      }
+      const int fnext = next_fill(fcur);
+      if (fnext < n_fills) prefetch(fnext);
       __syncthreads();
       if (!has_tile) continue;
 #pragma unroll 1
@@ -216,38 +253,37 @@ __global__ __launch_bounds__(NW * 64) void ring_attn_mfma_kernel(const RingParam
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int64_t kpos = kp_s[kb + 16 * kt + 4 * q4 + i];
-            const bool ok = q_valid && kpos >= 0 && kpos <= qpos && kpos > qpos - W;
+            const int rel = kp_all[kbase + kb + 16 * kt + 4 * q4 + i];
+            const bool ok = q_valid && rel <= l_tok && rel > l_tok - W;   // KP_NONE fails the second
             const float v = ok ? S[kt][i] * p.scale : -INFINITY;
             s[4 * kt + i] = v;
             bmax = fmaxf(bmax, v);
           }
         }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        bmax = max_pair32(max_pair16(bmax));   // over q4 (lane xor 16, 32)
         const float m_new = fmaxf(m_run, bmax);
         const float m_safe = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = expf(m_run - m_safe);   // exp(-inf) = 0 before the first visible key
+        const float alpha = exp_fast(m_run - m_safe);   // exp(-inf) = 0 before the first visible key
         float psum = 0.f;
         uint32_t pk[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p0 = expf(s[2 * i] - m_safe);
-          const float p1 = expf(s[2 * i + 1] - m_safe);
+          const float p0 = exp_fast(s[2 * i] - m_safe);
+          const float p1 = exp_fast(s[2 * i + 1] - m_safe);
           psum += p0 + p1;
           pk[i] = pack_bf16(p0, p1);
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = add_xor32(add_xor16(psum));
         l_run = l_run * alpha + psum;
         m_run = m_new;
         const bf16x8 pb = as_bf16x8(make_uint4(pk[0], pk[1], pk[2], pk[3]));
         // ---- O^T += V^T . P^T over the block's 32 keys, in the lane's key order ----
 #pragma unroll
         for (int t = 0; t < D / 16; ++t) {
-          const uint16_t* vrow = &Vt[(16 * t + mcol) * VT_STRIDE + kb];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * q4);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * q4);
+          // dim 16 t + mcol of keys kb + 4 q4 .. +3 and kb + 16 + 4 q4 .. +3 (the lane's key order of P)
+          const uint16_t* vsrc = &Vs[(kb + 4 * q4 + (mcol >> 2)) * KS_STRIDE + 16 * t + 4 * (mcol & 3)];
+          const uint2 lo = ld_tr4(vsrc);
+          const uint2 hi = ld_tr4(vsrc + 16 * KS_STRIDE);
           const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
           f32x4 o = O[t];
 #pragma unroll
