@@ -60,7 +60,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 w) { return __builtin_bit_cast
 constexpr int KP_NONE = -(1 << 30);
 
 // exp of the softmax argument on the hardware exp2 (v_exp_f32): exp(x) = 2^(x log2 e). The reference kernel
-// takes tl.exp, Triton's fast exponential, here too (src/hs_guard/engine/fused_kernels.py:318).
+// takes tl.exp, Triton's fast exponential, here too (src/hs_guard/engine/fused_kernels.py:318-319,335-336).
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_;

@@ -32,6 +32,15 @@ constexpr int G_MAX = 16;          // query heads per kv head
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
+// exp of a softmax argument or rescale exponent on the hardware exp2 (v_exp_f32): exp(x) = 2^(x log2 e), as the
+// reference kernel's tl.exp (src/hs_guard/engine/fused_kernels.py:318-319,335-336).
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
+// value of lane l (l uniform over the wave): v_readlane, no LDS round trip
+__device__ __forceinline__ float readlane_f(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
 struct DecParams {
   const uint16_t* q; int64_t q_sn, q_sl, q_sh, q_sg;
   uint16_t* ring_k; uint16_t* ring_v; int64_t ring_rows; int W;
@@ -141,8 +150,7 @@ __global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
         }
         if (m16 < G) *reinterpret_cast<f32x4*>(sc + m16 * p.sc_stride + b * KB + 16 * t + 4 * g4) = sv;
       }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+      bmax = max_pair32(max_pair16(bmax));   // over g4 (lane xor 16, 32)
       if (g4 == 0 && m16 < G) bm[m16 * KB + b] = bmax;
     }
   }
@@ -221,7 +229,7 @@ __global__ __launch_bounds__(256) void decode_values_kernel(const DecParams p) {
   float lpart = 0.f;   // lane g < G: this wave's weighted normaliser for head g
 
   // a block without any visible key has no scores written (every head shares the step's visibility)
-  const bool has_block = ring_block && __shfl(bmv[b < NB ? b : 0], 0, 64) != -INFINITY;
+  const bool has_block = ring_block && readlane_f(bmv[b < NB ? b : 0], 0) != -INFINITY;
   if (has_block) {
     const float mb_l = mb;
     uint4 vr[KB / 2];
@@ -236,25 +244,22 @@ __global__ __launch_bounds__(256) void decode_values_kernel(const DecParams p) {
       const float m_g = __shfl(mb_l, g < G ? g : 0, 64);
       float p0 = 0.f, p1 = 0.f;
       if (g < G && m_g != -INFINITY) {
-        p0 = sv[gr][0] == -INFINITY ? 0.f : expf(sv[gr][0] - m_g);
-        p1 = sv[gr][1] == -INFINITY ? 0.f : expf(sv[gr][1] - m_g);
+        p0 = sv[gr][0] == -INFINITY ? 0.f : exp_fast(sv[gr][0] - m_g);
+        p1 = sv[gr][1] == -INFINITY ? 0.f : exp_fast(sv[gr][1] - m_g);
       }
       if (g < G) {
         pb_s[wave][g][key] = rbf(p0);
         pb_s[wave][g][key + 1] = rbf(p1);
       }
       float ps = p0 + p1;   // unrounded, as the reference's row sum
-      ps += __shfl_xor(ps, 1, 64);
-      ps += __shfl_xor(ps, 2, 64);
-      ps += __shfl_xor(ps, 4, 64);
-      ps += __shfl_xor(ps, 8, 64);
+      ps = sum16_dpp(ps);
       // lane 16 j holds the sum for head g0 + j; move it to lane g0 + j
       const float got = __shfl(ps, 16 * ((lane - g0) & 3), 64);
       if (lane >= g0 && lane < g0 + 4 && lane < G) lpart = got;
     }
     // block weight exp(m_b - m_final) per head (lane g < G)
     float wgt = 0.f;
-    if (lane < G && mb_l != -INFINITY) wgt = expf(mb_l - mf);
+    if (lane < G && mb_l != -INFINITY) wgt = exp_fast(mb_l - mf);
     lpart *= wgt;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -277,9 +282,9 @@ __global__ __launch_bounds__(256) void decode_values_kernel(const DecParams p) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       if (g < G) {
-        const float wg = __shfl(wgt, g, 64);
+        const float wg = readlane_f(wgt, g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = (acc[g][i] + __shfl_xor(acc[g][i], 32, 64)) * wg;  // both key halves
+        for (int i = 0; i < 8; ++i) acc[g][i] = add_xor32(acc[g][i]) * wg;  // both key halves (lane xor 32)
       }
     }
   }
@@ -291,13 +296,13 @@ __global__ __launch_bounds__(256) void decode_values_kernel(const DecParams p) {
     load4_bf16(vn, v);
     load4_bf16(vn + 4, v + 4);
     float pnew = 0.f;
-    if (lane < G) pnew = expf(sc[lane * p.sc_stride + W] - mf);
+    if (lane < G) pnew = exp_fast(sc[lane * p.sc_stride + W] - mf);
     lpart += pnew;
     if (kh == 0) {
 #pragma unroll
       for (int g = 0; g < GT; ++g) {
         if (g < G) {
-          const float pk = rbf(__shfl(pnew, g, 64));
+          const float pk = rbf(readlane_f(pnew, g));
 #pragma unroll
           for (int i = 0; i < 8; ++i) acc[g][i] += pk * v[i];
         }
