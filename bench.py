@@ -4,10 +4,12 @@ Workload (config 5, mixed serving): 352 concurrent slots on the full random-init
 24 layers 3 GDN : 1 attention, GDN 16x128, attention 16q/4kv/256, MLP 3584, vocab 151,936, bf16 weights
 N(0, 0.02)), fp32 recurrent state. Every slot first gets an initial context drawn uniformly from
 {512, 2048, 8000} tokens (untimed prefill). Each step every slot appends c tokens, c = 1 (p 0.8),
-U{2..16} (p 0.15), U{17..64} (p 0.05); the step is one StreamingGuard-engine tick under hipGraph:
-H2D of the packed tick, graph replay, D2H of both roles' probabilities, stream sync. After each step every
-slot is reset with p = 0.01 and re-prefilled with a fresh context, untimed (prefill is outside the
-reference's timing scope, docs/technical_report.tex:117).
+U{2..16} (p 0.15), U{17..64} (p 0.05); the step is one engine tick under hipGraph through step_packed, the
+call the reference's serving backend makes (examples/demo/runtime_v10.py:114): H2D of the packed tick, graph
+replay, D2H of both roles' probabilities, stream sync, probabilities on the host as [R, n, lb, 3]. The same
+load through step() (one CPU tensor per request and role, StreamingGuard's call) is reported as api_step.
+After each step every slot is reset with p = 0.01 and re-prefilled with a fresh context, untimed (prefill is
+outside the reference's timing scope, docs/technical_report.tex:117).
 
 value = streamed tokens / summed host-to-host step time over the K timed steps. Also reported: p50/p95
 of those step times, the pure 352 x 1-token decode step and the 1-slot single-token step (20 warm-up +
@@ -328,7 +330,7 @@ def main():
         caps = eng.stats["captures"]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        eng.step(req)
+        eng.step_packed(req)
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
         step_tokens.append(sum(len(ids) for _, ids in req))
@@ -347,11 +349,27 @@ def main():
     slow = sorted(range(len(times)), key=lambda i: -times[i])[:3]
     log("slowest steps: " + ", ".join(f"#{i} {times[i] * 1e3:.1f} ms ({step_tokens[i]} tokens)" for i in slow))
     step_ms = [t * 1e3 for t in times]
+    # the same mixed load through step() (StreamingGuard's call: one CPU tensor per request and role), 60 steps
+    api_t, api_tok = [], 0
+    for i in range(60):
+        req = load.step_requests()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.step(req)
+        torch.cuda.synchronize()
+        api_t.append(time.perf_counter() - t0)
+        api_tok += sum(len(ids) for _, ids in req)
+        reprefill(load.resets())
+    api_step = {"steps": len(api_t), "tokens_per_s": round(api_tok / sum(api_t), 1),
+                "p50": round(percentile([t * 1e3 for t in api_t], 50), 3),
+                "p95": round(percentile([t * 1e3 for t in api_t], 95), 3)}
+    log(f"step() leg {api_step}")
     if args.mixed_only:
         print(json.dumps({"mixed_only": True, "value": round(value, 1), "unit": "tokens/s", "steps": args.steps,
                           "tokens": tokens, "ms_per_step": round(total / args.steps * 1e3, 4),
                           "latency_ms": {"p50": round(percentile(step_ms, 50), 3),
-                                         "p95": round(percentile(step_ms, 95), 3)}}), flush=True)
+                                         "p95": round(percentile(step_ms, 95), 3)}, "api_step": api_step}),
+              flush=True)
         return
 
     # ---- per-context latency: every slot restarted with one initial-context length, then timed mixed steps
@@ -371,7 +389,7 @@ def main():
                 req = ctx_load.step_requests()
                 torch.cuda.synchronize()
                 t = time.perf_counter()
-                eng.step(req)
+                eng.step_packed(req)
                 torch.cuda.synchronize()
                 if i >= 5:
                     ts.append((time.perf_counter() - t) * 1e3)
@@ -391,7 +409,7 @@ def main():
             req = make()
             torch.cuda.synchronize()
             t = time.perf_counter()
-            eng.step(req)
+            eng.step_packed(req)
             torch.cuda.synchronize()
             if i >= warm:
                 out.append((time.perf_counter() - t) * 1e3)
@@ -441,6 +459,7 @@ def main():
         "latency_ms": {"p50": round(percentile(step_ms, 50), 3), "p95": round(percentile(step_ms, 95), 3),
                        "max": round(max(step_ms), 3)},
         "latency_by_context_ms": by_context,
+        "api_step": api_step,
         "decode_352x1_ms": {"p50": round(percentile(dec, 50), 3), "p95": round(percentile(dec, 95), 3),
                             "tokens_per_s": round(args.slots / (np.mean(dec) / 1e3), 1)},
         "single_token_ms": {"p50": round(percentile(one, 50), 3), "p95": round(percentile(one, 95), 3)},

@@ -103,6 +103,18 @@ def request_order(flat, lens, offsets):
     return np.ascontiguousarray(flat[:, gather])
 
 
+def padded_rows(flat, lens, offsets, lb):
+    """Tick outputs [R, T, 3] (row r at positions offsets[r] .. offsets[r] + lens[r] - 1) as [R, n, lb, 3] with
+    request r's outputs at [:, r, :lens[r]] and zeros after (step_packed's layout), in one scatter."""
+    lens = np.asarray(lens, dtype=np.int64)
+    n = len(lens)
+    out = np.zeros((flat.shape[0], n, lb, 3), dtype=np.float32)
+    row = np.repeat(np.arange(n, dtype=np.int64), lens)
+    col = np.arange(int(lens.sum()), dtype=np.int64) - np.repeat(np.cumsum(lens) - lens, lens)
+    out[:, row, col] = flat[:, np.repeat(np.asarray(offsets, dtype=np.int64), lens) + col]
+    return out
+
+
 class PreparedWeights:
     """The backbone's weights in the kernels' layouts: fused projections (GDN qkv|z|b|a, attention q|k|v, MLP
     gate|up, both heads' first Linear), RMSNorm gains as fp32 1 + w, rotary inverse frequencies. Needs
@@ -487,13 +499,11 @@ class SlotStreamEngine(PreparedWeights):
         self._validate(requests)
         if len(requests) > self.max_rows or any(len(c) > self.max_tick_tokens for _, c in requests):
             raise ValueError("step_packed takes one tick: too many rows or tokens")
-        slots = np.fromiter((s for s, _ in requests), dtype=np.int64, count=len(requests))
-        flat, lens, offsets = self._run_arrays([list(c) for _, c in requests], slots)
+        n = len(requests)
+        slots = np.fromiter((s for s, _ in requests), dtype=np.int64, count=n)
+        flat, lens, offsets = self._run_arrays([c if isinstance(c, list) else list(c) for _, c in requests], slots)
         lb = bucket(int(lens.max()), (1, 2, 4, 8, 16, 32, 64))
-        out = np.zeros((flat.shape[0], len(requests), lb, 3), dtype=np.float32)
-        for r, (o, ln) in enumerate(zip(offsets, lens)):
-            out[:, r, :ln] = flat[:, o:o + ln]
-        return out, lens
+        return padded_rows(flat, lens, offsets, lb), lens
 
     @torch.inference_mode()
     def step(self, requests):

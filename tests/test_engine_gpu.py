@@ -198,6 +198,32 @@ def test_graph_replays_match_eager(setup):
         assert torch.equal(getattr(eg, name), getattr(ee, name)), name
 
 
+def test_step_packed_matches_step(setup):
+    """step_packed (the serving scheduler's call, src/hs_guard/engine/slot_engine_v7.py:138-145) returns, for
+    the same ticks on an identical engine, exactly step's per-request probabilities in its [R, n, lb, 3]
+    layout (lb = the token bucket of the tick's longest request), zeros past each request's length, and
+    leaves the same pools and lengths."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine, bucket
+    cfg, model, _ = setup
+    print("[engine] step_packed vs step", flush=True)
+    ea = SlotStreamEngine(model, 4)
+    eb = SlotStreamEngine(model, 4)
+    rng = np.random.default_rng(4)
+    for t, tick in enumerate(_schedule(rng, cfg.vocab_size)):
+        tick = [(s, ids[:ea.max_tick_tokens]) for s, ids in tick]   # step_packed takes one tick
+        a = ea.step(tick)
+        packed, lens = eb.step_packed(tick)
+        lb = bucket(max(len(ids) for _, ids in tick), (1, 2, 4, 8, 16, 32, 64))
+        assert packed.shape == (len(ea.roles), len(tick), lb, 3) and list(lens) == [len(ids) for _, ids in tick]
+        for r_i, role in enumerate(ea.roles):
+            for n, (_, ids) in enumerate(tick):
+                np.testing.assert_array_equal(packed[r_i, n, :len(ids)], a[role][n].numpy(), err_msg=f"tick {t}")
+                assert not packed[r_i, n, len(ids):].any()
+    for name in ("rec", "conv", "ring_k", "ring_v", "ring_pos"):
+        assert torch.equal(getattr(ea, name), getattr(eb, name)), name
+    assert np.array_equal(ea.length, eb.length)
+
+
 def test_streaming_guard_api(setup):
     """Drop-in API: cut scores = 1 - p(safe) of the chosen role, reset clears every slot, snapshots restore."""
     from hs_guard.runtime import StreamingGuard, random_metadata

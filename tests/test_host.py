@@ -167,3 +167,24 @@ def test_request_order_gathers_rows():
     assert got.shape == want.shape and np.array_equal(got, want)
     one = request_order(flat, lens[:1], offsets[:1])
     assert np.array_equal(one, flat[:, offsets[0]:offsets[0] + lens[0]])
+
+
+def test_padded_rows_scatters_each_request():
+    """step_packed's [R, n, lb, 3] layout: request r's outputs (packed at offsets[r], rows packed longest first)
+    at [:, r, :lens[r]], zeros after; the same as copying each row out on its own."""
+    from hs_guard.engine.slot_engine import padded_rows
+    rng = np.random.default_rng(6)
+    lens = rng.integers(1, 65, 41)
+    order = np.argsort(-lens, kind="stable")
+    packed_off = np.concatenate([[0], np.cumsum(lens[order])[:-1]])
+    offsets = np.empty(len(lens), dtype=np.int64)
+    offsets[order] = packed_off
+    flat = rng.random((2, int(lens.sum()) + 3, 3)).astype(np.float32)
+    got = padded_rows(flat, lens, offsets, 64)
+    want = np.zeros((2, len(lens), 64, 3), dtype=np.float32)
+    for r, (o, n) in enumerate(zip(offsets, lens)):
+        want[:, r, :n] = flat[:, o:o + n]
+    assert got.shape == want.shape and np.array_equal(got, want)
+    one = padded_rows(flat, lens[:1], offsets[:1], 64)
+    assert np.array_equal(one[:, 0, :lens[0]], flat[:, offsets[0]:offsets[0] + lens[0]])
+    assert not one[:, 0, lens[0]:].any()
