@@ -44,10 +44,12 @@ def percentile(xs, q):
 
 
 def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
-    """Average duration of hsg_gdn_slot_step_gated at the decode shape (rows x 1 token, 16 heads x 128x128),
-    HIP events recorded on the stream the kernel is launched on. Algorithmic bytes per launch: per (row,
-    head) the state read + write 2*K*V*4 B, plus per (row, head, token) q, k, v, z in and out = 5 x 256 B and
-    a, b = 4 B."""
+    """Average duration of hsg_gdn_conv_slot_step_gated (the GDN layers' conv + SiLU and gated slot step in one
+    kernel, as the engine runs it) at the decode shape (rows x 1 token, 16 heads x 128x128), HIP events recorded
+    on the stream the kernel is launched on. Algorithmic bytes per launch: per (row, head) the state read +
+    write 2*K*V*4 B and the 3-row conv history of its 3*128 channels read + written 2 x 3 x 384 x 2 B, per (row,
+    head, token) the raw q, k, v, z in and out = 5 x 256 B and a, b = 4 B, and once per launch the conv
+    weights 16 x 384 x 4 x 2 B."""
     dev = torch.device("cuda:0")
     H = HV = 16
     K = V = 128
@@ -57,7 +59,8 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     state = (torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02)
     if state_dtype == 1:
         state = state.half()
-    conv = torch.randn(rows, C, generator=gen, device=dev).bfloat16()
+    pool = torch.randn(rows + 1, 3, C, generator=gen, device=dev).bfloat16()
+    conv_w = (torch.randn(C, 4, generator=gen, device=dev) * 0.3).bfloat16()
     proj = torch.randn(rows, stride, generator=gen, device=dev).bfloat16()
     out = torch.empty(rows, HV * V, dtype=torch.bfloat16, device=dev)
     A = torch.zeros(HV, dtype=torch.bfloat16, device=dev)
@@ -69,11 +72,12 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     base = proj.data_ptr()
 
     def launch():
-        rc = lib.hsg_gdn_slot_step_gated(conv.data_ptr(), C, 0, H * K, 2 * H * K, base + 2 * (C + HV * V + HV),
-                                         base + 2 * (C + HV * V), stride, A.data_ptr(), A.data_ptr(), state.data_ptr(),
-                                         state_dtype, rows + 1, slots.data_ptr(), lens.data_ptr(), offs.data_ptr(),
-                                         rows, 0, H, HV, K, V, K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6,
-                                         out.data_ptr(), 0, 0, stream.cuda_stream)
+        rc = lib.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, conv_w.data_ptr(), pool.data_ptr(),
+                                              C, base + 2 * (C + HV * V + HV), base + 2 * (C + HV * V), stride,
+                                              A.data_ptr(), A.data_ptr(), state.data_ptr(), state_dtype, rows + 1,
+                                              slots.data_ptr(), lens.data_ptr(), offs.data_ptr(), rows, H, HV, K, V,
+                                              K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(),
+                                              stream.cuda_stream)
         assert rc == 0, rc
     for _ in range(10):
         launch()
@@ -86,12 +90,13 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     torch.cuda.synchronize()
     us = t0.elapsed_time(t1) * 1e3 / iters
     elem = 4 if state_dtype == 0 else 2
-    per_unit_state = 2 * K * V * elem
+    per_unit = 2 * K * V * elem + 2 * 3 * 3 * K * 2
     per_token = 5 * 256 + 4
-    traffic_alg = rows * HV * (per_unit_state + per_token)
+    traffic_alg = rows * HV * (per_unit + per_token) + HV * 3 * K * 4 * 2
     gbs = traffic_alg / (us * 1e-6) / 1e9
-    return {"kernel": "gdn_step_kernel (hsg_gdn_slot_step_gated)", "shape": f"{rows} rows x 1 token x 16 heads",
-            "avg_us": round(us, 2), "alg_bytes_per_launch": traffic_alg, "achieved_gbs": round(gbs, 1)}
+    return {"kernel": "gdn_step_kernel conv variant (hsg_gdn_conv_slot_step_gated)",
+            "shape": f"{rows} rows x 1 token x 16 heads", "avg_us": round(us, 2), "alg_bytes_per_launch": traffic_alg,
+            "achieved_gbs": round(gbs, 1)}
 
 
 def measured_traffic(rows, state_dtype):

@@ -58,6 +58,10 @@ struct GdnParams {
   float eps;
   uint16_t* out;
   int skip_rows, skip_min_len;   // packed layout: rows n < skip_rows with lens >= skip_min_len are left alone
+  // fused causal conv (CONV): qkv holds the raw projection; weights [conv_C, 4], history pool [state_rows, 3, conv_C]
+  const uint16_t* conv_w;
+  uint16_t* conv_pool;
+  int conv_C;
 };
 
 template <typename ST>
@@ -96,7 +100,10 @@ struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
 // Sum over the 8 lanes sharing (lane & 7): lane xor 8, 16, 32 (DPP row rotate, then the two permlane swaps).
 __device__ __forceinline__ float sum_rg(float x) { return sum_stride8_dpp(x); }
 
-template <typename ST, bool GATED>
+constexpr int CKS = 4;            // conv taps
+constexpr int CH3 = 3 * KD;       // conv channels of one (row, value head) workgroup: q and k of its key head, v
+
+template <typename ST, bool GATED, bool CONV>
 __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -113,16 +120,31 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   if (!padded && n < p.skip_rows && ntok >= p.skip_min_len) ntok = 0;   // routed to the chunk kernels
   const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
   const int col = wave * TILE_V + c * 4;
+  // padded layout: the row's outputs at positions t >= ntok are zeros
+  auto zero_tail = [&]() __attribute__((always_inline)) {
+    if (!padded || rg != 0) return;
+    const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int t = ntok; t < p.L; ++t) {
+      const int64_t tok = tok0 + t;
+      if constexpr (!GATED) {
+        const int64_t base = (tok * p.HV + hv) * VD + col;
+        store4_bf16(p.o + base, zero);
+        if (p.sq != nullptr) *reinterpret_cast<float4*>(p.sq + base) = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        store4_bf16(p.out + tok * (int64_t)(p.HV * VD) + hv * VD + col, zero);
+      }
+    }
+  };
+  if (ntok == 0) {   // uniform over the workgroup; nothing is read or updated
+    zero_tail();
+    return;
+  }
 
   // The registers hold St with S = D * St: the per-token decay multiplies the scalar D instead of all 64
   // registers; D is folded back into St before 1 / D could overflow and when the state is stored.
   float S[ROWS][4];
   float D = 1.0f;
   ST* sp = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * KD + rg * ROWS) * (int64_t)VD + col;
-  if (ntok > 0) {
-#pragma unroll
-    for (int j = 0; j < ROWS; ++j) StateIO<ST>::load(sp + j * VD, S[j]);
-  }
   const float A = expf(bf2f(p.A_log[hv]));
   const float dt = bf2f(p.dt_bias[hv]);
   // per burst: normalised q (times scale) and k in fp32, one 16-row piece per lane group (stride 20 floats, so
@@ -134,24 +156,77 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   __shared__ __align__(16) float so_[GATED ? CT : 1][VD];   // bf16-rounded o of the burst, for the gated norm
   __shared__ float sdec_[CT], sbe_[CT];
   constexpr int SEGS = GATED ? 64 : 48;   // 16-byte segments per token: q, k, v (, z)
-  constexpr int PF = (CT * SEGS + 255) / 256;   // segments per thread per burst (the last partly idle)
+  // CONV: the burst's raw q, k, v rows (48 segments each), then its z rows; the first burst also fetches the 3
+  // raw rows before it (the conv history pool), later bursts take them from the previous burst's raw rows in LDS
+  constexpr int RAWSEG0 = (CT + CKS - 1) * 48, RAWSEG = CT * 48;
+  constexpr int NSEG0 = CONV ? RAWSEG0 + CT * 16 : CT * SEGS;
+  constexpr int NSEG = CONV ? RAWSEG + CT * 16 : CT * SEGS;
+  constexpr int PF = (NSEG + 255) / 256;    // segments per thread per burst (the last partly idle)
+  constexpr int PF0 = (NSEG0 + 255) / 256;  // the same for the first burst
+  // CONV: raw rows (row r = token t0 + r - 3 of the burst), conv + SiLU outputs of the burst, tap weights
+  __shared__ __align__(16) uint16_t rw_[CONV ? CT + CKS - 1 : 1][CONV ? CH3 : 8];
+  __shared__ __align__(16) uint16_t co_[CONV ? CT : 1][CONV ? CH3 : 8];
+  __shared__ __align__(16) uint16_t cw_[CONV ? CH3 : 1][CKS];
+  // conv channel of local channel lc (q of key head h, then its k, then v of value head hv)
+  auto conv_ch = [&](int lc) {
+    return lc < KD ? p.q_off + h * KD + lc : lc < 2 * KD ? p.k_off + h * KD + lc - KD : p.v_off + hv * VD + lc - 2 * KD;
+  };
   // gated-norm weights staged in LDS once (read per token from global memory they were reloaded after every
   // output store, since `out` may alias them: one global round trip per token)
   __shared__ __align__(16) uint16_t sw_[GATED ? VD : 1];
-  if (GATED && threadIdx.x < VD / 8)
-    *reinterpret_cast<u32x4*>(&sw_[8 * threadIdx.x]) = *reinterpret_cast<const u32x4*>(p.norm_w + 8 * threadIdx.x);
 
   // The tokens of a row go through LDS in bursts of CT; the next burst is loaded into registers while the
   // current one is processed. Segment e = threadIdx.x + 256 i of a burst is token e / SEGS, piece e % SEGS
   // (pieces 16j .. 16j+15 are q, k, v, z for j = 0..3: an aligned group of 16 lanes holds one whole vector);
   // positions past the row's end re-read its last token (never stored to LDS).
-  u32x4 pf[PF];
+  u32x4 pf[PF], pf0[CONV ? PF0 : 1];
   uint16_t pa = 0, pb = 0;
-  auto fetch = [&](int t) {
+  // CONV, first burst: raw row r = token r - 3 (negative: conv history pool row r), then the z rows
+  auto fetch_first_conv = [&]() __attribute__((always_inline)) {
+    const int tid = tid_per_site();
+#pragma unroll
+    for (int i = 0; i < PF0; ++i) {
+      const int e = min((int)tid + 256 * i, NSEG0 - 1);
+      const uint16_t* src;
+      if (e < RAWSEG0) {
+        const int r = e / 48, gc = conv_ch((e % 48) * 8);
+        src = r < CKS - 1 ? p.conv_pool + (slot * (CKS - 1) + r) * (int64_t)p.conv_C + gc
+                          : p.qkv + (tok0 + min(r - (CKS - 1), ntok - 1)) * p.qkv_stride + gc;
+      } else {
+        const int u = min((e - RAWSEG0) / 16, ntok - 1);
+        src = p.z + (tok0 + u) * p.z_stride + hv * VD + ((e - RAWSEG0) & 15) * 8;
+      }
+      pf0[CONV ? i : 0] = *reinterpret_cast<const u32x4*>(src);
+    }
+    const int64_t tok = tok0 + min((int)tid, ntok - 1);
+    pa = p.a[tok * p.ab_stride + hv];
+    pb = p.b[tok * p.ab_stride + hv];
+  };
+  auto fetch = [&](int t) __attribute__((always_inline)) {
+    const int tid = tid_per_site();
     const int last = ntok - 1 - t;
+    if constexpr (CONV) {   // raw rows of tokens t .. t + 7, then their z rows
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int e = tid + 256 * i;
+        const uint16_t* src;
+        if (e < RAWSEG) {
+          const int u = min(e / 48, last);
+          src = p.qkv + (tok0 + t + u) * p.qkv_stride + conv_ch((e % 48) * 8);
+        } else {
+          const int u = min((e - RAWSEG) / 16, last);
+          src = p.z + (tok0 + t + u) * p.z_stride + hv * VD + ((e - RAWSEG) & 15) * 8;
+        }
+        pf[i] = *reinterpret_cast<const u32x4*>(src);
+      }
+      const int64_t tok = tok0 + t + min((int)tid, last);
+      pa = p.a[tok * p.ab_stride + hv];
+      pb = p.b[tok * p.ab_stride + hv];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int e = threadIdx.x + 256 * i;
+      const int e = tid + 256 * i;
       const int u = min(e / SEGS, last);
       const int sg = e % SEGS;
       const int which = sg >> 4;
@@ -164,16 +239,120 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
                                        : p.z + tok * p.z_stride + hv * VD + c;
       pf[i] = *reinterpret_cast<const u32x4*>(src);
     }
-    const int64_t tok = tok0 + t + min((int)threadIdx.x, last);
+    const int64_t tok = tok0 + t + min((int)tid, last);
     pa = p.a[tok * p.ab_stride + hv];
     pb = p.b[tok * p.ab_stride + hv];
   };
   // prefetched burst -> LDS: q <- q / sqrt(|q|^2 + 1e-6) * scale and k <- k / sqrt(|k|^2 + 1e-6) once per token
   // (|x|^2 summed over the 16 lanes holding the vector), v and z as loaded, exp(g) and beta by thread u
-  auto stage = [&](int nt) {
+  // CONV: raw rows -> LDS, then each (token, 8 channels) of the burst gets acc = sum_k w[c, k] x[t - 3 + k] in
+  // fp32 (as conv_silu_kernel) and bf16(silu(bf16(acc))), then q and k are normalised from those outputs
+  // (later bursts: hist holds the previous burst's raw rows CT .. CT + 2, read by threads < 144)
+  u32x4 hist;
+  auto stage_conv = [&](int nt, bool first) __attribute__((always_inline)) {
+    const int tid = tid_per_site();
+    if (first) {
+#pragma unroll
+      for (int i = 0; i < PF0; ++i) {
+        const int e = tid + 256 * i;
+        if (e < RAWSEG0) {
+          const int r = e / 48;
+          if (r < nt + CKS - 1) *reinterpret_cast<u32x4*>(&rw_[CONV ? r : 0][(e % 48) * 8]) = pf0[CONV ? i : 0];
+        } else if (e < NSEG0) {
+          const int u = (e - RAWSEG0) / 16;
+          if (u < nt) *reinterpret_cast<u32x4*>(&sz_[GATED ? u : 0][((e - RAWSEG0) & 15) * 8]) = pf0[CONV ? i : 0];
+        }
+      }
+    } else {
+      if (tid < (CKS - 1) * 48)
+        *reinterpret_cast<u32x4*>(&rw_[CONV ? tid / 48 : 0][(tid % 48) * 8]) = hist;
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int e = tid + 256 * i;
+        if (e < RAWSEG) {
+          const int u = e / 48;
+          if (u < nt) *reinterpret_cast<u32x4*>(&rw_[CONV ? u + CKS - 1 : 0][(e % 48) * 8]) = pf[i];
+        } else {
+          const int u = (e - RAWSEG) / 16;
+          if (u < nt) *reinterpret_cast<u32x4*>(&sz_[GATED ? u : 0][((e - RAWSEG) & 15) * 8]) = pf[i];
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < (CT * 48 + 255) / 256; ++i) {
+      const int item = tid + 256 * i;
+      const int u = item / 48, c0 = (item % 48) * 8;
+      if (u < nt) {
+        u32x4 xr[CKS];
+#pragma unroll
+        for (int k = 0; k < CKS; ++k) xr[k] = *reinterpret_cast<const u32x4*>(&rw_[CONV ? u + k : 0][c0]);
+        u32x4 y;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float rr[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const uint2 wv = *reinterpret_cast<const uint2*>(&cw_[CONV ? c0 + j + hh : 0][0]);
+            float w4[4];
+            unpack2(wv.x, w4[0], w4[1]);
+            unpack2(wv.y, w4[2], w4[3]);
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < CKS; ++k) {
+              const uint32_t word = xr[k][(j + hh) >> 1];
+              acc = fmaf(w4[k], __uint_as_float(((j + hh) & 1) ? (word & 0xffff0000u) : (word << 16)), acc);
+            }
+            rr[hh] = siluf_(rbf(acc));
+          }
+          y[j >> 1] = (uint32_t)f2bf(rr[0]) | ((uint32_t)f2bf(rr[1]) << 16);
+        }
+        *reinterpret_cast<u32x4*>(&co_[CONV ? u : 0][c0]) = y;
+      }
+    }
+    __syncthreads();
+    {  // q, k of the burst: 8 tokens x 32 segments, one per thread
+      const int e = tid;
+      const int u = e >> 5, which = (e >> 4) & 1, c = (e & 15) * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&co_[CONV ? u : 0][which * KD + c]);
+      float x[8];
+      unpack2(v[0], x[0], x[1]);
+      unpack2(v[1], x[2], x[3]);
+      unpack2(v[2], x[4], x[5]);
+      unpack2(v[3], x[6], x[7]);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+      ss = sum16_dpp(ss);
+      if (u < nt) {
+        const float r = 1.0f / sqrtf(ss + 1e-6f);
+        f32x4_t y0, y1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y0[j] = which == 0 ? x[j] * r * p.scale : x[j] * r;
+          y1[j] = which == 0 ? x[4 + j] * r * p.scale : x[4 + j] * r;
+        }
+        float* dst = which == 0 ? &fq_[u][c / ROWS][c % ROWS] : &fk_[u][c / ROWS][c % ROWS];
+        *reinterpret_cast<f32x4_t*>(dst) = y0;
+        *reinterpret_cast<f32x4_t*>(dst + 4) = y1;
+      }
+    }
+    if (tid < nt) {
+      const float x = bf2f(pa) + dt;
+      const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
+      sdec_[tid] = expf(g);
+      sbe_[tid] = sigmoidf_(bf2f(pb));
+    }
+  };
+  auto stage = [&](int nt, bool first) __attribute__((always_inline)) {
+    const int tid = tid_per_site();
+    if constexpr (CONV) {
+      stage_conv(nt, first);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int e = threadIdx.x + 256 * i;
+      const int e = tid + 256 * i;
       const int u = e / SEGS;
       const int sg = e % SEGS;
       const int which = sg >> 4;
@@ -214,25 +393,50 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
         }
       }
     }
-    if (threadIdx.x < nt) {
+    if (tid < nt) {
       const float x = bf2f(pa) + dt;
       const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
-      sdec_[threadIdx.x] = expf(g);
-      sbe_[threadIdx.x] = sigmoidf_(bf2f(pb));
+      sdec_[tid] = expf(g);
+      sbe_[tid] = sigmoidf_(bf2f(pb));
     }
   };
-  if (ntok > 0) fetch(0);
+  // Issue order: the first burst, the weights, then the state. Load counters retire in order, so staging the
+  // burst (and the weights' copy to LDS) waits only for the loads issued before the state's and overlaps the
+  // state's latency. Every load here is unconditional (the weight loads of surplus threads repeat the last
+  // piece): a load under a branch makes the compiler wait for all outstanding loads where the paths join.
+  if constexpr (CONV) fetch_first_conv();
+  else fetch(0);
+  u32x4 cwr[4], swr;
+  const bool has_cw = CONV && threadIdx.x < CH3 / 8;   // 8 channels x 4 taps = 64 bytes per thread
+  const bool has_sw = GATED && threadIdx.x < VD / 8;
+  if constexpr (CONV) {
+    const uint16_t* wsrc = p.conv_w + (int64_t)conv_ch(8 * min((int)threadIdx.x, CH3 / 8 - 1)) * CKS;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cwr[j] = *reinterpret_cast<const u32x4*>(wsrc + 8 * j);
+  }
+  if constexpr (GATED) swr = *reinterpret_cast<const u32x4*>(p.norm_w + 8 * min((int)threadIdx.x, VD / 8 - 1));
+  __builtin_amdgcn_sched_barrier(0);   // keep the state loads last
+#pragma unroll
+  for (int j = 0; j < ROWS; ++j) StateIO<ST>::load(sp + j * VD, S[j]);
+  if (has_cw) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(&cw_[CONV ? 8 * threadIdx.x : 0][0] + 8 * j) = cwr[j];
+  }
+  if (has_sw) *reinterpret_cast<u32x4*>(&sw_[8 * threadIdx.x]) = swr;
 
+  // The first burst is staged before the loop and each later one at the end of the previous iteration: a
+  // staging at the top of the loop would merge the first iteration's wait with the back edge's and wait for
+  // the state too.
+  stage(min(CT, ntok), true);
   for (int t0 = 0; t0 < ntok; t0 += CT) {
     const int nt = min(CT, ntok - t0);
-    __syncthreads();   // every read of the previous burst's LDS is done
-    stage(nt);
     if (t0 + CT < ntok) fetch(t0 + CT);
     __syncthreads();
 
     for (int tt = 0; tt < nt; ++tt) {
       float v[4];
-      load4_bf16(&sv_[tt][col], v);
+      if constexpr (CONV) load4_bf16(&co_[CONV ? tt : 0][2 * KD + col], v);
+      else load4_bf16(&sv_[tt][col], v);
       const float beta = sbe_[tt];
       float Dn = D * sdec_[tt];
       if (Dn < 0x1p-40f) {   // uniform over the workgroup (every lane has the same D and decay)
@@ -321,29 +525,31 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
         store4_bf16(p.out + (tok0 + t0 + u) * (int64_t)(p.HV * VD) + hv * VD + cc, y);
       }
     }
-  }
-
-  if (padded && rg == 0) {
-    const float zero[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int t = ntok; t < p.L; ++t) {
-      const int64_t tok = tok0 + t;
-      if constexpr (!GATED) {
-        const int64_t base = (tok * p.HV + hv) * VD + col;
-        store4_bf16(p.o + base, zero);
-        if (p.sq != nullptr) *reinterpret_cast<float4*>(p.sq + base) = make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        store4_bf16(p.out + tok * (int64_t)(p.HV * VD) + hv * VD + col, zero);
-      }
+    if (t0 + CT < ntok) {
+      // the next burst's conv history: this (full) burst's last 3 raw rows
+      if (CONV && threadIdx.x < (CKS - 1) * 48)
+        hist = *reinterpret_cast<const u32x4*>(&rw_[CONV ? CT + threadIdx.x / 48 : 0][(threadIdx.x % 48) * 8]);
+      __syncthreads();   // every read of this burst's LDS is done
+      stage(min(CT, ntok - t0 - CT), false);
     }
   }
 
-  if (ntok > 0) {
+  if (CONV && threadIdx.x < (CKS - 1) * 48) {
+    // new conv history = ext[ntok .. ntok + 2] of ext = [pool; tokens]: raw rows nt .. nt + 2 of the last burst
+    // (the row's last three tokens, or old pool rows when it has fewer); every read of the old rows came first
+    const int nt_last = ntok - (ntok - 1) / CT * CT;
+    const int i = threadIdx.x / 48, sg = threadIdx.x % 48;
+    *reinterpret_cast<u32x4*>(p.conv_pool + (slot * (CKS - 1) + i) * (int64_t)p.conv_C + conv_ch(8 * sg)) =
+        *reinterpret_cast<const u32x4*>(&rw_[CONV ? nt_last + i : 0][8 * sg]);
+  }
+
+  zero_tail();
+
 #pragma unroll
-    for (int j = 0; j < ROWS; ++j) {
+  for (int j = 0; j < ROWS; ++j) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) S[j][i] *= D;
-      StateIO<ST>::store(sp + j * VD, S[j]);
-    }
+    for (int i = 0; i < 4; ++i) S[j][i] *= D;
+    StateIO<ST>::store(sp + j * VD, S[j]);
   }
 }
 
@@ -359,14 +565,14 @@ int check_common(const GdnParams& p, int state_dtype, int n_rows, int K, int V) 
   return 1;  // proceed
 }
 
-template <bool GATED>
+template <bool GATED, bool CONV = false>
 int launch(const GdnParams& p, int state_dtype, int n_rows, void* stream) {
   const dim3 grid((unsigned)(n_rows * p.HV));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (state_dtype == HSG_STATE_F32)
-    hipLaunchKernelGGL((gdn_step_kernel<float, GATED>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gdn_step_kernel<float, GATED, CONV>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gdn_step_kernel<uint16_t, GATED>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gdn_step_kernel<uint16_t, GATED, CONV>), grid, dim3(256), 0, s, p);
   return launch_status();
 }
 
@@ -436,4 +642,47 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
   if (!z || !norm_w || !out || skip_rows < 0 || (skip_rows > 0 && skip_min_len < 1)) return HSG_ERR_ARG;
   if (!hsg::aligned(z, 16) || z_stride % 8 || !hsg::aligned(norm_w, 16) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
   return hsg::launch<true>(p, state_dtype, n_rows, stream);
+}
+
+extern "C" int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_stride, int32_t q_off, int32_t k_off,
+                                            int32_t v_off, const void* conv_w, void* conv_pool, int32_t channels,
+                                            const void* a, const void* b, int64_t ab_stride, const void* A_log,
+                                            const void* dt_bias, void* state, int32_t state_dtype,
+                                            int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                                            const int64_t* offsets, int32_t n_rows, int32_t H, int32_t HV,
+                                            int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
+                                            const void* norm_w, float eps, void* out, void* stream) {
+  GdnParams p{};
+  p.qkv = static_cast<const uint16_t*>(proj);
+  p.qkv_stride = proj_stride;
+  p.q_off = q_off; p.k_off = k_off; p.v_off = v_off;
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  p.ab_stride = ab_stride;
+  p.A_log = static_cast<const uint16_t*>(A_log);
+  p.dt_bias = static_cast<const uint16_t*>(dt_bias);
+  p.state = state;
+  p.state_rows = state_rows;
+  p.slots = slots; p.lens = lens; p.offsets = offsets;
+  p.L = 0; p.H = H; p.HV = HV; p.scale = scale;
+  p.z = static_cast<const uint16_t*>(z);
+  p.z_stride = z_stride;
+  p.norm_w = static_cast<const uint16_t*>(norm_w);
+  p.eps = eps;
+  p.out = static_cast<uint16_t*>(out);
+  p.conv_w = static_cast<const uint16_t*>(conv_w);
+  p.conv_pool = static_cast<uint16_t*>(conv_pool);
+  p.conv_C = channels;
+  if (!offsets) return HSG_ERR_ARG;   // packed rows only
+  const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
+  if (rc <= 0) return rc;
+  if (!z || !norm_w || !out || !conv_w || !conv_pool) return HSG_ERR_ARG;
+  // one value head per key head: every (row, head) workgroup owns its q / k conv channels and history
+  if (HV != H) return HSG_ERR_SHAPE;
+  if (channels <= 0 || q_off < 0 || k_off < 0 || v_off < 0 || q_off + H * K > channels || k_off + H * K > channels ||
+      v_off + HV * V > channels || channels > proj_stride)
+    return HSG_ERR_ARG;
+  if (channels % 8 || !hsg::aligned(conv_w, 16) || !hsg::aligned(conv_pool, 16)) return HSG_ERR_ALIGN;
+  if (!hsg::aligned(z, 16) || z_stride % 8 || !hsg::aligned(norm_w, 16) || !hsg::aligned(out, 8)) return HSG_ERR_ALIGN;
+  return hsg::launch<true, true>(p, state_dtype, n_rows, stream);
 }

@@ -13,7 +13,7 @@ namespace {
 // RMSNorm over a 1024-wide row, one wave per token (16 values per lane, two 16-byte loads).
 // add_square + rms_finish (src/hs_guard/engine/fused_kernels.py:30-72): h = bf16(res + mix) (plain fp32
 // add), out = bf16((h * rsqrt(mean(h^2) + eps)) * w1), w1 = 1 + weight in fp32.
-// Embedding variant (slot_engine_v8.py:205,209-210): h = embedding row of the token id.
+// Embedding variant (slot_engine_v8.py:38,42-43): h = embedding row of the token id.
 // ---------------------------------------------------------------------------------------------------
 constexpr int HID_PER_LANE = 16;
 
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64
 
 // ---------------------------------------------------------------------------------------------------
 // Risk heads (src/hs_guard/runtime.py:61-74, src/hs_guard/engine/slot_engine_v7.py:58-61,
-// slot_engine_v8.py:223): given y = bf16(Linear_1024->512(x) + b1) for each role (columns
+// slot_engine_v8.py:56): given y = bf16(Linear_1024->512(x) + b1) for each role (columns
 // [role*512, role*512+512) of the fused projection), LayerNorm(512) in fp32, SiLU, round to bf16, Linear
 // 512->3 with bf16 output, softmax in fp32. One wave per (token, role).
 // ---------------------------------------------------------------------------------------------------
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void risk_head_kernel(const uint16_t* y, int64
 
 // ---------------------------------------------------------------------------------------------------
 // ring_pos[slot, (start + j) % W] = start + j for the valid steps of every row
-// (src/hs_guard/engine/slot_engine_v8.py:208,224; column W stays -1).
+// (src/hs_guard/engine/slot_engine_v8.py:41,57; column W stays -1).
 // ---------------------------------------------------------------------------------------------------
 __global__ void ring_pos_kernel(int64_t* ring_pos, int64_t ring_rows, const int64_t* slots, const int64_t* starts,
                                 const int64_t* lens, int W, int lb_max) {

@@ -118,6 +118,15 @@ __device__ __forceinline__ float max_pair32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// threadIdx.x through an empty asm: a code block called from several sites computes its own addresses from
+// it at each (otherwise the compiler shares them between the sites and keeps them live across the loops in
+// between, which costs registers).
+__device__ __forceinline__ int tid_per_site() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp_<0xB1>(x));
   x = fmaxf(x, dpp_<0x4E>(x));

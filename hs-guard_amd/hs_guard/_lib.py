@@ -49,6 +49,14 @@ SIGNATURES = {
         _P, _P, _P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F,
         _P, _I64, _P, _F, _P, _I32, _I32, _P]),   # z, z_stride, norm_w, eps, out, skip_rows, skip_min_len, stream
+    "hsg_gdn_conv_slot_step_gated": (ctypes.c_int, [
+        _P, _I64, _I32, _I32, _I32,          # proj, proj_stride, q_off, k_off, v_off
+        _P, _P, _I32,                        # conv_w, conv_pool, channels
+        _P, _P, _I64, _P, _P,                # a, b, ab_stride, A_log, dt_bias
+        _P, _I32, _I64,                      # state, state_dtype, state_rows
+        _P, _P, _P, _I32,                    # slots, lens, offsets, n_rows
+        _I32, _I32, _I32, _I32, _F,          # H, HV, K, V, scale
+        _P, _I64, _P, _F, _P, _P]),          # z, z_stride, norm_w, eps, out, stream
     "hsg_ring_attention": (ctypes.c_int, [
         _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
         _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window

@@ -1,7 +1,7 @@
 """MI355X slot-stream engine: per-slot state pools, packed ticks, one hipGraph per (rows, tokens) bucket.
 
 Host orchestration mirrors SlotStreamEngineV7/V8 (src/hs_guard/engine/slot_engine_v7.py:117-167,
-slot_engine_v8.py:197-256): a request list is cut into ticks of at most ``max_tick_tokens`` tokens per slot
+slot_engine_v8.py:30-89): a request list is cut into ticks of at most ``max_tick_tokens`` tokens per slot
 and at most the largest session bucket of rows; each tick is one H2D copy of a packed int64 buffer, one
 graph replay, one D2H copy of the per-token class probabilities of both roles and one stream sync.
 
@@ -166,7 +166,7 @@ class SlotStreamEngine(PreparedWeights):
     slot of padding rows)."""
 
     def __init__(self, model: GuardModel, max_slots, state_dtype="float32", use_graphs=True, roles=ROLES,
-                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=0):
+                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=0, fuse_conv=True):
         if not isinstance(max_slots, int) or max_slots < 1:
             raise ValueError("max_slots must be a positive integer")
         if state_dtype not in STATE_DTYPES:
@@ -182,6 +182,10 @@ class SlotStreamEngine(PreparedWeights):
         self.chunk_min_tokens = chunk_min_tokens
         lib()  # fail loudly here if the HIP library is missing
         cfg = model.config
+        # the GDN layers' causal conv runs inside the slot step (hsg_gdn_conv_slot_step_gated) when every value
+        # head has its own key head and no rows go to the chunk kernels; otherwise as its own kernel first
+        self.fuse_conv = bool(fuse_conv) and chunk_min_tokens == 0 and \
+            cfg.linear_num_value_heads == cfg.linear_num_key_heads
         self.model, self.cfg = model, cfg
         self.max_slots, self.roles, self.use_graphs = max_slots, tuple(roles), use_graphs
         self.window = cfg.window_tokens
@@ -299,7 +303,7 @@ class SlotStreamEngine(PreparedWeights):
                 "starts": x[2 * tb + 3 * nb:2 * tb + 4 * nb], "all": x[:2 * tb + 4 * nb]}
 
     def _forward(self, nb, tb, inp):
-        """The tick's device program (src/hs_guard/engine/slot_engine_v8.py:197-225), launched on the current
+        """The tick's device program (src/hs_guard/engine/slot_engine_v8.py:30-58), launched on the current
         stream. Reads only device memory, so it can be captured into a hipGraph."""
         L = lib()
         cfg = self.cfg
@@ -324,32 +328,43 @@ class SlotStreamEngine(PreparedWeights):
                 C = cfg.conv_dim
                 proj = self._view("proj", tb, self.gdn_in)
                 torch.mm(normed, Lw["w_in"].t(), out=proj)
-                conv = self._view("conv", tb, C)
-                check(L.hsg_conv_silu_update(proj.data_ptr(), self.gdn_in, self.conv[idx].data_ptr(), S,
-                                             Lw["conv_w"].data_ptr(), cfg.linear_conv_kernel_dim, slots.data_ptr(),
-                                             lens.data_ptr(), offsets.data_ptr(), nb, 0, C, conv.data_ptr(), C, st),
-                      "hsg_conv_silu_update")
                 out = self._view("mid", tb, cfg.value_dim)
                 base = proj.data_ptr()
-                # rows are packed longest first: the rows of >= chunk_min_tokens tokens among the first R go to
-                # the chunked kernels (one WY/UT chunk each), the rest to the slot step
-                R = self._chunk_rows(nb, tb)
-                check(L.hsg_gdn_slot_step_gated(
-                    conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
-                    base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), self.gdn_in,
-                    Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), self.rec[idx].data_ptr(),
-                    _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb, 0,
-                    nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in, Lw["norm_w"].data_ptr(), eps,
-                    out.data_ptr(), R, max(self.chunk_min_tokens, 1), st), "hsg_gdn_slot_step_gated")
-                if R:
-                    check(L.hsg_gdn_chunk_prefill_gated(
+                if self.fuse_conv:
+                    # causal conv + SiLU inside the slot step, from the raw projection and the conv history pool
+                    check(L.hsg_gdn_conv_slot_step_gated(
+                        base, self.gdn_in, 0, cfg.key_dim, 2 * cfg.key_dim, Lw["conv_w"].data_ptr(),
+                        self.conv[idx].data_ptr(), C, base + 2 * (C + cfg.value_dim + hv),
+                        base + 2 * (C + cfg.value_dim), self.gdn_in, Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(),
+                        self.rec[idx].data_ptr(), _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(),
+                        offsets.data_ptr(), nb, nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in,
+                        Lw["norm_w"].data_ptr(), eps, out.data_ptr(), st), "hsg_gdn_conv_slot_step_gated")
+                else:
+                    conv = self._view("conv", tb, C)
+                    check(L.hsg_conv_silu_update(proj.data_ptr(), self.gdn_in, self.conv[idx].data_ptr(), S,
+                                                 Lw["conv_w"].data_ptr(), cfg.linear_conv_kernel_dim,
+                                                 slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb, 0, C,
+                                                 conv.data_ptr(), C, st), "hsg_conv_silu_update")
+                    # rows are packed longest first: the rows of >= chunk_min_tokens tokens among the first R go
+                    # to the chunked kernels (one WY/UT chunk each), the rest to the slot step
+                    R = self._chunk_rows(nb, tb)
+                    check(L.hsg_gdn_slot_step_gated(
                         conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
                         base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), self.gdn_in,
                         Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), self.rec[idx].data_ptr(),
-                        _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), R,
-                        self.max_tick_tokens, nh, hv, kd, vd, kd ** -0.5, self._view("gdn_o", tb, cfg.value_dim).data_ptr(),
-                        base + 2 * C, self.gdn_in, Lw["norm_w"].data_ptr(), eps, out.data_ptr(), self.chunk_min_tokens,
-                        self.chunk_ws.data_ptr(), self.chunk_ws.numel(), st), "hsg_gdn_chunk_prefill_gated")
+                        _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb,
+                        0, nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in, Lw["norm_w"].data_ptr(), eps,
+                        out.data_ptr(), R, max(self.chunk_min_tokens, 1), st), "hsg_gdn_slot_step_gated")
+                    if R:
+                        check(L.hsg_gdn_chunk_prefill_gated(
+                            conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
+                            base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), self.gdn_in,
+                            Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), self.rec[idx].data_ptr(),
+                            _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
+                            R, self.max_tick_tokens, nh, hv, kd, vd, kd ** -0.5,
+                            self._view("gdn_o", tb, cfg.value_dim).data_ptr(), base + 2 * C, self.gdn_in,
+                            Lw["norm_w"].data_ptr(), eps, out.data_ptr(), self.chunk_min_tokens,
+                            self.chunk_ws.data_ptr(), self.chunk_ws.numel(), st), "hsg_gdn_chunk_prefill_gated")
                 torch.mm(out, Lw["w_out"].t(), out=mix)
             else:
                 proj = self._view("proj", tb, self.att_in)

@@ -63,7 +63,7 @@ int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_
 /*
  * The same step with Qwen3.5's gated RMSNorm fused into the epilogue.
  * Replaces gdn_slot_v8 followed by gated_finish (src/hs_guard/engine/fused_kernels.py:215-233,
- * composed at src/hs_guard/engine/slot_engine_v8.py:234-238):
+ * composed at src/hs_guard/engine/slot_engine_v8.py:67-71):
  *   out[tok, hv*V + c] = bf16( bf16(w[c] * bf16(o*rsqrt(mean(bf16(o)^2)+eps))) * silu(z[tok, hv*V + c]) )
  *   z [tokens, z_stride] bf16, norm_w [V] bf16, out [tokens, HV*V] bf16.
  * Packed layout: rows n < skip_rows with lens[n] >= skip_min_len (>= 1) are left alone (no output, state
@@ -77,6 +77,26 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
                             int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
                             const void* norm_w, float eps, void* out, int32_t skip_rows, int32_t skip_min_len,
                             void* stream);
+
+/*
+ * hsg_gdn_slot_step_gated with the causal conv + SiLU of its inputs fused in (conv_silu_update,
+ * src/hs_guard/engine/fused_kernels.py:94-136, followed by gdn_slot_v8 and gated_finish, as composed at
+ * src/hs_guard/engine/slot_engine_v8.py:66-71): `proj` holds the raw
+ * projection rows (stride proj_stride), whose first `channels` columns are the conv channels with q, k, v at
+ * q_off, k_off, v_off; conv_w [channels, 4] bf16; conv_pool [state_rows, 3, channels] bf16, the per-slot conv
+ * history, updated in place at slots[n] for rows with lens[n] > 0. Each (row, head) workgroup convolves its own
+ * q, k, v channels from the pool and the raw rows, with the conv kernel's arithmetic, so outputs, state and pool
+ * equal hsg_conv_silu_update followed by hsg_gdn_slot_step_gated bit for bit. Packed rows only (offsets
+ * required), HV == H (every q / k channel belongs to one workgroup), no chunk-routing filter. out must not
+ * alias proj, z or conv_pool; rows must name distinct slots.
+ */
+int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_stride, int32_t q_off, int32_t k_off, int32_t v_off,
+                                 const void* conv_w, void* conv_pool, int32_t channels, const void* a, const void* b,
+                                 int64_t ab_stride, const void* A_log, const void* dt_bias, void* state,
+                                 int32_t state_dtype, int64_t state_rows, const int64_t* slots, const int64_t* lens,
+                                 const int64_t* offsets, int32_t n_rows, int32_t H, int32_t HV, int32_t K, int32_t V,
+                                 float scale, const void* z, int64_t z_stride, const void* norm_w, float eps,
+                                 void* out, void* stream);
 
 /*
  * Chunked gated-delta-rule prefill: the same recurrence and contract as hsg_gdn_slot_step, evaluated
@@ -120,7 +140,7 @@ int hsg_gdn_chunk_prefill_gated(const void* qkv, int64_t qkv_stride, int32_t q_o
  * Window-W GQA attention of this tick's queries over the slot's ring plus this tick's new keys.
  * Replaces ring_attention_v8 (src/hs_guard/engine/fused_kernels.py:358-376; kernel :288-356),
  * ring_attention (src/hs_guard/engine/ring_attention_kernel.py:91-105) and the Lb > 1 ring scatter
- * (src/hs_guard/engine/slot_engine_v8.py:253-255).
+ * (src/hs_guard/engine/slot_engine_v8.py:86-88).
  * Element addresses (row base B(x) = offsets ? offsets[n]*x_sl : n*x_sn):
  *   q[n,l,h,g,:]     = q     + B(q) + l*q_sl + h*q_sh + g*q_sg
  *   new_k[n,l,h,:]   = new_k + B(nk) + l*nk_sl + h*nk_sh         (same for new_v)
@@ -174,7 +194,7 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
 
 /*
  * Embedding gather + RMSNorm of the first layer. Replaces embed_tokens + add_square(hidden) + rms_finish
- * (src/hs_guard/engine/slot_engine_v8.py:205,209-210; fused_kernels.py:30-72):
+ * (src/hs_guard/engine/slot_engine_v8.py:38,42-43; fused_kernels.py:30-72):
  *   hidden[t] = emb[ids[t]];  normed[t] = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1)
  *   emb [vocab, width] bf16, w1 [width] fp32 (= 1 + weight), hidden/normed [tokens, width] bf16.
  * Supported: width == 1024. Ids outside [0, vocab) read row 0 (the host rejects them first).
@@ -184,7 +204,7 @@ int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vocab, const 
 
 /*
  * Residual add + RMSNorm. Replaces add_square + sq.mean + rms_finish
- * (src/hs_guard/engine/fused_kernels.py:30-72; slot_engine_v8.py:216-222):
+ * (src/hs_guard/engine/fused_kernels.py:30-72; slot_engine_v8.py:49-55):
  *   hidden = bf16(hidden + mix) (in place; mix may be NULL: no add);
  *   normed = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1). Supported: width == 1024.
  */
@@ -217,8 +237,8 @@ int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* pool, int64_
 
 /*
  * Per-head RMSNorm(1+w) + partial rotate-half RoPE of q and k in one launch. Replaces square_rows +
- * mean + norm_rope x2 (src/hs_guard/engine/fused_kernels.py:237-284; slot_engine_v8.py:246-249) and the
- * rotary cos/sin of the backbone (slot_engine_v8.py:206): cos/sin = bf16(cos/sin(pos[t] * inv_freq[i])).
+ * mean + norm_rope x2 (src/hs_guard/engine/fused_kernels.py:237-284; slot_engine_v8.py:79-82) and the
+ * rotary cos/sin of the backbone (slot_engine_v8.py:39): cos/sin = bf16(cos/sin(pos[t] * inv_freq[i])).
  *   x[t, h, :] at src + t*row + h*head;  out[t, h, :] at out + t*out_row + h*out_head (bf16).
  *   w1 [head_dim] fp32 per tensor (16-byte aligned); inv_freq [rot/2] fp32; pos [tokens] int64.
  * Supported: head_dim == 256, rot a power of two in [8, 256].
@@ -239,7 +259,7 @@ int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* o
 
 /*
  * Risk heads after the fused first projection. Replaces _risk + softmax
- * (src/hs_guard/engine/slot_engine_v7.py:58-61; slot_engine_v8.py:223; src/hs_guard/runtime.py:61-74):
+ * (src/hs_guard/engine/slot_engine_v7.py:58-61; slot_engine_v8.py:56; src/hs_guard/runtime.py:61-74):
  *   for role r: v = y[t, r*width : (r+1)*width] (bf16 Linear output incl. bias), LayerNorm(eps) in fp32
  *   with ln_w/ln_b [roles, width], SiLU, bf16, Linear to 3 with w2 [roles, 3, width], b2 [roles, 3],
  *   bf16 logits, softmax -> probs [roles, tokens, 3] fp32. Supported: width == 512.
@@ -250,7 +270,7 @@ int hsg_risk_head(const void* y, int64_t y_stride, const void* ln_w, const void*
 
 /*
  * Ring position bookkeeping after all layers. Replaces ring_pos[slots, ring_col] = where(valid, pos, -1)
- * (src/hs_guard/engine/slot_engine_v8.py:208,224): ring_pos[slot, (start + j) % window] = start + j for
+ * (src/hs_guard/engine/slot_engine_v8.py:41,57): ring_pos[slot, (start + j) % window] = start + j for
  * j < min(lens[n], lb_max); column `window` is never written (it stays -1).
  */
 int hsg_ring_pos_update(int64_t* ring_pos, int64_t ring_rows, int32_t window, const int64_t* slots,

@@ -1,6 +1,6 @@
 """Whole streaming step on the CPU (test infrastructure only).
 
-``StreamOracle.tick`` restates ``SlotStreamEngineV8._forward`` (src/hs_guard/engine/slot_engine_v8.py:197-256)
+``StreamOracle.tick`` restates ``SlotStreamEngineV8._forward`` (src/hs_guard/engine/slot_engine_v8.py:30-89)
 in the reference's padded [n, lb] layout of ``pack_inputs`` (slot_engine_v7.py:7-25), with its per-slot
 pools (bucketed_engine.py:37-45, slot_engine.py:14-17): GDN layers run conv_silu_update -> gdn_slot_step
 -> gated RMSNorm -> out_proj; attention layers run q/k RMSNorm + RoPE -> ring attention with gate -> ring

@@ -5,7 +5,7 @@ Rounding points follow the reference's fused kernels (bf16 where they store bf16
 * ``conv_silu_update``  -- fused_kernels.py:94-136: causal depthwise conv (4 taps) over [pool(3 rows); new
   tokens], fp32 accumulate, round to bf16, SiLU, round to bf16; pool row i <- ext[len + i] when len > 0.
   Pinned against transformers' ``causal_conv1d_update`` (qwen3_5/modeling_qwen3_5.py:200-216).
-* ``add_rmsnorm``       -- add_square + rms_finish (fused_kernels.py:30-72, slot_engine_v8.py:209-222):
+* ``add_rmsnorm``       -- add_square + rms_finish (fused_kernels.py:30-72, slot_engine_v8.py:42-55):
   h = bf16(res + mix); out = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w)). Pinned against transformers'
   ``Qwen3_5RMSNorm`` (modeling_qwen3_5.py:720-737 of that file's class).
 * ``gated_rmsnorm``     -- gated_finish (fused_kernels.py:215-233): bf16(bf16(w * bf16(x * r)) * silu(z)),

@@ -4,7 +4,7 @@
   ``[ids nb*lb | lens nb | slots nb | starts nb]``, ids right-padded with 0, padded rows pointing at the
   scratch slot ``max_slots`` with start 0. Pinned by the reference's own known-answer vector
   (``tests/test_contract.py:14-18``), restated in ``tests/test_oracle_pack.py``.
-* ``ring_columns`` / ``ring_pos_update`` restate ``slot_engine_v8.py:208,224`` (``ring_col = pos % W`` for
+* ``ring_columns`` / ``ring_pos_update`` restate ``slot_engine_v8.py:41,57`` (``ring_col = pos % W`` for
   valid tokens, the scratch column ``W`` otherwise; after all layers ``ring_pos[slot, col] = pos`` or -1).
   Pinned by brute force against a dictionary model of the window in ``tests/test_oracle_pack.py``.
 * ``bucket`` restates ``bucketed_engine.py:12-16``.

@@ -9,11 +9,11 @@ keeping exactly the keys with ``kpos >= 0 and kpos <= qpos and kpos > qpos - W``
 ``ring_attention_v8`` adds the v8 epilogue of ``fused_kernels.py:341-355``: output rounded to bf16, times
 ``bf16(sigmoid(gate))`` (gate = second half of each q head's ``q_proj`` slice) rounded to bf16, written as
 ``[N, Lb, Hq*D]`` with q head ``h*G + g``; when ``write_ring`` (Lb == 1) and ``len > 0`` the new key/value go
-to ring column ``start % W``. ``ring_scatter`` is the Lb > 1 write of ``slot_engine_v8.py:253-255``
+to ring column ``start % W``. ``ring_scatter`` is the Lb > 1 write of ``slot_engine_v8.py:86-88``
 (column ``pos % W`` for valid steps, scratch column W otherwise).
 
 ``attend_blockwise`` restates the numerics of the reference's Triton kernels (fused_kernels.py:309-341,
-ring_attention_kernel.py:129-160): keys in blocks of 32 (the W ring columns in order, then the tick's new
+ring_attention_kernel.py:56-87): keys in blocks of 32 (the W ring columns in order, then the tick's new
 keys), a running max per query row, ``acc = acc * alpha + bf16(p) @ v`` and ``l = l * alpha + sum(p)`` with
 p in full precision in the sum; ``ring_attention_v8`` uses it. Without bf16 rounding (``oracle.bf16.exact``)
 it equals ``ring_attention_reference``.
@@ -130,7 +130,7 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
 
 
 def ring_scatter(ring_k, ring_v, new_k, new_v, slots, starts, lens, window):
-    """In-place scatter of slot_engine_v8.py:253-255 (new_k/new_v [N, Hkv, Lb, D])."""
+    """In-place scatter of slot_engine_v8.py:86-88 (new_k/new_v [N, Hkv, Lb, D])."""
     lb = new_k.shape[2]
     for n, s in enumerate(np.asarray(slots, dtype=np.int64)):
         for t in range(lb):

@@ -224,6 +224,30 @@ def test_step_packed_matches_step(setup):
     assert np.array_equal(ea.length, eb.length)
 
 
+def test_fused_conv_engine_equals_separate_conv():
+    """With one value head per key head the engine runs the GDN conv inside the slot step; over several ticks it
+    gives exactly the probabilities and pools of the engine that runs the conv as its own kernel."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    print("[engine] fused conv vs separate conv", flush=True)
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=2, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    model = GuardModel.random(cfg, seed=3, device="cuda:0")
+    ef = SlotStreamEngine(model, 4)
+    es = SlotStreamEngine(model, 4, fuse_conv=False)
+    assert ef.fuse_conv and not es.fuse_conv
+    rng = np.random.default_rng(9)
+    for t, tick in enumerate(_schedule(rng, cfg.vocab_size)):
+        a = ef.step(tick)
+        b = es.step(tick)
+        for role in a:
+            for x, y in zip(a[role], b[role]):
+                np.testing.assert_array_equal(x.numpy(), y.numpy(), err_msg=f"tick {t}")
+    for name in ("rec", "conv", "ring_k", "ring_v", "ring_pos"):
+        assert torch.equal(getattr(ef, name), getattr(es, name)), name
+
+
 def test_streaming_guard_api(setup):
     """Drop-in API: cut scores = 1 - p(safe) of the chosen role, reset clears every slot, snapshots restore."""
     from hs_guard.runtime import StreamingGuard, random_metadata

@@ -189,3 +189,71 @@ def test_packed_gated_long_rows_and_decay(case):
     lens = [64, 17, 1, 9, 0, 33, 8, 2]
     A_log = {"bursts": [0.0, -1.0], "fast_decay": [0.0, 3.0, -2.0, 3.0], "zero_decay": [6.0, 0.0, 3.0, 6.0]}[case]
     _check_packed_gated(lens, A_log, 1.0, seed=11, state_scale=0.05)
+
+
+@pytest.mark.parametrize("state_code", [0, 1])
+def test_conv_fused_step_equals_conv_then_step(state_code):
+    """hsg_gdn_conv_slot_step_gated (conv + SiLU inside the slot step) == hsg_conv_silu_update followed by
+    hsg_gdn_slot_step_gated, bit for bit on the gated outputs, the state and the conv history pool: rows of 0 to 64
+    tokens (one to eight 8-token bursts, rows shorter than the 3-token history), HV == H."""
+    from hs_guard._lib import lib
+    L = lib()
+    print(f"[gdn] conv fused, state code {state_code}", flush=True)
+    gen = torch.Generator().manual_seed(21)
+    H = HV = 4
+    K = 128
+    C = 3 * H * K
+    lens = torch.tensor([64, 17, 9, 8, 3, 2, 1, 0, 1, 33], dtype=torch.long)
+    N = len(lens)
+    offsets = torch.cumsum(lens, 0) - lens
+    T = int(lens.sum())
+    stride = C + HV * K + 2 * HV + 24          # raw projection row: qkv | z | b | a | pad
+    proj = torch.randn(T, stride, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(C, 4, generator=gen) * 0.5).to(torch.bfloat16)
+    S = N + 3
+    pool0 = torch.randn(S, 3, C, generator=gen).to(torch.bfloat16)
+    state0 = torch.randn(S, HV, K, K, generator=gen) * 0.05
+    if state_code == 1:
+        state0 = state0.half()
+    A_log = (torch.rand(HV, generator=gen) * 2 - 1).to(torch.bfloat16)
+    dt = torch.randn(HV, generator=gen).to(torch.bfloat16)
+    norm_w = (1 + 0.1 * torch.randn(K, generator=gen)).to(torch.bfloat16)
+    slots = torch.randperm(S, generator=gen)[:N]
+    dev = torch.device("cuda:0")
+    pd, wd, nwd = proj.to(dev), w.to(dev), norm_w.to(dev)
+    Ad, dtd = A_log.to(dev), dt.to(dev)
+    sl, ln, of = slots.to(dev), lens.to(dev), offsets.to(dev)
+    st = torch.cuda.current_stream().cuda_stream
+    base = pd.data_ptr()
+    a_ptr, b_ptr, z_ptr = base + 2 * (C + HV * K + HV), base + 2 * (C + HV * K), base + 2 * C
+    # separate kernels
+    pool_a, state_a = pool0.to(dev), state0.to(dev)
+    conv = torch.empty(T, C, dtype=torch.bfloat16, device=dev)
+    out_a = torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
+    assert L.hsg_conv_silu_update(base, stride, pool_a.data_ptr(), S, wd.data_ptr(), 4, sl.data_ptr(), ln.data_ptr(),
+                                  of.data_ptr(), N, 0, C, conv.data_ptr(), C, st) == 0
+    assert L.hsg_gdn_slot_step_gated(conv.data_ptr(), C, 0, H * K, 2 * H * K, a_ptr, b_ptr, stride, Ad.data_ptr(),
+                                     dtd.data_ptr(), state_a.data_ptr(), state_code, S, sl.data_ptr(), ln.data_ptr(),
+                                     of.data_ptr(), N, 0, H, HV, K, K, K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6,
+                                     out_a.data_ptr(), 0, 0, st) == 0
+    # fused
+    pool_b, state_b = pool0.to(dev), state0.to(dev)
+    out_b = torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
+    assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
+                                          a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
+                                          state_code, S, sl.data_ptr(), ln.data_ptr(), of.data_ptr(), N, H, HV, K, K,
+                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(state_a, state_b)
+    assert torch.equal(pool_a, pool_b)
+    assert torch.equal(pool_b[slots[lens == 0]], pool0[slots[lens == 0]].to(dev))   # untouched
+    # only packed rows and one value head per key head are accepted
+    assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
+                                          a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
+                                          state_code, S, sl.data_ptr(), ln.data_ptr(), None, N, H, HV, K, K,
+                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == -1
+    assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
+                                          a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
+                                          state_code, S, sl.data_ptr(), ln.data_ptr(), of.data_ptr(), N, H // 2, HV, K,
+                                          K, K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == -3
