@@ -18,6 +18,8 @@
 // launch instead of R (latency hidden across workgroups, not inside one).
 #include <math.h>
 
+#include <mutex>
+
 #include "hsg_common.h"
 
 namespace hsg {
@@ -451,4 +453,60 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   else hipLaunchKernelGGL(decode_values_kernel<16>, dim3(units * NS), dim3(256), 0, st, p);
   hipLaunchKernelGGL(decode_combine_kernel, dim3(units), dim3(256), 0, st, p);
   return launch_status();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Allocation-free variant: the split-K workspace is a static device array of the library, one copy per GPU,
+// held until the process ends. Host code never passes `scratch` itself to a kernel (on the host that name is a
+// stand-in, not a device address): the device address of each GPU's copy is looked up once per device with
+// hipGetSymbolAddress and kept in scratch_ptr[device].
+static __device__ __align__(256) unsigned char scratch[HSG_RING_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices] = {};
+
+// device address of the current device's scratch (looked up on the first call made on that device)
+int current_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return HSG_ERR_ARG;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return HSG_ERR_ARG;
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return HSG_OK;
+}
+}  // namespace
+
+extern "C" int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg,
+                                       void* ring_k, void* ring_v, int64_t ring_rows, int32_t window,
+                                       const void* new_k, int64_t nk_sn, int64_t nk_sl, int64_t nk_sh,
+                                       const void* new_v, int64_t nv_sn, int64_t nv_sl, int64_t nv_sh,
+                                       const void* gate, int64_t g_sn, int64_t g_sl, int64_t g_sh, int64_t g_sg,
+                                       int64_t g_off, const int64_t* ring_pos, const int64_t* slots,
+                                       const int64_t* starts, const int64_t* lens, const int64_t* offsets,
+                                       int32_t n_rows, int32_t hkv, int32_t groups, int32_t head_dim, float scale,
+                                       int32_t write_ring, void* out, int64_t o_sn, int64_t o_sl, int64_t o_sh,
+                                       int64_t o_sg, void* stream) {
+  if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
+  if (n_rows == 0) return HSG_OK;
+  if (hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) > (size_t)HSG_RING_DECODE_SCRATCH_BYTES)
+    return HSG_ERR_SHAPE;
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != HSG_OK) return rc;
+  // the kernels write every workspace word they read (scores of visible blocks, every block maximum, every
+  // split's partial sums), so nothing left by an earlier call is read and nothing needs clearing
+  return hsg_ring_decode(q, q_sn, q_sl, q_sh, q_sg, ring_k, ring_v, ring_rows, window, new_k, nk_sn, nk_sl, nk_sh,
+                         new_v, nv_sn, nv_sl, nv_sh, gate, g_sn, g_sl, g_sh, g_sg, g_off, ring_pos, slots, starts,
+                         lens, offsets, n_rows, hkv, groups, head_dim, scale, write_ring, out, o_sn, o_sl, o_sh,
+                         o_sg, ws, (size_t)HSG_RING_DECODE_SCRATCH_BYTES, stream);
 }

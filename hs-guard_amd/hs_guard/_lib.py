@@ -78,6 +78,15 @@ SIGNATURES = {
         _I32, _I32, _I32, _I32, _F, _I32,    # n_rows, hkv, groups, head_dim, scale, write_ring
         _P, _I64, _I64, _I64, _I64,          # out, o_sn, o_sl, o_sh, o_sg
         _P, ctypes.c_size_t, _P]),           # workspace, workspace_bytes, stream
+    "hsg_ring_decode_noalloc": (ctypes.c_int, [
+        _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
+        _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window
+        _P, _I64, _I64, _I64,                # new_k, nk_sn, nk_sl, nk_sh
+        _P, _I64, _I64, _I64,                # new_v, nv_sn, nv_sl, nv_sh
+        _P, _I64, _I64, _I64, _I64, _I64,    # gate, g_sn, g_sl, g_sh, g_sg, g_off
+        _P, _P, _P, _P, _P,                  # ring_pos, slots, starts, lens, offsets
+        _I32, _I32, _I32, _I32, _F, _I32,    # n_rows, hkv, groups, head_dim, scale, write_ring
+        _P, _I64, _I64, _I64, _I64, _P]),    # out, o_sn, o_sl, o_sh, o_sg, stream
     "hsg_embed_rmsnorm": (ctypes.c_int, [_P, _P, _I64, _P, _F, _P, _P, _I32, _I32, _P]),
     "hsg_add_rmsnorm": (ctypes.c_int, [_P, _P, _P, _F, _P, _I32, _I32, _P]),
     "hsg_conv_silu_update": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _P,

@@ -193,6 +193,27 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
                     int64_t o_sh, int64_t o_sg, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * hsg_ring_decode without the workspace argument: it allocates nothing. No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under hipGraph capture, allocation-free serving loops,
+ * harnesses that forbid hipMalloc). The split-K scratch is the library's own static device array of
+ * HSG_RING_DECODE_SCRATCH_BYTES, one copy per GPU, held until the process ends; its device address is looked up
+ * on the first call made on each device (make that first call outside graph capture). Arguments, outputs and
+ * numerics are those of hsg_ring_decode, bit for bit. Returns HSG_ERR_SHAPE when
+ * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 486 rows at 4 kv
+ * heads, G = 4, W = 512). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams,
+ * or two threads) race and must be serialised by the caller; nothing left by an earlier call is read.
+ */
+#define HSG_RING_DECODE_SCRATCH_BYTES (48u << 20)
+int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,
+                            void* ring_v, int64_t ring_rows, int32_t window, const void* new_k, int64_t nk_sn,
+                            int64_t nk_sl, int64_t nk_sh, const void* new_v, int64_t nv_sn, int64_t nv_sl,
+                            int64_t nv_sh, const void* gate, int64_t g_sn, int64_t g_sl, int64_t g_sh, int64_t g_sg,
+                            int64_t g_off, const int64_t* ring_pos, const int64_t* slots, const int64_t* starts,
+                            const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t hkv, int32_t groups,
+                            int32_t head_dim, float scale, int32_t write_ring, void* out, int64_t o_sn, int64_t o_sl,
+                            int64_t o_sh, int64_t o_sg, void* stream);
+
+/*
  * Embedding gather + RMSNorm of the first layer. Replaces embed_tokens + add_square(hidden) + rms_finish
  * (src/hs_guard/engine/slot_engine_v8.py:38,42-43; fused_kernels.py:30-72):
  *   hidden[t] = emb[ids[t]];  normed[t] = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1)

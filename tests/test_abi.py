@@ -62,6 +62,15 @@ def test_argument_errors_are_rejected_before_launch():
     assert L.hsg_ring_decode(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, 0,
                              0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0, None, 0,
                              None) == 0
+    # allocation-free decode: sizes beyond its 48 MiB scratch are rejected before any device call; 0 rows is a no-op
+    unit = L.hsg_ring_decode_workspace_bytes(1, 4, 4, 512)
+    rows = (48 << 20) // unit + 1
+    assert L.hsg_ring_decode_noalloc(16, 0, 256, 0, 0, 16, 16, rows + 1, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0,
+                                     0, 0, 0, 0, 8, 8, 8, 8, None, rows, 4, 4, 256, 1.0, 1, 16, 0, 0, 0, 0,
+                                     None) == -3
+    assert L.hsg_ring_decode_noalloc(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0,
+                                     0, 0, 0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0,
+                                     None) == 0
     # chunk prefill: workspace size is rows x ceil(L / 64) x HV units plus the row order (4 bytes per row in
     # 256-byte blocks); a too-small or unaligned workspace and L <= 0 are rejected
     unit = L.hsg_gdn_chunk_workspace_bytes(1, 64, 1) - 256

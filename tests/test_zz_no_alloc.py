@@ -1,0 +1,85 @@
+"""Allocation-free split-K decode: hsg_ring_decode_noalloc (scratch in the library's static device array)
+against hsg_ring_decode with a caller-allocated workspace, through the C ABI.
+
+Both entry points run the same kernels on the same inputs, so outputs and ring writes must be bitwise equal.
+Two calls in a row on one GPU, the second with fewer rows, check that the second call reads nothing the first
+left in the shared scratch.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+HKV, G, D, W = 4, 4, 256, 512
+
+
+def _case(seed, n, slots_total):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(n, HKV, G, D, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(slots_total, HKV, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(slots_total, HKV, W + 1, D, generator=gen).to(torch.bfloat16)
+    new_k = torch.randn(n, HKV, 1, D, generator=gen).to(torch.bfloat16)
+    value = torch.randn(n, 1, HKV * D, generator=gen).to(torch.bfloat16)
+    gate = torch.randn(n, 1, HKV * G * 2 * D, generator=gen).to(torch.bfloat16)
+    slots = torch.randperm(slots_total - 1, generator=gen)[:n]
+    starts = torch.randint(0, 3 * W, (n,), generator=gen)
+    fills = torch.randint(0, W + 1, (n,), generator=gen)
+    lens = (torch.rand(n, generator=gen) > 0.1).long()          # about one row in ten has no step
+    ring_pos = torch.full((slots_total, W + 1), -1, dtype=torch.long)
+    for s, st, f in zip(slots.tolist(), starts.tolist(), fills.tolist()):
+        for p in range(max(0, st - f), st):
+            ring_pos[s, p % W] = p
+    return dict(q=q, ring_k=ring_k, ring_v=ring_v, new_k=new_k, value=value, gate=gate, slots=slots,
+                starts=starts, lens=lens, ring_pos=ring_pos)
+
+
+def _call(inp, noalloc):
+    from hs_guard._lib import lib
+    L = lib()
+    dev = torch.device("cuda:0")
+    d = {k: v.to(dev) for k, v in inp.items()}
+    n = d["q"].shape[0]
+    out = torch.full((n, 1, HKV * G * D), 7.0, dtype=torch.bfloat16, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    args = (d["q"].data_ptr(), HKV * G * D, D, G * D, D,
+            d["ring_k"].data_ptr(), d["ring_v"].data_ptr(), d["ring_k"].shape[0], W,
+            d["new_k"].data_ptr(), HKV * D, D, D,
+            d["value"].data_ptr(), HKV * D, HKV * D, D,
+            d["gate"].data_ptr(), HKV * G * 2 * D, HKV * G * 2 * D, G * 2 * D, 2 * D, D,
+            d["ring_pos"].data_ptr(), d["slots"].data_ptr(), d["starts"].data_ptr(), d["lens"].data_ptr(), None,
+            n, HKV, G, D, D ** -0.5, 1,
+            out.data_ptr(), HKV * G * D, HKV * G * D, G * D, D)
+    if noalloc:
+        rc = L.hsg_ring_decode_noalloc(*args, st)
+    else:
+        ws = torch.empty(L.hsg_ring_decode_workspace_bytes(n, HKV, G, W), dtype=torch.uint8, device=dev)
+        rc = L.hsg_ring_decode(*args, ws.data_ptr(), ws.numel(), st)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return out.cpu(), d["ring_k"].cpu(), d["ring_v"].cpu()
+
+
+def test_noalloc_equals_workspace_entry_point():
+    for seed, n, slots_total in ((0, 352, 360), (1, 24, 40)):
+        print(f"[noalloc] seed {seed}: {n} rows, then the workspace entry point", flush=True)
+        inp = _case(seed, n, slots_total)
+        a = _call(inp, noalloc=True)
+        b = _call(inp, noalloc=False)
+        for x, y, what in zip(a, b, ("out", "ring_k", "ring_v")):
+            assert torch.equal(x, y), f"{what} differs at {n} rows"
+        assert not torch.equal(a[1], inp["ring_k"])      # the step's keys were written
+        live = inp["lens"].numpy() == 1
+        assert np.all(a[0][~live].float().numpy() == 0)  # rows without a step get zeros (padded layout)
+
+
+def test_noalloc_rejects_sizes_beyond_the_scratch():
+    from hs_guard._lib import lib
+    L = lib()
+    cap = 48 << 20
+    unit = L.hsg_ring_decode_workspace_bytes(1, HKV, G, W)
+    rows = cap // unit + 1   # unit: one row with all its kv heads
+    assert L.hsg_ring_decode_workspace_bytes(rows, HKV, G, W) > cap
+    rc = L.hsg_ring_decode_noalloc(16, 0, 256, 0, 0, 16, 16, rows + 1, W, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0,
+                                   0, 0, 0, 8, 8, 8, 8, None, rows, HKV, G, D, 1.0, 1, 16, 0, 0, 0, 0, None)
+    assert rc == -3
