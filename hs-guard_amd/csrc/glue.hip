@@ -246,37 +246,52 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64
 // [role*512, role*512+512) of the fused projection), LayerNorm(512) in fp32, SiLU, round to bf16, Linear
 // 512->3 with bf16 output, softmax in fp32. One wave per (token, role).
 // ---------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void risk_head_kernel(const uint16_t* y, int64_t y_stride, const uint16_t* ln_w,
-                                                        const uint16_t* ln_b, const uint16_t* w2,
-                                                        const uint16_t* b2, float eps, int roles, int width,
-                                                        float* probs, int tokens) {
+// One wave per (role, token). F32 = false: the streaming readout under autocast (slot_engine_v7.py:58-61): y is
+// the bf16 output of the first Linear, LayerNorm in fp32 with fp32 parameters, SiLU rounded to bf16 (the input
+// of the bf16 Linear), bf16 weights, bf16 logits. F32 = true: the complete-message readout (runtime.py:70-73),
+// every operand and intermediate in fp32 and nothing rounded to bf16.
+template <bool F32>
+__global__ __launch_bounds__(256) void risk_head_kernel(const void* y_, int64_t y_stride, const float* ln_w,
+                                                        const float* ln_b, const void* w2_, const void* b2_,
+                                                        float eps, int roles, int width, float* probs, int tokens) {
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= tokens * roles) return;
   const int role = item / tokens;
   const int tok = item - role * tokens;
-  const int per_lane = width / 64;  // 8 for width 512
-  const int d0 = lane * per_lane;
-  float v[8];
-  load8_bf16(y + tok * y_stride + role * width + d0, v);
+  constexpr int PL = 8;  // values per lane (width 512)
+  const int d0 = lane * PL;
+  float v[PL];
+  if constexpr (F32) {
+    const float* y = static_cast<const float*>(y_) + tok * y_stride + role * width + d0;
+    for (int i = 0; i < PL; ++i) v[i] = y[i];
+  } else {
+    load8_bf16(static_cast<const uint16_t*>(y_) + tok * y_stride + role * width + d0, v);
+  }
   float s = 0.f;
-  for (int i = 0; i < per_lane; ++i) s += v[i];
+  for (int i = 0; i < PL; ++i) s += v[i];
   const float mean = wave_sum(s) / (float)width;
   float s2 = 0.f;
-  for (int i = 0; i < per_lane; ++i) s2 += (v[i] - mean) * (v[i] - mean);
+  for (int i = 0; i < PL; ++i) s2 += (v[i] - mean) * (v[i] - mean);
   const float rstd = rsqrtf(wave_sum(s2) / (float)width + eps);
-  float lw[8], lb[8];
-  load8_bf16(ln_w + role * width + d0, lw);
-  load8_bf16(ln_b + role * width + d0, lb);
-  float a[8];
-  for (int i = 0; i < per_lane; ++i) a[i] = rbf(siluf_((v[i] - mean) * rstd * lw[i] + lb[i]));
+  float a[PL];
+  for (int i = 0; i < PL; ++i) {
+    const float t = siluf_((v[i] - mean) * rstd * ln_w[role * width + d0 + i] + ln_b[role * width + d0 + i]);
+    a[i] = F32 ? t : rbf(t);
+  }
   float logit[3];
   for (int j = 0; j < 3; ++j) {
-    float w[8];
-    load8_bf16(w2 + ((int64_t)role * 3 + j) * width + d0, w);
+    float w[PL];
+    if constexpr (F32) {
+      const float* wp = static_cast<const float*>(w2_) + ((int64_t)role * 3 + j) * width + d0;
+      for (int i = 0; i < PL; ++i) w[i] = wp[i];
+    } else {
+      load8_bf16(static_cast<const uint16_t*>(w2_) + ((int64_t)role * 3 + j) * width + d0, w);
+    }
     float acc = 0.f;
-    for (int i = 0; i < per_lane; ++i) acc += a[i] * w[i];
-    logit[j] = rbf(wave_sum(acc) + bf2f(b2[role * 3 + j]));
+    for (int i = 0; i < PL; ++i) acc += a[i] * w[i];
+    if constexpr (F32) logit[j] = wave_sum(acc) + static_cast<const float*>(b2_)[role * 3 + j];
+    else logit[j] = rbf(wave_sum(acc) + bf2f(static_cast<const uint16_t*>(b2_)[role * 3 + j]));
   }
   if (lane == 0) {
     const float m = fmaxf(logit[0], fmaxf(logit[1], logit[2]));
@@ -415,20 +430,34 @@ extern "C" int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t wid
   return launch_status();
 }
 
-extern "C" int hsg_risk_head(const void* y, int64_t y_stride, const void* ln_w, const void* ln_b, const void* w2,
+extern "C" int hsg_risk_head(const void* y, int64_t y_stride, const float* ln_w, const float* ln_b, const void* w2,
                              const void* b2, float eps, int32_t roles, int32_t width, float* probs, int32_t tokens,
                              void* stream) {
   if (tokens < 0 || roles <= 0) return HSG_ERR_ARG;
   if (width != 512) return HSG_ERR_SHAPE;
   if (tokens == 0) return HSG_OK;
   if (!y || !ln_w || !ln_b || !w2 || !b2 || !probs) return HSG_ERR_ARG;
-  if (y_stride % 8 || !aligned(y, 16) || !aligned(ln_w, 16) || !aligned(ln_b, 16) || !aligned(w2, 16))
+  if (y_stride % 8 || !aligned(y, 16) || !aligned(ln_w, 4) || !aligned(ln_b, 4) || !aligned(w2, 16))
     return HSG_ERR_ALIGN;
   const int items = tokens * roles;
-  hipLaunchKernelGGL(risk_head_kernel, dim3((items + 3) / 4), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(y), y_stride, static_cast<const uint16_t*>(ln_w),
-                     static_cast<const uint16_t*>(ln_b), static_cast<const uint16_t*>(w2),
-                     static_cast<const uint16_t*>(b2), eps, roles, width, probs, tokens);
+  hipLaunchKernelGGL(risk_head_kernel<false>, dim3((items + 3) / 4), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), y, y_stride, ln_w, ln_b, w2, b2, eps, roles, width, probs,
+                     tokens);
+  return launch_status();
+}
+
+extern "C" int hsg_risk_head_f32(const float* y, int64_t y_stride, const float* ln_w, const float* ln_b,
+                                 const float* w2, const float* b2, float eps, int32_t roles, int32_t width,
+                                 float* probs, int32_t tokens, void* stream) {
+  if (tokens < 0 || roles <= 0) return HSG_ERR_ARG;
+  if (width != 512) return HSG_ERR_SHAPE;
+  if (tokens == 0) return HSG_OK;
+  if (!y || !ln_w || !ln_b || !w2 || !b2 || !probs) return HSG_ERR_ARG;
+  if (!aligned(y, 4) || !aligned(ln_w, 4) || !aligned(ln_b, 4) || !aligned(w2, 4)) return HSG_ERR_ALIGN;
+  const int items = tokens * roles;
+  hipLaunchKernelGGL(risk_head_kernel<true>, dim3((items + 3) / 4), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), y, y_stride, ln_w, ln_b, w2, b2, eps, roles, width, probs,
+                     tokens);
   return launch_status();
 }
 

@@ -97,6 +97,7 @@ SIGNATURES = {
                                      _P, _P, _I32, _I32, _I32, _P]),
     "hsg_silu_mul": (ctypes.c_int, [_P, _I64, _I32, _P, _I32, _P]),
     "hsg_risk_head": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
+    "hsg_risk_head_f32": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
     "hsg_ring_pos_update": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I32, _P]),
 }
 

@@ -120,6 +120,16 @@ class PreparedWeights:
     gate|up, both heads' first Linear), RMSNorm gains as fp32 1 + w, rotary inverse frequencies. Needs
     ``model``, ``cfg``, ``kind``, ``roles`` and ``device`` set."""
 
+    @classmethod
+    def of(cls, model, roles=ROLES):
+        """The prepared weights of ``model`` alone (no pools, no kernels), on the model's device."""
+        self = cls.__new__(cls)
+        self.model, self.cfg, self.roles, self.device = model, model.config, tuple(roles), model.device
+        types = list(self.cfg.layer_types)
+        self.kind = [(t, sum(1 for u in types[:i] if u == t)) for i, t in enumerate(types)]
+        self._prepare_weights()
+        return self
+
     def _prepare_weights(self):
         m, cfg = self.model, self.cfg
         f32 = torch.float32
@@ -153,12 +163,15 @@ class PreparedWeights:
         self.emb = m["backbone.embed_tokens.weight"].contiguous()
         rot = cfg.rotary_dim
         self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=f32) / rot))).to(self.device)
-        self.head_w1 = torch.cat([m[f"heads.{r}.projection.0.weight"] for r in self.roles]).contiguous()
-        self.head_b1 = torch.cat([m[f"heads.{r}.projection.0.bias"] for r in self.roles]).contiguous()
-        self.head_ln_w = torch.stack([m[f"heads.{r}.projection.1.weight"] for r in self.roles]).contiguous()
-        self.head_ln_b = torch.stack([m[f"heads.{r}.projection.1.bias"] for r in self.roles]).contiguous()
-        self.head_w2 = torch.stack([m[f"heads.{r}.risk.weight"] for r in self.roles]).contiguous()
-        self.head_b2 = torch.stack([m[f"heads.{r}.risk.bias"] for r in self.roles]).contiguous()
+        # streaming readout (slot_engine_v7.py:44-61): both Linears' weights and biases cast to bf16, the
+        # LayerNorm in float32
+        bf16 = torch.bfloat16
+        self.head_w1 = torch.cat([m[f"heads.{r}.projection.0.weight"] for r in self.roles]).to(bf16).contiguous()
+        self.head_b1 = torch.cat([m[f"heads.{r}.projection.0.bias"] for r in self.roles]).to(bf16).contiguous()
+        self.head_ln_w = torch.stack([m[f"heads.{r}.projection.1.weight"] for r in self.roles]).float().contiguous()
+        self.head_ln_b = torch.stack([m[f"heads.{r}.projection.1.bias"] for r in self.roles]).float().contiguous()
+        self.head_w2 = torch.stack([m[f"heads.{r}.risk.weight"] for r in self.roles]).to(bf16).contiguous()
+        self.head_b2 = torch.stack([m[f"heads.{r}.risk.bias"] for r in self.roles]).to(bf16).contiguous()
 
 
 class SlotStreamEngine(PreparedWeights):

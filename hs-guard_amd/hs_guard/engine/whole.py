@@ -9,6 +9,9 @@ roles' risk heads (runtime.py:71-74).
   WY/UT chunk form on MFMA) -> ``hsg_gated_rmsnorm`` -> out_proj.
 * Attention layers: fused q|k|v GEMM -> q/k RMSNorm + RoPE at positions 0 .. T-1 -> window attention ->
   sigmoid(gate) -> o_proj.
+* Risk heads in float32, as the reference's readout on ``hidden.float()`` outside autocast (runtime.py:70-73,
+  141): an fp32 GEMM with the heads' fp32 weights, then ``hsg_risk_head_f32`` (LayerNorm, SiLU, logits and
+  softmax, nothing rounded to bf16).
 * The sequence is cut into 64-token segments for the conv and the attention. Segment s is given, as its conv
   history, the 3 tokens before it and, as its "ring", the keys and values of the W positions before it
   (positions [64 s - W, 64 s) at columns p mod W, ring_pos = p, or -1 before the sequence start), gathered on
@@ -33,6 +36,19 @@ SEG = 64                  # tokens per conv / attention segment (the tiled ring 
 MAX_ATT_SEGMENTS = 128    # segments per attention launch: bounds the gathered rings to ~270 MB at W = 512
 
 
+def fp32_heads(model, roles=ROLES):
+    """Both roles' risk heads for the complete-message readout, float32 and unrounded (runtime.py:70-73): the first
+    Linear fused over the roles (w1 [roles*E, hidden], b1), the LayerNorm (ln_w, ln_b [roles, E]) and the risk
+    Linear (w2 [roles, 3, E], b2 [roles, 3])."""
+    m, f32 = model, torch.float32
+    return {"w1": torch.cat([m[f"heads.{r}.projection.0.weight"] for r in roles]).to(f32).contiguous(),
+            "b1": torch.cat([m[f"heads.{r}.projection.0.bias"] for r in roles]).to(f32).contiguous(),
+            "ln_w": torch.stack([m[f"heads.{r}.projection.1.weight"] for r in roles]).to(f32).contiguous(),
+            "ln_b": torch.stack([m[f"heads.{r}.projection.1.bias"] for r in roles]).to(f32).contiguous(),
+            "w2": torch.stack([m[f"heads.{r}.risk.weight"] for r in roles]).to(f32).contiguous(),
+            "b2": torch.stack([m[f"heads.{r}.risk.bias"] for r in roles]).to(f32).contiguous()}
+
+
 class WholeSequenceScorer(PreparedWeights):
     """Scores whole token sequences with the kernels of libhsg.so. ``shared``: a SlotStreamEngine (or another
     scorer) whose prepared weights are reused instead of building a second copy."""
@@ -51,6 +67,7 @@ class WholeSequenceScorer(PreparedWeights):
                 setattr(self, name, getattr(shared, name))
         else:
             self._prepare_weights()
+        self.head32 = fp32_heads(model, self.roles)
 
     @torch.inference_mode()
     def forward(self, ids):
@@ -167,9 +184,10 @@ class WholeSequenceScorer(PreparedWeights):
             check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), nxt.data_ptr(), eps, normed.data_ptr(), T, H,
                                     st), "hsg_add_rmsnorm")
         R, E = len(self.roles), cfg.head_hidden
-        y = torch.addmm(self.head_b1, normed, self.head_w1.t())
+        h32 = self.head32
+        y = torch.addmm(h32["b1"], normed.float(), h32["w1"].t())
         probs = torch.empty(R, T, 3, dtype=torch.float32, device=dev)
-        check(L.hsg_risk_head(y.data_ptr(), R * E, self.head_ln_w.data_ptr(), self.head_ln_b.data_ptr(),
-                              self.head_w2.data_ptr(), self.head_b2.data_ptr(), cfg.layer_norm_eps, R, E,
-                              probs.data_ptr(), T, st), "hsg_risk_head")
+        check(L.hsg_risk_head_f32(y.data_ptr(), R * E, h32["ln_w"].data_ptr(), h32["ln_b"].data_ptr(),
+                                  h32["w2"].data_ptr(), h32["b2"].data_ptr(), cfg.layer_norm_eps, R, E,
+                                  probs.data_ptr(), T, st), "hsg_risk_head_f32")
         return probs

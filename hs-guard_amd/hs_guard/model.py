@@ -135,6 +135,15 @@ class GuardConfig:
 _UNIT_GAINS = ("linear_attn.norm.weight", "projection.1.weight")
 
 
+def head_dtype(name):
+    """Storage dtype of a parameter. The classifier heads stay float32, as the reference keeps them: its
+    backbone parameters are cast to bf16 and its heads are float32 modules the checkpoint is loaded into
+    (src/hs_guard/runtime.py:108-113); the streaming readout casts the Linear weights to bf16 but applies the
+    float32 LayerNorm (slot_engine_v7.py:44-61), and the complete-message readout runs entirely in float32
+    (runtime.py:70-73,141). Everything else is bf16."""
+    return torch.float32 if name.startswith("heads.") else torch.bfloat16
+
+
 class _Backbone:
     def __init__(self, config):
         self.config = config
@@ -158,7 +167,8 @@ class GuardModel:
     @classmethod
     def random(cls, config: GuardConfig = None, seed: int = 0, device="cuda", std=0.02, gen_device="cpu"):
         """Seeded random init, drawn in sorted-name order on ``gen_device`` (the CPU by default, so every
-        device gets identical bytes) then moved to ``device``."""
+        device gets identical bytes) then moved to ``device``. Every value is rounded to bf16 (the heads are
+        stored as float32 holding those values)."""
         config = config or GuardConfig.baseline()
         gen = torch.Generator(device=gen_device).manual_seed(seed)
         weights = {}
@@ -166,7 +176,7 @@ class GuardModel:
             t = torch.randn(*shape, generator=gen, device=gen_device) * std
             if name.endswith(_UNIT_GAINS):
                 t = t + 1.0
-            weights[name] = t.to(torch.bfloat16).to(device)
+            weights[name] = t.to(torch.bfloat16).to(head_dtype(name)).to(device)
         return cls(config, weights)
 
     @classmethod
@@ -175,7 +185,8 @@ class GuardModel:
         strict=True): every backbone and head tensor this build uses must be present with its shape, and any
         other key must be one of the checkpoint's classifier tensors this build does not use (category and
         general heads). head="general" reads the general projection and risk layers in place of the red-line
-        ones (runtime.py:119-121). Tensors are stored as bf16 on ``device``."""
+        ones (runtime.py:119-121). Backbone tensors are stored as bf16 and head tensors as float32 (head_dtype)
+        on ``device``."""
         shapes = config.parameter_shapes()
         known_extra = ("category.", "general_projection.", "general.", "general_category.")
         unexpected = [k for k in state if k not in shapes and
@@ -192,7 +203,7 @@ class GuardModel:
             t = state[src]
             if tuple(t.shape) != tuple(shape):
                 raise ValueError(f"Shape mismatch for {src}: {tuple(t.shape)} != {tuple(shape)}")
-            weights[name] = t.to(torch.bfloat16).to(device).contiguous()
+            weights[name] = t.to(head_dtype(name)).to(device).contiguous()
         return cls(config, weights)
 
     def to(self, device):

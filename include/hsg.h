@@ -279,15 +279,25 @@ int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t width, void* o
                  void* stream);
 
 /*
- * Risk heads after the fused first projection. Replaces _risk + softmax
- * (src/hs_guard/engine/slot_engine_v7.py:58-61; slot_engine_v8.py:56; src/hs_guard/runtime.py:61-74):
+ * Risk heads after the fused first projection, as the streaming engine reads them out under autocast. Replaces
+ * _risk + softmax (src/hs_guard/engine/slot_engine_v7.py:44-61; slot_engine_v8.py:56; src/hs_guard/runtime.py:61-74):
  *   for role r: v = y[t, r*width : (r+1)*width] (bf16 Linear output incl. bias), LayerNorm(eps) in fp32
- *   with ln_w/ln_b [roles, width], SiLU, bf16, Linear to 3 with w2 [roles, 3, width], b2 [roles, 3],
+ *   with fp32 ln_w/ln_b [roles, width], SiLU, bf16, Linear to 3 with bf16 w2 [roles, 3, width], b2 [roles, 3],
  *   bf16 logits, softmax -> probs [roles, tokens, 3] fp32. Supported: width == 512.
  */
-int hsg_risk_head(const void* y, int64_t y_stride, const void* ln_w, const void* ln_b, const void* w2,
+int hsg_risk_head(const void* y, int64_t y_stride, const float* ln_w, const float* ln_b, const void* w2,
                   const void* b2, float eps, int32_t roles, int32_t width, float* probs, int32_t tokens,
                   void* stream);
+
+/*
+ * The same heads read out entirely in fp32, as the complete-message scorer does: Classifier.readout on
+ * hidden.float() outside autocast, then softmax (src/hs_guard/runtime.py:70-73,141). y [tokens, y_stride] is the
+ * fp32 output of the first Linear (fp32 weights, incl. bias); ln_w, ln_b [roles, width], w2 [roles, 3, width],
+ * b2 [roles, 3] fp32; nothing is rounded to bf16. Supported: width == 512.
+ */
+int hsg_risk_head_f32(const float* y, int64_t y_stride, const float* ln_w, const float* ln_b, const float* w2,
+                      const float* b2, float eps, int32_t roles, int32_t width, float* probs, int32_t tokens,
+                      void* stream);
 
 /*
  * Ring position bookkeeping after all layers. Replaces ring_pos[slots, ring_col] = where(valid, pos, -1)

@@ -30,8 +30,13 @@ ROLES = ("user", "assistant")
 
 
 class StreamOracle:
-    def __init__(self, weights, cfg, max_slots, roles=ROLES):
-        """weights: name -> float32 numpy array of the bf16 weights (reference parameter names)."""
+    def __init__(self, weights, cfg, max_slots, roles=ROLES, gdn="recurrent"):
+        """weights: name -> float32 numpy array of the bf16 weights (reference parameter names). gdn: "recurrent"
+        (``gdn_slot_step``, token by token) or "chunk" (``gdn_slot_step_chunked`` for ticks of more than one
+        step: the same float64 recurrence in the chunk form, for full-geometry ticks of long rows)."""
+        if gdn not in ("recurrent", "chunk"):
+            raise ValueError("gdn must be 'recurrent' or 'chunk'")
+        self.gdn = gdn
         self.w = weights
         self._fused = {}
         self.cfg = cfg
@@ -52,8 +57,18 @@ class StreamOracle:
         rot = cfg.rotary_dim
         self.inv_freq = oglue.inv_freq(rot, cfg.rope_theta)
 
-    def reset(self):
-        self.__init__(self.w, self.cfg, self.max_slots, self.roles)
+    def reset(self, slots=None):
+        """Zero every slot (the reference's reset, bucketed_engine.py:51-55) or only ``slots``."""
+        if slots is None:
+            self.__init__(self.w, self.cfg, self.max_slots, self.roles, self.gdn)
+            return
+        idx = np.asarray(list(slots), dtype=np.int64)
+        self.rec[:, idx] = 0
+        self.conv[:, idx] = 0
+        self.ring_k[:, idx] = 0
+        self.ring_v[:, idx] = 0
+        self.ring_pos[idx] = -1
+        self.length[idx] = 0
 
     def _cat(self, prefix, names):
         key = (prefix,) + tuple(names)
@@ -94,8 +109,9 @@ class StreamOracle:
                 bb, aa = proj[..., C + VD:C + VD + HV], proj[..., C + VD + HV:C + VD + 2 * HV]
                 conv_out, self.conv[idx] = oglue.conv_silu_update(qkv, self.conv[idx], w[a + "conv1d.weight"],
                                                                   slots, lens)
-                o, _, self.rec[idx] = ogdn.gdn_slot_step(conv_out, cfg.key_dim, H, K, HV, V, aa, bb, w[a + "A_log"],
-                                                         w[a + "dt_bias"], self.rec[idx], slots, lens)
+                step = ogdn.gdn_slot_step_chunked if self.gdn == "chunk" and lb > 1 else ogdn.gdn_slot_step
+                o, _, self.rec[idx] = step(conv_out, cfg.key_dim, H, K, HV, V, aa, bb, w[a + "A_log"],
+                                           w[a + "dt_bias"], self.rec[idx], slots, lens)
                 gated = oglue.gated_rmsnorm(bf16(o), z.reshape(n, lb, HV, V), w[a + "norm.weight"], eps)
                 mix = gemm(gated.reshape(n, lb, HV * V), w[a + "out_proj.weight"], None, lens)
             else:

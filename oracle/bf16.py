@@ -8,6 +8,7 @@ import contextlib
 import numpy as np
 
 _ROUND = [True]
+_FLIP_ULPS = [0]
 
 
 @contextlib.contextmanager
@@ -21,14 +22,39 @@ def exact():
         _ROUND[0] = True
 
 
+@contextlib.contextmanager
+def perturbed(ulps):
+    """Within this context ``bf16`` rounds every value that lies within ``ulps`` fp32 ulps of a bf16 rounding tie
+    to the other of its two bf16 neighbours. An evaluation of the same formulas in fp32 (as any GPU kernel, the
+    reference's Triton kernels included, computes them) carries errors of a few fp32 ulps, so it may round
+    exactly these values either way: the oracle run perturbed and unperturbed brackets how far two equally
+    valid fp32 implementations can drift apart, which is the noise floor an end-to-end comparison must be read
+    against. About (2 ulps + 1) / 65536 of all roundings change."""
+    previous = _FLIP_ULPS[0]
+    _FLIP_ULPS[0] = int(ulps)
+    try:
+        yield
+    finally:
+        _FLIP_ULPS[0] = previous
+
+
 def bf16(x):
     """Round to the nearest bf16 value (ties to even); returns float32 values."""
     if not _ROUND[0]:
         return np.asarray(x, dtype=np.float64)
     x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = x.view(np.uint32).astype(np.uint64)
-    r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32)
-    out = r.view(np.float32).copy()
+    u = x.view(np.uint32)
+    # uint32 arithmetic: finite values and infinities cannot carry past bit 31; NaNs are restored below
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    if _FLIP_ULPS[0]:
+        # within _FLIP_ULPS of the tie (low half 0x8000): take the other neighbour (truncation or the next value
+        # up in magnitude, whichever round-to-nearest-even did not pick)
+        low = (u & np.uint32(0xFFFF)).astype(np.int64)
+        near = (np.abs(low - 0x8000) <= _FLIP_ULPS[0]) & np.isfinite(x)
+        if near.any():
+            down = u & np.uint32(0xFFFF0000)
+            r = np.where(near, np.where(r == down, down + np.uint32(0x10000), down), r)
+    out = r.view(np.float32)
     nan = np.isnan(x)
     if nan.any():
         out[nan] = np.nan

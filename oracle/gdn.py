@@ -15,7 +15,8 @@ Rows with ``lens == 0`` neither read nor write the state (:154, :194); padded po
 ``gdn_chunk`` is the WY/UT chunk form of the same recurrence (the algorithm behind FLA's
 ``chunk_gated_delta_rule``, called at ``runtime.py:80-89`` / ``bucketed_engine.py:109-111``; FLA 0.5.2 is
 not vendored). It restates the published chunk algorithm, as also written out in transformers'
-``torch_chunk_gated_delta_rule`` (qwen3_5/modeling_qwen3_5.py:249-327).
+``torch_chunk_gated_delta_rule`` (qwen3_5/modeling_qwen3_5.py:249-327). ``gdn_slot_step_chunked`` is
+``gdn_slot_step`` evaluated through ``gdn_chunk``.
 
 Pinning (``tests/test_oracle_gdn.py``): transformers' ``torch_recurrent_gated_delta_rule`` and
 ``torch_chunk_gated_delta_rule`` (library routines); closed forms (beta=0 pure decay; zero state and one
@@ -150,3 +151,31 @@ def gdn_chunk(q, k, v, g, beta, S0, chunk=64, scale=None, normalize=True):
         Kd = np.ascontiguousarray((Kc * np.exp(G[:, -1:] - G)[:, :, None]).transpose(0, 2, 1))
         S = np.exp(G[:, -1])[:, None, None] * S + Kd @ Vn
     return out, S
+
+
+def gdn_slot_step_chunked(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log, dt_bias, state, slots,
+                          lens, scale=None, chunk=64):
+    """``gdn_slot_step`` (same arguments and returns) evaluated per live row in the chunk form ``gdn_chunk``.
+
+    Both are float64 evaluations of one recurrence (fused_kernels.py:166-188), so they agree to float64
+    rounding (``tests/test_oracle_gdn.py`` holds them to 1e-10); the chunk form replaces the per-token state
+    updates of a long row by a few matrix products per 64 tokens, which is what makes full-geometry ticks of
+    many-token rows affordable on the CPU."""
+    packed = np.asarray(packed, dtype=np.float64)
+    N, L, _ = packed.shape
+    H, K, HV, V = heads, head_k, value_heads, head_v
+    scale = K ** -0.5 if scale is None else scale
+    st = np.array(state, dtype=np.float64, copy=True)
+    slots = np.asarray(slots, dtype=np.int64)
+    lens = np.asarray(lens, dtype=np.int64)
+    o = np.zeros((N, L, HV, V))
+    kh = np.arange(HV) // (HV // H)
+    g_all, beta_all = gates(a, b, A_log, dt_bias)
+    for n in np.nonzero(lens > 0)[0]:
+        T = int(lens[n])
+        q = packed[n, :T, :key_dim].reshape(T, H, K)[:, kh]
+        k = packed[n, :T, key_dim:2 * key_dim].reshape(T, H, K)[:, kh]
+        v = packed[n, :T, 2 * key_dim:2 * key_dim + HV * V].reshape(T, HV, V)
+        o[n, :T], st[slots[n]] = gdn_chunk(q, k, v, g_all[n, :T], beta_all[n, :T], st[slots[n]], chunk=chunk,
+                                           scale=scale)
+    return o, bf16(o).astype(np.float64) ** 2, st

@@ -19,6 +19,8 @@ Rounding points follow the reference's fused kernels (bf16 where they store bf16
 * ``risk_probs``        -- Classifier.readout risk path (runtime.py:61-74, slot_engine_v7.py:58-61):
   Linear(bf16) -> LayerNorm (fp32) -> SiLU -> Linear (bf16 in/out) -> softmax fp32. Pinned against
   torch.nn.functional on CPU.
+* ``risk_probs_f32``    -- the complete-message readout (runtime.py:70-73,141): the same layers on
+  ``hidden.float()`` outside autocast, nothing rounded to bf16. Pinned against torch.nn.functional in float64.
 """
 import numpy as np
 
@@ -48,9 +50,11 @@ def conv_silu_update(qkv, pool, weight, slots, lens):
     for n in range(N):
         s = int(slots[n])
         ext = np.concatenate([np.asarray(pool, dtype=np.float64)[s], qkv[n]], 0)   # [keep + L, C]
-        for t in range(L):
-            acc = (ext[t:t + ks] * w.T).sum(0).astype(np.float32)
-            out[n, t] = bf16(silu(bf16(acc)))
+        # out[t] = sum_i ext[t + i] * w[:, i], taps summed in order, for every t at once
+        acc = ext[0:L] * w[:, 0]
+        for i in range(1, ks):
+            acc = acc + ext[i:i + L] * w[:, i]
+        out[n] = bf16(silu(bf16(acc.astype(np.float32))))
         if lens[n] > 0:
             pool2[s] = ext[int(lens[n]):int(lens[n]) + keep]
     return out, pool2
@@ -128,6 +132,16 @@ def risk_probs_from_projection(y, ln_w, ln_b, w2, b2, eps=1e-5):
     """The head after its first Linear: y [T, 512] bf16 values -> softmax(risk logits) [T, 3] float64."""
     y = silu(layer_norm(y, ln_w, ln_b, eps))
     logits = linear_bf16(bf16(y), w2, b2).astype(np.float64)
+    logits = logits - logits.max(-1, keepdims=True)
+    e = np.exp(logits)
+    return e / e.sum(-1, keepdims=True)
+
+
+def risk_probs_f32(hidden, w1, b1, ln_w, ln_b, w2, b2, eps=1e-5):
+    """hidden [T, hidden] -> softmax(risk logits) [T, 3] float64, with no bf16 rounding anywhere."""
+    y = np.asarray(hidden, np.float64) @ np.asarray(w1, np.float64).T + np.asarray(b1, np.float64)
+    y = silu(layer_norm(y, ln_w, ln_b, eps))
+    logits = y @ np.asarray(w2, np.float64).T + np.asarray(b2, np.float64)
     logits = logits - logits.max(-1, keepdims=True)
     e = np.exp(logits)
     return e / e.sum(-1, keepdims=True)

@@ -71,9 +71,22 @@ def ring_attention_reference(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, s
     return np.einsum('nhmj,nhjd->nhmd', p, values)
 
 
+def _blocks(window, lb, block):
+    """(start, end) of the key blocks: the W ring columns in blocks of ``block``, then the tick's new keys."""
+    edges = list(range(0, window, block)) + [window + j for j in range(0, lb, block)]
+    ends = edges[1:] + [window + lb]
+    return [(b0, min(b1, window) if b0 < window else b1) for b0, b1 in zip(edges, ends)]
+
+
 def attend_blockwise(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, lens, scale, window, block=32):
     """Same contract as ring_attention_reference, with the Triton kernels' blockwise online softmax and bf16
-    probabilities in the P.V product. Returns [N, Hkv, G*Lb, D] float64."""
+    probabilities in the P.V product. Returns [N, Hkv, G*Lb, D] float64.
+
+    Evaluated in closed form: with m_b the running max after block b (the prefix maximum of the block maxima),
+    the online recurrence ``acc = acc * exp(m_{b-1} - m_b) + bf16(exp(s - m_b)) @ v`` multiplies out to
+    ``acc = sum_b exp(m_b - m_last) * bf16(exp(s_b - m_b)) @ v_b`` (and the same for l with unrounded p), so
+    every bf16 rounding sits where the reference's loop puts it; ``attend_blockwise_online`` is the loop itself
+    and ``tests/test_oracle_ring.py`` holds the two together."""
     q = np.asarray(q, dtype=np.float64)
     N, Hkv, M, D = q.shape
     lb = new_k.shape[2]
@@ -83,21 +96,46 @@ def attend_blockwise(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, l
                            np.asarray(new_k, dtype=np.float64)], 2)
     values = np.concatenate([np.asarray(ring_v, dtype=np.float64)[slots, :, :window],
                              np.asarray(new_v, dtype=np.float64)], 2)
-    scores = np.where(ok[:, None], np.einsum('nhmd,nhjd->nhmj', q, keys) * scale, -np.inf)
+    scores = np.where(ok[:, None], np.matmul(q, keys.transpose(0, 1, 3, 2)) * scale, -np.inf)
+    blocks = _blocks(window, lb, block)
+    bmax = np.stack([scores[..., b0:b1].max(-1) for b0, b1 in blocks], -1)       # [N, Hkv, M, nblocks]
+    run = np.maximum.accumulate(bmax, -1)                                       # m_b
+    last = run[..., -1:]
+    width = np.array([b1 - b0 for b0, b1 in blocks])
+    m_key = np.repeat(run, width, axis=-1)                                      # m_b of each key's block
+    m_safe = np.where(np.isfinite(m_key), m_key, 0.0)
+    p = np.where(np.isfinite(scores), np.exp(scores - m_safe), 0.0)
+    wgt = np.where(np.isfinite(run), np.exp(run - np.where(np.isfinite(last), last, 0.0)), 0.0)
+    w_key = np.repeat(wgt, width, axis=-1)
+    acc = np.matmul(np.asarray(bf16(p), np.float64) * w_key, values)
+    l = (p * w_key).sum(-1)
+    return np.where(l[..., None] > 0, acc / np.where(l > 0, l, 1.0)[..., None], 0.0)
+
+
+def attend_blockwise_online(q, ring_k, ring_v, new_k, new_v, ring_pos, slots, starts, lens, scale, window,
+                            block=32):
+    """attend_blockwise as the reference kernels' loop (fused_kernels.py:309-341): one block at a time, the running
+    max updated and the accumulator and row sum rescaled after each block."""
+    q = np.asarray(q, dtype=np.float64)
+    N, Hkv, M, D = q.shape
+    lb = new_k.shape[2]
+    ok = allowed_mask(ring_pos, slots, starts, lens, lb, M // lb, window)
+    slots = np.asarray(slots, dtype=np.int64)
+    keys = np.concatenate([np.asarray(ring_k, dtype=np.float64)[slots, :, :window],
+                           np.asarray(new_k, dtype=np.float64)], 2)
+    values = np.concatenate([np.asarray(ring_v, dtype=np.float64)[slots, :, :window],
+                             np.asarray(new_v, dtype=np.float64)], 2)
+    scores = np.where(ok[:, None], np.matmul(q, keys.transpose(0, 1, 3, 2)) * scale, -np.inf)
     m = np.full((N, Hkv, M), -np.inf)
     l = np.zeros((N, Hkv, M))
     acc = np.zeros((N, Hkv, M, D))
-    edges = list(range(0, window, block)) + [window + j for j in range(0, lb, block)]
-    ends = edges[1:] + [window + lb]
-    for b0, b1 in zip(edges, ends):
-        b1 = min(b1, window) if b0 < window else b1
+    for b0, b1 in _blocks(window, lb, block):
         sb = scores[..., b0:b1]
         m_new = np.maximum(m, sb.max(-1))
         m_safe = np.where(np.isfinite(m_new), m_new, 0.0)
         pb = np.where(np.isfinite(sb), np.exp(sb - m_safe[..., None]), 0.0)
         alpha = np.where(np.isfinite(m), np.exp(m - m_safe), 0.0)
-        acc = acc * alpha[..., None] + np.einsum('nhmj,nhjd->nhmd', np.asarray(bf16(pb), np.float64),
-                                                 values[:, :, b0:b1])
+        acc = acc * alpha[..., None] + np.matmul(np.asarray(bf16(pb), np.float64), values[:, :, b0:b1])
         l = l * alpha + pb.sum(-1)
         m = m_new
     return np.where(l[..., None] > 0, acc / np.where(l > 0, l, 1.0)[..., None], 0.0)

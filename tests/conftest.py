@@ -15,7 +15,7 @@ def pytest_configure(config):
 def write_bundle(root, cfg, seed=0, extra_heads=True):
     """A synthetic local bundle in the released layout (hs_guard.json manifest with SHA-256s, config.json in
     transformers' Qwen3_5TextConfig.to_dict() form, a WordLevel tokenizer.json, model.safetensors with the
-    classifier's tensors). Returns (root, the bf16 state dict written)."""
+    classifier's tensors: backbone bf16, heads float32). Returns (root, the state dict written)."""
     import json
 
     import torch
@@ -28,6 +28,10 @@ def write_bundle(root, cfg, seed=0, extra_heads=True):
     root.mkdir(parents=True, exist_ok=True)
     state = dict(GuardModel.random(cfg, seed=seed, device="cpu").weights)
     gen = torch.Generator().manual_seed(seed + 1)
+    # the classifier heads are float32 modules in a released checkpoint: give them values bf16 cannot hold
+    for name in list(state):
+        if name.startswith("heads."):
+            state[name] = state[name].float() + torch.randn(state[name].shape, generator=gen) * 1e-4
     if extra_heads:   # the checkpoint's other heads: category and the general red-line alternative
         for role, cats in (("user", 9), ("assistant", 8)):
             p = f"heads.{role}."
@@ -39,7 +43,7 @@ def write_bundle(root, cfg, seed=0, extra_heads=True):
                                 (p + "general.weight", (3, cfg.head_hidden)), (p + "general.bias", (3,)),
                                 (p + "general_category.weight", (cats, cfg.head_hidden)),
                                 (p + "general_category.bias", (cats,))):
-                state[name] = (torch.randn(*shape, generator=gen) * 0.02).to(torch.bfloat16)
+                state[name] = torch.randn(*shape, generator=gen) * 0.02
     save_file({k: v.contiguous() for k, v in state.items()}, str(root / "model.safetensors"))
     hf = {"vocab_size": cfg.vocab_size, "hidden_size": cfg.hidden_size, "num_hidden_layers": cfg.num_hidden_layers,
           "intermediate_size": cfg.intermediate_size, "num_attention_heads": cfg.num_attention_heads,

@@ -20,6 +20,8 @@ kernel alone is held to 1e-3 in test_gdn_gpu.py).
 import numpy as np
 import pytest
 import torch
+from parity_helpers import matched_gemm as _matched_gemm
+from parity_helpers import max_diff as _max_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -52,50 +54,6 @@ def setup():
     model_cpu = GuardModel.random(cfg, seed=0, device="cpu")
     weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
     return cfg, model_cpu.to("cuda:0"), weights
-
-
-def _matched_gemm(eng):
-    """The engine's product (torch.mm / addmm into a [tb, N] bf16 buffer, tb the engine's token bucket) applied
-    to the oracle's padded [n, lb, K] activations: rows packed in request order, padded positions skipped."""
-    from hs_guard.engine.slot_engine import bucket, gdn_proj_width
-    cache = {}
-    cfg = eng.cfg
-    gdn_n = cfg.conv_dim + cfg.value_dim + 2 * cfg.linear_num_value_heads
-
-    def gemm(x, w, bias, lens):
-        n, lb, K = x.shape
-        lens = np.asarray(lens)
-        total = int(lens.sum())
-        tb = bucket(total, eng.token_buckets)
-        xp = np.zeros((tb, K), dtype=np.float32)
-        xp[:total] = np.concatenate([x[r, :lens[r]] for r in range(n)])
-        key = (w.shape, float(w.ravel()[0]), float(w.ravel()[-1]), float(w.sum()))
-        if key not in cache:
-            wp = w
-            if w.shape == (gdn_n, cfg.hidden_size):   # the engine's GDN projection carries zero padding rows
-                wp = np.concatenate([w, np.zeros((gdn_proj_width(cfg) - gdn_n, w.shape[1]), w.dtype)])
-            cache[key] = torch.from_numpy(np.ascontiguousarray(wp)).to(torch.bfloat16).cuda().contiguous()
-        W = cache[key]
-        xd = torch.from_numpy(xp).to(torch.bfloat16).cuda()
-        out = torch.empty(tb, W.shape[0], dtype=torch.bfloat16, device="cuda")
-        if bias is None:
-            torch.mm(xd, W.t(), out=out)
-        else:
-            torch.addmm(torch.from_numpy(bias).to(torch.bfloat16).cuda(), xd, W.t(), out=out)
-        y = out.float().cpu().numpy()[:, :w.shape[0]]
-        res = np.zeros((n, lb, w.shape[0]), dtype=np.float32)
-        at = 0
-        for r in range(n):
-            res[r, :lens[r]] = y[at:at + lens[r]]
-            at += lens[r]
-        return res
-    return gemm
-
-
-def _max_diff(got, ref):
-    """Largest per-token difference of the cut score 1 - p(safe) over both roles (the north-star quantity)."""
-    return max(np.abs(g.numpy()[:, 0] - e[:, 0]).max() for role in ("user", "assistant")
-               for g, e in zip(got[role], ref[role]))
 
 
 @pytest.fixture(scope="module")
@@ -271,3 +229,87 @@ def test_streaming_guard_api(setup):
         guard.step([(3, [1])])
     with pytest.raises(ValueError):
         guard.step([(0, [cfg.vocab_size])])
+
+
+def test_reset_slots_neighbours_untouched_and_fresh(setup2):
+    """reset(slots) (the per-slot reset config 5's sessions and the demo's scheduler rely on,
+    examples/demo/runtime_v10.py:98-111): the reset slots' pools return to the empty state, every other slot's
+    pools stay bit for bit, later ticks match the oracle reset the same way (matched GEMMs, 2e-3), and the
+    reset slot's outputs equal bit for bit those of a fresh engine that never saw the slot's earlier tokens
+    but runs the same later ticks."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from oracle.backbone import StreamOracle
+    cfg, model, weights = setup2
+    print("[engine] reset(slots)", flush=True)
+    sched = _schedule(np.random.default_rng(5), cfg.vocab_size)
+    first, later = sched[:5], sched[5:]
+    eng = SlotStreamEngine(model, 4, use_graphs=False)
+    fresh = SlotStreamEngine(model, 4, use_graphs=False)
+    orc = StreamOracle(weights, cfg, 4)
+    gemm = _matched_gemm(eng)
+    reset = [1, 3]
+    for tick in first:
+        eng.step(tick)
+        orc.step(tick, gemm=gemm)
+        rest = [(s, ids) for s, ids in tick if s not in reset]
+        if rest:
+            fresh.step(rest)
+    before = {n: getattr(eng, n).clone() for n in ("rec", "conv", "ring_k", "ring_v", "ring_pos")}
+    length = eng.length.copy()
+    eng.reset(reset)
+    orc.reset(reset)
+    keep = [0, 2, 4]                       # the other slots and the scratch slot
+    for n, t in before.items():
+        now = getattr(eng, n)
+        if n == "ring_pos":
+            assert torch.equal(now[keep], t[keep]) and bool((now[reset] == -1).all())
+        else:
+            assert torch.equal(now[:, keep], t[:, keep]), n
+            assert int(torch.count_nonzero(now[:, reset])) == 0, n
+    assert list(eng.length[reset]) == [0, 0] and list(eng.length[[0, 2]]) == list(length[[0, 2]])
+    worst = 0.0
+    for t, tick in enumerate(later):
+        got = eng.step(tick)
+        ref = orc.step(tick, gemm=gemm)
+        alone = fresh.step(tick)
+        worst = max(worst, _max_diff(got, ref))
+        assert worst <= PROB_TOL, f"tick {t}: {worst:.2e}"
+        for i, (s, _) in enumerate(tick):
+            if s in reset:
+                for role in got:
+                    np.testing.assert_array_equal(got[role][i].numpy(), alone[role][i].numpy(), err_msg=f"tick {t}")
+    print(f"[engine] after reset: worst prob diff {worst:.2e}", flush=True)
+    np.testing.assert_array_equal(eng.length, orc.length)
+    np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
+    for n in ("rec", "conv", "ring_k", "ring_v"):
+        assert torch.equal(getattr(eng, n)[:, reset], getattr(fresh, n)[:, reset]), n
+
+
+def test_matched_engine_pools_match_oracle(setup2):
+    """With matched GEMMs the pools the engine leaves behind match the oracle's: the GDN layer's conv history
+    (raw projections of the embedding's RMSNorm, identical inputs) bit for bit; the attention layer's ring keys
+    and values, whose inputs have passed the GDN layer (fp32 against float64 arithmetic, so a few bf16 roundings
+    of its output go the other way), within 5e-3 relative; state within 1e-3 relative."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from oracle.backbone import StreamOracle
+    cfg, model, weights = setup2
+    print("[engine] pools vs oracle, matched GEMMs", flush=True)
+    eng = SlotStreamEngine(model, 4, use_graphs=False)
+    orc = StreamOracle(weights, cfg, 4)
+    gemm = _matched_gemm(eng)
+    for tick in _schedule(np.random.default_rng(0), cfg.vocab_size):
+        eng.step(tick)
+        orc.step(tick, gemm=gemm)
+    W = cfg.window_tokens
+    conv = eng.conv[:, :4].float().cpu().numpy()
+    np.testing.assert_array_equal(conv, orc.conv[:, :4])
+    for name in ("ring_k", "ring_v"):
+        got = getattr(eng, name)[:, :4, :, :W].float().cpu().numpy()
+        ref = getattr(orc, name)[:, :4, :, :W]
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        print(f"[engine] {name}: {np.mean(got != ref):.1e} of values differ, rel {rel:.1e}", flush=True)
+        assert rel <= 5e-3, f"{name} rel {rel:.2e}"
+    rec = eng.rec.double().cpu().numpy()
+    for s in range(4):
+        rel = np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
+        assert rel < 1e-3, f"slot {s} state rel err {rel:.2e}"

@@ -183,23 +183,53 @@ def test_silu_mul_and_risk_head():
     act = torch.empty(T, I, dtype=torch.bfloat16, device=DEV)
     assert lib().hsg_silu_mul(gu_d.data_ptr(), 2 * I, I, act.data_ptr(), T, _stream()) == 0
     _close(_np(act), oglue.silu_mul(gu[:, :I], gu[:, I:]), "silu_mul")
-    E, R = 512, 2
+    # heads at the model's scale (weights N(0, 0.02)), LayerNorm parameters fp32 values bf16 cannot hold
+    T, E, R = 64, 512, 2
     y = bf16(rng.standard_normal((T, R * E)))
-    ln_w = bf16(1 + 0.05 * rng.standard_normal((R, E)))
-    ln_b = bf16(0.05 * rng.standard_normal((R, E)))
-    w2 = bf16(rng.standard_normal((R, 3, E)) * 0.05)
-    b2 = bf16(rng.standard_normal((R, 3)) * 0.1)
+    ln_w = (1 + 0.05 * rng.standard_normal((R, E))).astype(np.float32)
+    ln_b = (0.05 * rng.standard_normal((R, E))).astype(np.float32)
+    w2 = bf16(rng.standard_normal((R, 3, E)) * 0.02)
+    b2 = bf16(rng.standard_normal((R, 3)) * 0.02)
     probs = torch.empty(R, T, 3, dtype=torch.float32, device=DEV)
-    d = [_bf(x).to(DEV) for x in (y, ln_w, ln_b, w2, b2)]
+    d = [_bf(y).to(DEV), torch.from_numpy(ln_w).to(DEV), torch.from_numpy(ln_b).to(DEV), _bf(w2).to(DEV),
+         _bf(b2).to(DEV)]
     assert lib().hsg_risk_head(d[0].data_ptr(), R * E, d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(),
                                d[4].data_ptr(), 1e-5, R, E, probs.data_ptr(), T, _stream()) == 0
     got = _np(probs)
     for r in range(R):
-        # the reference head from the projection output on: LayerNorm -> SiLU -> bf16 -> Linear -> bf16
+        # the reference head from the projection output on: LayerNorm -> SiLU -> bf16 -> Linear -> bf16.
+        # A bf16 logit of magnitude below 1 is one step of at most 2**-9 from its neighbour, which moves a
+        # probability by at most 2**-9 / 4, so fp32-vs-float64 rounding flips stay below 1e-3.
         v = oglue.silu(oglue.layer_norm(y[:, r * E:(r + 1) * E], ln_w[r], ln_b[r]))
         logits = oglue.linear_bf16(bf16(v), w2[r], b2[r]).astype(np.float64)
+        assert np.abs(logits).max() < 1.0
         e = np.exp(logits - logits.max(-1, keepdims=True))
-        np.testing.assert_allclose(got[r], e / e.sum(-1, keepdims=True), rtol=0, atol=4e-3)
+        np.testing.assert_allclose(got[r], e / e.sum(-1, keepdims=True), rtol=0, atol=1e-3)
+
+
+def test_risk_head_f32():
+    """hsg_risk_head_f32 (the complete-message readout: fp32 everywhere) against the float64 oracle."""
+    from hs_guard._lib import lib
+    print("[glue] risk head fp32", flush=True)
+    rng = np.random.default_rng(6)
+    T, E, R, H = 37, 512, 2, 1024
+    h = bf16(rng.standard_normal((T, H)))
+    w1 = (rng.standard_normal((R * E, H)) * 0.02).astype(np.float32)
+    b1 = (rng.standard_normal(R * E) * 0.02).astype(np.float32)
+    ln_w = (1 + 0.05 * rng.standard_normal((R, E))).astype(np.float32)
+    ln_b = (0.05 * rng.standard_normal((R, E))).astype(np.float32)
+    w2 = (rng.standard_normal((R, 3, E)) * 0.3).astype(np.float32)
+    b2 = (rng.standard_normal((R, 3)) * 0.1).astype(np.float32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+    y = torch.addmm(t(b1), t(h), t(w1).t())             # fp32 GEMM, as the scorer runs it
+    probs = torch.empty(R, T, 3, dtype=torch.float32, device=DEV)
+    dl = [t(x) for x in (ln_w, ln_b, w2, b2)]
+    assert lib().hsg_risk_head_f32(y.data_ptr(), R * E, dl[0].data_ptr(), dl[1].data_ptr(), dl[2].data_ptr(),
+                                   dl[3].data_ptr(), 1e-5, R, E, probs.data_ptr(), T, _stream()) == 0
+    got = _np(probs)
+    for r in range(R):
+        ref = oglue.risk_probs_f32(h, w1[r * E:(r + 1) * E], b1[r * E:(r + 1) * E], ln_w[r], ln_b[r], w2[r], b2[r])
+        np.testing.assert_allclose(got[r], ref, rtol=0, atol=2e-5)
 
 
 def test_ring_pos_update_bit_exact():

@@ -107,3 +107,43 @@ def test_planted_mistakes_are_detected():
     with exact():
         bad = _stream_hidden(StreamOracle(w2, cfg, 2), 0, ids, [4, 8])
     assert _rel(bad, ref) > 1e-2
+
+
+def _floor(cfg, seed, slots, ctx, decode_ticks, ulps=1):
+    """Largest per-token |d(1 - p(safe))| between the oracle and the oracle with fp32-level rounding freedom
+    (oracle.bf16.perturbed(4): the roughly 1.4e-4 of bf16 roundings that lie within 4 fp32 ulps of a tie go the
+    other way) everywhere except in the GEMM outputs, which stay one fixed function of their inputs as in the
+    matched-GEMM engine tests; over a tick of ``ctx`` tokens per slot and ``decode_ticks`` single-token ticks."""
+    from hs_guard.model import GuardModel
+    from oracle.bf16 import perturbed
+    from oracle.glue import linear_bf16
+
+    def gemm(x, wt, bias, lens):
+        with perturbed(0):
+            return linear_bf16(x, wt, bias)
+    m = GuardModel.random(cfg, seed=seed, device="cpu")
+    w = {k: v.float().numpy() for k, v in m.weights.items()}
+    rng = np.random.default_rng(seed)
+    ticks = [[(s, rng.integers(0, cfg.vocab_size, ctx).tolist()) for s in range(slots)]]
+    ticks += [[(s, [int(rng.integers(0, cfg.vocab_size))]) for s in range(slots)] for _ in range(decode_ticks)]
+    a, b = StreamOracle(w, cfg, slots, gdn="chunk"), StreamOracle(w, cfg, slots, gdn="chunk")
+    worst = 0.0
+    for tick in ticks:
+        pa, _ = a.tick(tick, gemm=gemm)
+        with perturbed(ulps):
+            pb, _ = b.tick(tick, gemm=gemm)
+        worst = max(worst, float(np.abs(pa[..., 0] - pb[..., 0]).max()))
+    return worst
+
+
+def test_noise_floor_at_benchmark_depth():
+    """At the 24-layer benchmark geometry (GuardConfig.baseline(), random-init N(0, 0.02) weights) the oracle's
+    own fp32-level noise floor exceeds the 2e-3 end-to-end bar: letting the values within one fp32 ulp of a bf16
+    rounding tie round the other way -- a freedom any fp32 evaluation has, the reference's kernels included --
+    moves cut scores by several times 2e-3. A full-geometry comparison is therefore held to this floor,
+    measured on identical inputs (tests/test_full_geometry_gpu.py); the 2e-3 bar is kept for the 2-layer
+    matched-GEMM tests (tests/test_engine_gpu.py)."""
+    from hs_guard.model import GuardConfig
+    f24 = _floor(GuardConfig.baseline(), 0, 2, 64, 1)
+    print(f"noise floor at 24 layers: {f24:.2e}")
+    assert f24 > 2e-3

@@ -148,3 +148,22 @@ def test_tick_size_invariance():
                                         A_log, dt, st, [1], [1])
         np.testing.assert_allclose(o_t[0, 0], o_all[0, t], rtol=1e-12, atol=1e-14)
     np.testing.assert_allclose(st, st_all, rtol=1e-12, atol=1e-14)
+
+
+def test_chunked_slot_step_equals_recurrent_slot_step():
+    """gdn_slot_step_chunked (the chunk form per row, used for full-geometry ticks) gives gdn_slot_step's outputs
+    and state to float64 rounding: rows longer than one chunk, a row shorter than its tick, an empty row, the
+    GQA head map (HV > H), untouched other slots."""
+    rng = np.random.default_rng(6)
+    H, HV, K = 2, 4, 128
+    packed, a, b, A_log, dt, state = _slot_inputs(rng, N=4, L=70, H=H, HV=HV)
+    packed[..., :2 * H * K] *= 0.2          # raw q, k of conv-output scale
+    slots, lens = np.array([3, 0, 5, 1]), np.array([70, 9, 0, 1])
+    o_r, sq_r, st_r = ogdn.gdn_slot_step(packed, H * K, H, K, HV, K, a, b, A_log, dt, state, slots, lens)
+    o_c, sq_c, st_c = ogdn.gdn_slot_step_chunked(packed, H * K, H, K, HV, K, a, b, A_log, dt, state, slots, lens)
+    scale = np.abs(o_r).max()
+    np.testing.assert_allclose(o_c, o_r, rtol=1e-10, atol=1e-12 * scale)
+    np.testing.assert_allclose(st_c, st_r, rtol=1e-10, atol=1e-12 * np.abs(st_r).max())
+    assert (o_c[1, 9:] == 0).all() and (o_c[2] == 0).all()
+    for s in (2, 4):
+        np.testing.assert_array_equal(st_c[s], state[s])

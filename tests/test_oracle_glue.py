@@ -118,3 +118,24 @@ def test_silu_mul_and_risk_head_match_torch():
     logits = torch.nn.functional.linear(y.to(torch.bfloat16).double(), t(w2), t(b2)).to(torch.bfloat16).double()
     ref = torch.softmax(logits, -1).numpy()
     np.testing.assert_allclose(oglue.risk_probs(h, w1, b1, lw, lb, w2, b2), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_risk_head_f32_matches_torch_modules():
+    """risk_probs_f32 (the complete-message readout) equals the reference's head modules -- nn.Linear,
+    nn.LayerNorm, nn.SiLU, nn.Linear in float64 -- applied to hidden.float(), with no bf16 rounding; and it
+    differs from the streaming readout (risk_probs) by the three bf16 roundings that readout makes."""
+    rng = np.random.default_rng(5)
+    h = bf16(rng.standard_normal((7, 16)))
+    w1, b1 = rng.standard_normal((8, 16)) * 0.3, rng.standard_normal(8) * 0.1      # fp32 values, not bf16
+    lw, lb = 1 + 0.1 * rng.standard_normal(8), 0.1 * rng.standard_normal(8)
+    w2, b2 = rng.standard_normal((3, 8)), rng.standard_normal(3) * 0.1
+    proj = torch.nn.Sequential(torch.nn.Linear(16, 8), torch.nn.LayerNorm(8), torch.nn.SiLU()).double()
+    risk = torch.nn.Linear(8, 3).double()
+    with torch.no_grad():
+        for p_, v in zip((proj[0].weight, proj[0].bias, proj[1].weight, proj[1].bias, risk.weight, risk.bias),
+                         (w1, b1, lw, lb, w2, b2)):
+            p_.copy_(torch.from_numpy(v))
+        ref = torch.softmax(risk(proj(torch.from_numpy(h).double())), -1).numpy()
+    got = oglue.risk_probs_f32(h, w1, b1, lw, lb, w2, b2)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-14)
+    assert np.abs(oglue.risk_probs(h, w1, b1, lw, lb, w2, b2) - got).max() > 1e-6

@@ -57,3 +57,26 @@ def test_bf16_matches_torch_cast():
                         np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, 1e-40], dtype=np.float32)])
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(bf16(x), ref)
+
+
+def test_bf16_perturbed_flips_exactly_the_values_near_a_tie():
+    """Inside perturbed(k) the values within k fp32 ulps of a bf16 rounding tie take the other bf16 neighbour
+    and every other value rounds as torch's cast does."""
+    from oracle.bf16 import perturbed
+    torch = pytest.importorskip("torch")
+    base = np.random.default_rng(2).standard_normal(4000).astype(np.float32)
+    hi = base.view(np.uint32) & np.uint32(0xFFFF0000)
+    offsets = np.arange(-6, 7, dtype=np.int64)            # distance (fp32 ulps) to the tie at low half 0x8000
+    u = (hi[:, None].astype(np.int64) + 0x8000 + offsets[None]).astype(np.uint32)
+    x = u.view(np.float32).ravel()
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    with perturbed(3):
+        got = bf16(x)
+    flipped = (got != ref).reshape(u.shape)
+    np.testing.assert_array_equal(flipped, np.broadcast_to(np.abs(offsets) <= 3, u.shape))
+    near = np.broadcast_to(np.abs(offsets) <= 3, u.shape)
+    lo = np.minimum(got, ref).reshape(u.shape)[near]
+    hi_ = np.maximum(got, ref).reshape(u.shape)[near]
+    xs = x.reshape(u.shape)[near]
+    assert np.all((lo < xs) & (xs < hi_)) or np.all((lo > xs) & (xs > hi_))   # the two neighbours of each value
+    np.testing.assert_array_equal(bf16(x), ref)              # outside the context: plain rounding again

@@ -99,3 +99,14 @@ def test_blockwise_equals_exact_without_rounding_and_is_within_bf16_p_bound():
         # bf16 p: each weight moves by at most 2**-8 relative, so the output by at most 2**-8 * sum|p v| / l
         bound = 2.0 ** -8 * np.abs(nv).max() * 2 + 1e-12
         assert np.abs(rounded - ref).max() <= bound
+
+
+def test_closed_form_equals_online_loop():
+    """attend_blockwise (the rescale chain multiplied out) equals the reference kernels' block-by-block loop with
+    bf16 probabilities, to float64 rounding: decode and multi-step ticks, partly filled and empty rings."""
+    rng = np.random.default_rng(8)
+    for lb in (1, 3, 40):
+        q, rk, rv, nk, nv, rp, slots, starts, lens, W = _setup(rng, N=4, Lb=lb, W=64, D=16)
+        a = oring.attend_blockwise(q, rk, rv, nk, nv, rp, slots, starts, lens, 0.4, W)
+        b = oring.attend_blockwise_online(q, rk, rv, nk, nv, rp, slots, starts, lens, 0.4, W)
+        np.testing.assert_allclose(a, b, rtol=1e-11, atol=1e-13)

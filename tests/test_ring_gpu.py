@@ -21,7 +21,8 @@ def _check(got, ref, rtol=2.0 ** -7, atol_frac=1e-3, what="out"):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     atol = atol_frac * max(np.abs(ref).max(), 1e-30)
-    bad = np.abs(got - ref) > rtol * np.abs(ref) + atol
+    # steps counted in the binade of the larger magnitude: one step of the upper binade is two of the lower
+    bad = np.abs(got - ref) > rtol * np.maximum(np.abs(ref), np.abs(got)) + atol
     assert not bad.any(), f"{what}: {int(bad.sum())} values off, max diff {np.abs(got - ref).max():.3e}"
 
 
@@ -207,3 +208,80 @@ def test_mixed_packed_tick_split_between_kernels():
     _check(a, b, rtol=2.0 ** -8, what="split vs single kernel")
     np.testing.assert_array_equal(rka, rkb)
     np.testing.assert_array_equal(rva, rvb)
+
+
+def test_config4_window_fill_64_tokens():
+    """Config 4's second leg: after contexts of 512 / 2048 / 8000 tokens (rings full and wrapped), one 64-token
+    tick per slot at W = 512 through hsg_ring_attention with the ring write (packed rows, 16 q / 4 kv heads,
+    D = 256), against the oracle's attention and its Lb > 1 scatter (slot_engine_v8.py:86-88). A row of 37 tokens
+    and a row whose tick crosses column 0 cover ragged and wrapping writes. Outputs within two bf16 steps; every
+    ring column bit-exact."""
+    from hs_guard._lib import lib
+    print("[ring] config-4 window fill, 64-token tick at W=512", flush=True)
+    gen = torch.Generator().manual_seed(44)
+    Hkv, G, D, W, Lb = 4, 4, 256, 512, 64
+    N = 16
+    S = N + 1
+    hq = Hkv * G
+    starts = torch.tensor([(512, 2048, 8000)[i % 3] for i in range(N)], dtype=torch.long)
+    starts[5] = 500                     # the tick's columns run 500..511, then 0..51
+    lens = torch.full((N,), Lb, dtype=torch.long)
+    lens[9] = 37
+    offsets = torch.cumsum(lens, 0) - lens
+    T = int(lens.sum())
+    slots = torch.randperm(S - 1, generator=gen)[:N]
+    ring_k = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, Hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s, st in zip(slots.tolist(), starts.tolist()):
+        for p_ in range(max(0, st - W), st):
+            ring_pos[s, p_ % W] = p_
+    att_in = hq * 2 * D + 2 * Hkv * D
+    proj = torch.randn(T, att_in, generator=gen).to(torch.bfloat16)      # q|gate per head, k, v (engine layout)
+    q = torch.randn(T, hq * D, generator=gen).to(torch.bfloat16)
+    k = torch.randn(T, Hkv * D, generator=gen).to(torch.bfloat16)
+    dev = torch.device("cuda:0")
+    d = {n: t.to(dev) for n, t in dict(proj=proj, q=q, k=k, slots=slots, starts=starts, lens=lens,
+                                         offsets=offsets, ring_pos=ring_pos, ring_k=ring_k, ring_v=ring_v).items()}
+    out = torch.zeros(T, hq * D, dtype=torch.bfloat16, device=dev)
+    base = d["proj"].data_ptr()
+    rc = lib().hsg_ring_attention(
+        d["q"].data_ptr(), 0, hq * D, G * D, D, d["ring_k"].data_ptr(), d["ring_v"].data_ptr(), S, W,
+        d["k"].data_ptr(), 0, Hkv * D, D, base + 2 * (hq * 2 * D + Hkv * D), 0, att_in, D,
+        base, 0, att_in, G * 2 * D, 2 * D, D,
+        d["ring_pos"].data_ptr(), d["slots"].data_ptr(), d["starts"].data_ptr(), d["lens"].data_ptr(),
+        d["offsets"].data_ptr(), N, Lb, Hkv, G, D, D ** -0.5, 1, 0, out.data_ptr(), 0, hq * D, G * D, D,
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    # oracle in the padded [N, Lb] layout
+    qn, kn, pn = _np(q), _np(k), _np(proj)
+    qp = np.zeros((N, Lb, hq * D), np.float32)
+    kp = np.zeros((N, Lb, Hkv * D), np.float32)
+    vp = np.zeros((N, Lb, Hkv * D), np.float32)
+    gp = np.zeros((N, Lb, hq * 2 * D), np.float32)
+    for n in range(N):
+        o0, ln = int(offsets[n]), int(lens[n])
+        qp[n, :ln], kp[n, :ln] = qn[o0:o0 + ln], kn[o0:o0 + ln]
+        gp[n, :ln] = pn[o0:o0 + ln, :hq * 2 * D]
+        vp[n, :ln] = pn[o0:o0 + ln, hq * 2 * D + Hkv * D:]
+    qg = qp.reshape(N, Lb, Hkv, G, D).transpose(0, 2, 3, 1, 4).reshape(N, Hkv, G * Lb, D)
+    new_k = kp.reshape(N, Lb, Hkv, D).transpose(0, 2, 1, 3)
+    rk, rv = _np(ring_k), _np(ring_v)
+    ref, _, _, _ = oring.ring_attention_v8(qg, rk, rv, new_k, vp, gp, ring_pos.numpy(), slots.numpy(),
+                                           starts.numpy(), lens.numpy(), D ** -0.5, W, False)
+    oring.ring_scatter(rk, rv, new_k, vp.reshape(N, Lb, Hkv, D).transpose(0, 2, 1, 3), slots.numpy(),
+                       starts.numpy(), lens.numpy(), W)
+    got = _np(out)
+    far = 0
+    for n in range(N):
+        o0, ln = int(offsets[n]), int(lens[n])
+        # output = bf16(bf16(o) * bf16(sigmoid(gate))): a one-step flip of bf16(o) near the top of its binade
+        # becomes two steps of the product's lower binade, so the bound is 2**-6 with almost all within 2**-7
+        _check(got[o0:o0 + ln], ref[n, :ln], rtol=2.0 ** -6, what=f"row {n}")
+        g, r = got[o0:o0 + ln].astype(np.float64), ref[n, :ln].astype(np.float64)
+        far += int((np.abs(g - r) > 2.0 ** -7 * np.maximum(np.abs(g), np.abs(r)) + 1e-3 * np.abs(r).max()).sum())
+    assert far <= 1e-5 * got.size, f"{far} values beyond two bf16 steps"
+    # the scratch column W takes the padded steps in the reference's scatter; this build never writes it
+    np.testing.assert_array_equal(_np(d["ring_k"])[:, :, :W], rk[:, :, :W])
+    np.testing.assert_array_equal(_np(d["ring_v"])[:, :, :W], rv[:, :, :W])

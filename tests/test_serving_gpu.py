@@ -1,0 +1,108 @@
+"""Config 5's serving shape on the GPU: 352 slots of the baseline backbone (GuardConfig.baseline(): 24 layers,
+16q/4kv attention with a 512-token window, vocab 151,936), contexts of 8-599 tokens (some rings wrap), then
+mixed ticks with config 5's chunk sizes (1 token p 0.8, 2-16 p 0.15, 17-64 p 0.05) and per-slot resets between
+them (src/hs_guard/engine/slot_engine_v7.py:138-145 for the tick, examples/demo/runtime_v10.py:98-111 for the
+per-slot resets).
+
+Checked after every tick:
+* ring_pos and length of all 352 slots bit-exact against the oracle's pack model (oracle.pack.ring_pos_update
+  per tick, zeroed rows for reset slots);
+* a reset zeroes exactly the reset slots' pools and leaves every other slot's pools bit for bit;
+* sampled slots (one of them reset) give the outputs of the same slots run alone on a 3-slot engine. The two
+  engines run the same kernels on the same rows; only the GEMMs' row count differs, and hipBLASLt may pick a
+  different algorithm (summation order) for a different M, so the bound is the independent-GEMM bar of
+  tests/test_engine_gpu.py, 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SLOTS = 352
+ALONE_TOL = 1e-2
+
+
+def _chunk_sizes(rng, n):
+    u = rng.random(n)
+    return np.where(u < 0.8, 1, np.where(u < 0.95, rng.integers(2, 17, n), rng.integers(17, 65, n)))
+
+
+class _PackModel:
+    """ring_pos / length bookkeeping of the reference over 64-token ticks (oracle.pack)."""
+
+    def __init__(self, slots, window):
+        self.W = window
+        self.ring_pos = np.full((slots + 1, window + 1), -1, dtype=np.int64)
+        self.length = np.zeros(slots, dtype=np.int64)
+
+    def step(self, requests):
+        from oracle import pack as opack
+        pending = [(s, len(ids)) for s, ids in requests]
+        while pending:
+            slots = np.array([s for s, _ in pending])
+            lens = np.array([min(n, 64) for _, n in pending])
+            opack.ring_pos_update(self.ring_pos, slots, self.length[slots], lens, int(lens.max()), self.W)
+            self.length[slots] += lens
+            pending = [(s, n - 64) for s, n in pending if n > 64]
+
+    def reset(self, slots):
+        self.ring_pos[slots] = -1
+        self.length[slots] = 0
+
+
+def test_config5_mixed_ticks_with_resets():
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    print("[serve] 352-slot baseline engine", flush=True)
+    cfg = GuardConfig.baseline()
+    model = GuardModel.random(cfg, seed=0, device="cuda:0")
+    V, W = cfg.vocab_size, cfg.window_tokens
+    rng = np.random.default_rng(0)
+    eng = SlotStreamEngine(model, SLOTS)
+    pm = _PackModel(SLOTS, W)
+    sample = [7, 100, 351]
+    alone = SlotStreamEngine(model, len(sample), use_graphs=False)
+    to_alone = {s: i for i, s in enumerate(sample)}
+
+    def run(requests):
+        got = eng.step(requests)
+        pm.step(requests)
+        mine = [(to_alone[s], ids) for s, ids in requests if s in to_alone]
+        ref = alone.step(mine)
+        worst = 0.0
+        for j, (s, _) in enumerate(r for r in requests if r[0] in to_alone):
+            i = [r[0] for r in requests].index(s)
+            for role in got:
+                worst = max(worst, float(np.abs(got[role][i].numpy()[:, 0] - ref[role][j].numpy()[:, 0]).max()))
+        np.testing.assert_array_equal(eng.length, pm.length)
+        np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), pm.ring_pos)
+        return worst
+
+    ctx = rng.integers(8, 600, SLOTS)
+    ctx[sample[0]] = 590                      # a sampled slot whose ring wraps
+    worst = run([(s, rng.integers(0, V, int(n)).tolist()) for s, n in enumerate(ctx)])
+    print(f"[serve] contexts: {int(ctx.sum())} tokens, {int((ctx > W).sum())} rings wrapped, "
+          f"alone diff {worst:.2e}", flush=True)
+    assert worst <= ALONE_TOL
+    for t in range(4):
+        if t:
+            reset = sorted(set(np.nonzero(rng.random(SLOTS) < 0.01)[0].tolist()) | {sample[t % 3], 200 + t})
+            before = {n: getattr(eng, n).clone() for n in ("rec", "conv", "ring_k", "ring_v", "ring_pos")}
+            eng.reset(reset)
+            pm.reset(reset)
+            alone.reset([to_alone[s] for s in reset if s in to_alone])
+            keep = np.setdiff1d(np.arange(SLOTS + 1), reset)
+            for n, old in before.items():
+                now = getattr(eng, n)
+                if n == "ring_pos":
+                    assert torch.equal(now[keep], old[keep]) and bool((now[reset] == -1).all())
+                else:
+                    assert torch.equal(now[:, keep], old[:, keep]), n
+                    assert int(torch.count_nonzero(now[:, reset])) == 0, n
+            del before
+        sizes = _chunk_sizes(rng, SLOTS)
+        worst = run([(s, rng.integers(0, V, int(n)).tolist()) for s, n in enumerate(sizes)])
+        print(f"[serve] mixed tick {t}: {int(sizes.sum())} tokens, alone diff {worst:.2e}", flush=True)
+        assert worst <= ALONE_TOL
+    assert eng.stats["graph_replays"] > 0

@@ -12,9 +12,11 @@ many windows and 64-token segments.
 import numpy as np
 import pytest
 import torch
+from parity_helpers import oracle_whole, whole_matched_gemm
 
 pytestmark = pytest.mark.gpu
 
+PROB_TOL = 2e-3
 PROB_TOL_INDEPENDENT = 1e-2
 
 
@@ -32,16 +34,39 @@ def setup():
 @pytest.mark.parametrize("T", [1, 63, 200])
 def test_whole_sequence_matches_oracle(setup, T):
     from hs_guard.engine.whole import WholeSequenceScorer
-    from oracle.backbone import StreamOracle
     cfg, model, weights = setup
     print(f"[whole] T={T} vs oracle", flush=True)
     ids = np.random.default_rng(T).integers(0, cfg.vocab_size, T).tolist()
     got = WholeSequenceScorer(model).forward(ids).cpu().numpy()
-    ref = StreamOracle(weights, cfg, 1).step([(0, ids)])
+    ref = oracle_whole(weights, cfg, ids)
     for i, role in enumerate(("user", "assistant")):
-        diff = np.abs(got[i] - ref[role][0]).max()
+        diff = np.abs(got[i] - ref[i]).max()
         print(f"[whole] T={T} {role}: max prob diff {diff:.2e}", flush=True)
         assert diff <= PROB_TOL_INDEPENDENT, f"{role}: {diff:.2e}"
+
+
+def test_whole_sequence_matched_gemms():
+    """On the 2-layer [GDN, attention] net with the oracle's projections computed by the scorer's own product
+    (tests/parity_helpers.py), every other kernel of the complete-message path -- conv, chunked GDN prefill,
+    gated RMSNorm, window attention over gathered segment rings, the fp32 risk heads -- is held to the north
+    star's 2e-3 on 1 - p(safe) against the float64 oracle read out in fp32 (runtime.py:70-73,141)."""
+    from hs_guard.engine.whole import WholeSequenceScorer
+    from hs_guard.model import GuardConfig, GuardModel
+    print("[whole] matched GEMMs, 2 layers", flush=True)
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=2,
+                      layer_types=["linear_attention", "full_attention"], intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    model_cpu = GuardModel.random(cfg, seed=1, device="cpu")
+    weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
+    model = model_cpu.to("cuda:0")
+    for T in (50, 200):
+        ids = np.random.default_rng(T + 1).integers(0, cfg.vocab_size, T).tolist()
+        got = WholeSequenceScorer(model).forward(ids).cpu().numpy()
+        ref = oracle_whole(weights, cfg, ids, gemm=whole_matched_gemm(cfg))
+        diff = float(np.abs(got[:, :, 0] - ref[:, :, 0]).max())
+        print(f"[whole] T={T}: max |d cut| {diff:.2e}", flush=True)
+        assert diff <= PROB_TOL, f"T={T}: {diff:.2e}"
 
 
 def test_attention_segment_batches_agree(setup, monkeypatch):
