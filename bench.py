@@ -196,33 +196,116 @@ def chunk_prefill_rate(torch, iters=10):
             "roof_tflops": round(ridge, 1), "roof_frac": round(tflops / ridge, 4)}
 
 
-def cpu_baseline(model, cfg, seed=0, slots=8, ticks=3):
-    """The CPU restatement (oracle.backbone.StreamOracle: numpy fp32 GEMMs, float64 recurrence) on a bounded
-    sample of config 5: ``slots`` slots with a 32-token context (untimed), then ``ticks`` mixed ticks with
-    config-5 chunk sizes. Returns streamed tokens per CPU second."""
-    import numpy as np
-    from oracle.backbone import StreamOracle
-    from hs_guard.synthetic import MixedServingLoad
+def cpu_model_name():
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        cores = os.cpu_count()
-    w = {k: v.float().cpu().numpy() for k, v in model.weights.items()}
-    orc = StreamOracle(w, cfg, max_slots=slots)
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model, cfg, seed=0, slots=352, steps=10, decode_steps=20):
+    """CPU baseline: oracle/torch_cpu.py, the PyTorch float32 restatement of the same step, on this host's cores
+    (torch threads = this job's CPU share: OMP_NUM_THREADS, else os.cpu_count()). The reference has no CPU path.
+    Legs:
+    * config 5 (the headline): ``slots`` slots, initial contexts U{512, 2048, 8000} (the pools filled as after
+      them: state, conv history and rings random, ring positions and lengths exact; a step's work does not depend
+      on the pools' values), one warm-up step, then ``steps`` timed mixed steps of config 5's chunk sizes.
+      tokens/s over those steps; the 2,000-step run of the config is extrapolated from the per-step time;
+    * config 3: 64 slots x 1 token after 512-token contexts, ``decode_steps`` steps;
+    * config 1: the GDN step alone, 16 slots x 1 token x 64 sequential steps, 16 heads x 128, fp32 state;
+    * config 2: one decode step of the window attention with its ring write, 64 slots, 16q / 4kv / 256, W = 512;
+    * config 4: the chunk form over 16 rows of 512 / 2048 / 8000 tokens (53,312 tokens), 16 heads x 128."""
+    import numpy as np
+    import torch
+    from hs_guard.synthetic import MixedServingLoad, chunk_prefill_inputs, gdn_step_inputs, ring_decode_inputs
+    from oracle.torch_cpu import TorchStream, gdn_chunk_torch, gdn_step_torch, ring_decode_torch
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    legs = {}
+    # ---- config 5 ----
     load = MixedServingLoad(slots=slots, vocab=cfg.vocab_size, seed=seed + 7)
-    rng = np.random.default_rng(seed)
-    orc.step([(s, rng.integers(0, cfg.vocab_size, 32).tolist()) for s in range(slots)])
+    lengths = [int(load.rng.choice(load.contexts)) for _ in range(slots)]
+    ts = TorchStream(model.weights, cfg, slots)
+    ts.fill_synthetic(lengths, seed=seed)
+    ts.tick(load.step_requests())
     tokens, secs = 0, 0.0
-    for _ in range(ticks):
+    for _ in range(steps):
         req = load.step_requests()
         t0 = time.perf_counter()
-        orc.step(req)
+        ts.tick(req)
         secs += time.perf_counter() - t0
         tokens += sum(len(ids) for _, ids in req)
-    return {"value": round(tokens / secs, 2), "unit": "tokens/s", "cores": int(cores), "kind": "port",
-            "sample": f"oracle.backbone.StreamOracle, full backbone, {slots} slots after 32-token contexts, "
-                      f"{ticks} config-5 mixed ticks ({tokens} tokens, {secs:.1f} s)"}
+    legs["config5"] = {"steps": steps, "tokens": tokens, "s_per_step": round(secs / steps, 3),
+                       "tokens_per_s": round(tokens / secs, 1),
+                       "extrapolated_2000_steps_s": round(secs / steps * 2000, 1)}
+    del ts
+    # ---- config 3 ----
+    ts = TorchStream(model.weights, cfg, 64)
+    ts.fill_synthetic([512] * 64, seed=seed + 1)
+    rng = np.random.default_rng(seed)
+    ts.tick([(s, [int(rng.integers(0, cfg.vocab_size))]) for s in range(64)])
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        ts.tick([(s, [int(rng.integers(0, cfg.vocab_size))]) for s in range(64)])
+    dt = time.perf_counter() - t0
+    legs["config3"] = {"steps": decode_steps, "ms_per_step": round(dt / decode_steps * 1e3, 2),
+                       "tokens_per_s": round(64 * decode_steps / dt, 1)}
+    del ts
+    # ---- config 1 ----
+    inp = gdn_step_inputs(slots=16, steps=64)
+    state = inp["state0"].float().clone()
+    A_log, dt_b = inp["A_log"].float(), inp["dt_bias"].float()
+    sl = torch.arange(16)
+    t0 = time.perf_counter()
+    for t in range(64):
+        gdn_step_torch(inp["packed"][t, :, 0].float(), 16 * 128, 16, 128, 16, 128, inp["a"][t, :, 0].float(),
+                       inp["b"][t, :, 0].float(), A_log, dt_b, state, sl)
+    dt = time.perf_counter() - t0
+    legs["config1"] = {"steps": 64, "ms_per_step": round(dt / 64 * 1e3, 3),
+                       "gbs": round(33948672 * 64 / dt / 1e9, 2)}
+    # ---- config 2 ----
+    r = ring_decode_inputs(rows=64)
+    f = {k: (v.float() if torch.is_tensor(v) and v.is_floating_point() else v) for k, v in r.items()}
+    gate = f["gate"].reshape(64, 16, 512)[..., 256:].reshape(64, 4, 4, 256)
+    times = []
+    for _ in range(4):
+        rk, rv = f["ring_k"].clone(), f["ring_v"].clone()
+        t0 = time.perf_counter()
+        ring_decode_torch(f["q"], rk, rv, f["new_k"][:, :, 0], f["new_v"][:, :, 0], gate, r["ring_pos"], r["slots"],
+                          r["starts"], 1 / 16, 512)
+        times.append(time.perf_counter() - t0)
+    legs["config2"] = {"ms": round(min(times[1:]) * 1e3, 2)}
+    # ---- config 4 ----
+    inp = chunk_prefill_inputs(rows=16)
+    t_all = 0.0
+    for L in (512, 2048, 8000):
+        rows = [i for i in range(16) if int(inp["lens"][i]) == L]
+        pk = torch.stack([inp["packed"][int(inp["offsets"][i]):int(inp["offsets"][i]) + L].float() for i in rows])
+        a = torch.stack([inp["a"][int(inp["offsets"][i]):int(inp["offsets"][i]) + L].float() for i in rows])
+        b = torch.stack([inp["b"][int(inp["offsets"][i]):int(inp["offsets"][i]) + L].float() for i in rows])
+        n = len(rows)
+        q = pk[..., :2048].reshape(n, L, 16, 128)
+        k = pk[..., 2048:4096].reshape(n, L, 16, 128)
+        v = pk[..., 4096:].reshape(n, L, 16, 128)
+        t0 = time.perf_counter()
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6) * 128 ** -0.5
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+        g = -torch.nn.functional.softplus(a, threshold=20.0)
+        flat = lambda x: x.transpose(1, 2).reshape(n * 16, L, -1)
+        S = torch.zeros(n * 16, 128, 128)
+        gdn_chunk_torch(flat(q), flat(k), flat(v), g.transpose(1, 2).reshape(n * 16, L),
+                        torch.sigmoid(b).transpose(1, 2).reshape(n * 16, L), S)
+        t_all += time.perf_counter() - t0
+    legs["config4"] = {"ms": round(t_all * 1e3, 1), "tflops": round(156058871472 / t_all / 1e12, 3)}
+    c5 = legs["config5"]
+    return {"value": c5["tokens_per_s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/torch_cpu.py (PyTorch fp32 restatement of the step), config 5 at {slots} slots: "
+                      f"{steps} timed mixed steps ({c5['tokens']} tokens, {c5['s_per_step']} s/step; 2,000 steps "
+                      f"extrapolated to {c5['extrapolated_2000_steps_s']} s) after contexts emulated in the pools",
+            "cpu_model": cpu_model_name(), "os_cpu_count": os.cpu_count(), "configs": legs}
 
 
 def main():
