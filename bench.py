@@ -196,6 +196,42 @@ def chunk_prefill_rate(torch, iters=10):
             "roof_tflops": round(ridge, 1), "roof_frac": round(tflops / ridge, 4)}
 
 
+def v10_leg(torch, slots=352, steps=60, warmup=10, seed=0, state_dtype="float32"):
+    """The config-5 mixed load on the released v10 geometry (8 q / 2 kv attention heads, vocab 248,320; 754.5M
+    parameters, docs/evaluation.json:623) instead of the BASELINE geometry: random-init weights, contexts
+    U{512, 2048, 8000} prefilled untimed, ``steps`` timed mixed steps through step_packed (no resets). Reported
+    apart from the headline, which is quoted on the BASELINE geometry."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    from hs_guard.synthetic import MixedServingLoad
+    dev = torch.device("cuda:0")
+    cfg = GuardConfig.v10()
+    model = GuardModel.random(cfg, seed=seed, device=dev, gen_device=dev)
+    eng = SlotStreamEngine(model, slots, state_dtype=state_dtype)
+    load = MixedServingLoad(slots=slots, vocab=cfg.vocab_size, seed=seed + 11, reset_p=0.0)
+    eng.step([(s, load.context()) for s in range(slots)])
+    mean, sd = 4.175 * slots, 9.48 * slots ** 0.5
+    eng.prepare(slots, range(slots, int(mean + 8 * sd) + 1, 16))
+    for _ in range(warmup):
+        eng.step(load.step_requests())
+    times, tokens = [], 0
+    for _ in range(steps):
+        req = load.step_requests()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.step_packed(req)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+        tokens += sum(len(ids) for _, ids in req)
+    out = {"geometry": "v10: hidden 1024, 24 layers 3 GDN:1 attn, GDN 16x128, attn 8q/2kv/256 window 512, MLP 3584, "
+                       "vocab 248320", "params": model.num_parameters(), "slots": slots, "steps": steps,
+           "tokens_per_s": round(tokens / (sum(times) / 1e3), 1), "p50": round(percentile(times, 50), 3),
+           "p95": round(percentile(times, 95), 3)}
+    del eng, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -520,6 +556,10 @@ def main():
     whole_ms = (time.perf_counter() - t0) / 3 * 1e3
     log(f"complete-message scorer, 8000 tokens: {whole_ms:.1f} ms")
 
+    del scorer
+    v10 = v10_leg(torch, slots=args.slots, seed=args.seed, state_dtype=args.state_dtype)
+    log(f"v10 geometry {v10}")
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
@@ -560,6 +600,7 @@ def main():
         "ring_decode_352": ring,
         "chunk_prefill_cfg4": chunk,
         "complete_message_8000": {"ms": round(whole_ms, 2), "tokens_per_s": round(8000 / whole_ms * 1e3, 1)},
+        "v10_geometry": v10,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -1,4 +1,5 @@
-"""Parity of the streaming step at the benchmark geometry (config 3) against the CPU oracle.
+"""Parity of the streaming step at the benchmark geometry (config 3) and the released v10 geometry against the CPU
+oracle.
 
 Geometry: GuardConfig.baseline() -- 24 layers [GDN, GDN, GDN, attention] x 6, hidden 1024, GDN 16 heads x 128,
 attention 16 q / 4 kv heads of 256 with a 512-token window, MLP 3584, vocab 151,936, random-init bf16 weights
@@ -26,14 +27,16 @@ pytestmark = pytest.mark.gpu
 FLOOR_FACTOR = 1.5
 
 
-@pytest.fixture(scope="module")
-def full():
+@pytest.fixture(scope="module", params=["baseline", "v10"])
+def full(request):
+    """The benchmark geometry at 8 slots, and the released v10 geometry (8 q / 2 kv heads, vocab 248,320,
+    docs/evaluation.json:623) at 4 slots."""
     from hs_guard.model import GuardConfig, GuardModel
-    print("[full] random-init baseline model", flush=True)
-    cfg = GuardConfig.baseline()
+    print(f"[full] random-init {request.param} model", flush=True)
+    cfg = getattr(GuardConfig, request.param)()
     model_cpu = GuardModel.random(cfg, seed=0, device="cpu")
     weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
-    return cfg, model_cpu.to("cuda:0"), weights
+    return cfg, model_cpu.to("cuda:0"), weights, (8 if request.param == "baseline" else 4)
 
 
 def _ticks(rng, vocab, slots=8):
@@ -43,7 +46,7 @@ def _ticks(rng, vocab, slots=8):
         ticks.append([(s, c[t0:t0 + 64]) for s, c in enumerate(ctx) if t0 < len(c)])
     for _ in range(4):
         ticks.append([(s, [int(rng.integers(0, vocab))]) for s in range(slots)])
-    ticks.append([(s, rng.integers(0, vocab, n).tolist()) for s, n in enumerate((1, 2, 5, 17, 64, 1, 3, 9))])
+    ticks.append([(s, rng.integers(0, vocab, n).tolist()) for s, n in enumerate((1, 2, 5, 17, 64, 1, 3, 9)[:slots])])
     return ticks
 
 
@@ -57,13 +60,13 @@ def test_baseline_geometry_matches_oracle(full):
     from hs_guard.engine.slot_engine import SlotStreamEngine
     from oracle.backbone import StreamOracle
     from oracle.bf16 import perturbed
-    cfg, model, weights = full
-    eng = SlotStreamEngine(model, 8, use_graphs=False)
-    orc = StreamOracle(weights, cfg, 8, gdn="chunk")
-    twin = StreamOracle(weights, cfg, 8, gdn="chunk")
+    cfg, model, weights, slots = full
+    eng = SlotStreamEngine(model, slots, use_graphs=False)
+    orc = StreamOracle(weights, cfg, slots, gdn="chunk")
+    twin = StreamOracle(weights, cfg, slots, gdn="chunk")
     gemm = matched_gemm(eng)
     hip, floor = [], []
-    for t, tick in enumerate(_ticks(np.random.default_rng(0), cfg.vocab_size)):
+    for t, tick in enumerate(_ticks(np.random.default_rng(0), cfg.vocab_size, slots)):
         got = eng.step(tick)
         ref = orc.step(tick, gemm=gemm)
         with perturbed(1):
@@ -75,10 +78,11 @@ def test_baseline_geometry_matches_oracle(full):
     W = cfg.window_tokens
     np.testing.assert_array_equal(eng.length, orc.length)
     np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
-    assert (orc.ring_pos[:8, :W] >= 0).all() and (orc.length > W).all()     # every ring has wrapped
+    assert (orc.ring_pos[:slots, :W] >= 0).all() and (orc.length > W).all()     # every ring has wrapped
     rec = eng.rec.double().cpu().numpy()
-    rel = [np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s]) for s in range(8)]
-    rel_twin = [np.linalg.norm(twin.rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s]) for s in range(8)]
+    rel = [np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s]) for s in range(slots)]
+    rel_twin = [np.linalg.norm(twin.rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
+                for s in range(slots)]
     print(f"[full] state rel err: engine {max(rel):.1e}, perturbed oracle {max(rel_twin):.1e}", flush=True)
     hip, floor = np.concatenate(hip), np.concatenate(floor)
     stats = {name: (fn(hip), fn(floor)) for name, fn in (("p50", np.median), ("p99", lambda x: np.quantile(x, 0.99)),
