@@ -14,7 +14,7 @@
 // applied in order).
 //
 // Only the last three lines involve the state. gdn_chunk_prep_kernel computes everything else for every
-// (row, chunk, value head) at once, in parallel: M' and P as bf16 hi / lo planes and the per-token factors
+// (row, chunk, value head) at once, in parallel: M' and P as scaled fp16 hi / lo planes and the per-token factors
 // e^G rk, rq e^G, rk e^(G_C-G) and e^(G_C), into a workspace. gdn_chunk_state_kernel then walks each row's
 // chunks in order with only the state products on its chain: per chunk Y = Kr S and Qr S, Z = Vr - e^G rk . Y,
 // V' = M' Z (no substitution chain: M' is explicit), O, and the state update.
@@ -28,19 +28,25 @@
 // block and keeps S[:, those columns] (128 x 16 fp32) in MFMA accumulator layout for the whole sequence, so the
 // state is read once and written once per call; output wave 4 + w computes Q S and O for the same columns from
 // the split S and V' the chain wave hands over through LDS. The accumulator layout of a 16-row block (lane l:
-// column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of v_mfma_f32_16x16x16_bf16, so S, Z and V'
-// feed the next product from registers; pairs of 16-row blocks feed v_mfma_f32_16x16x32_bf16 by ordering its
+// column l%16, rows 4(l/16)..+3) is exactly the B-operand layout of a 16x16x16 MFMA, so S, Z and V'
+// feed the next product from registers; pairs of 16-row blocks feed v_mfma_f32_16x16x32_f16 by ordering its
 // 32 reduction slots as (4 rows of block J, 4 rows of block J+1) per lane, with the A operand read in the same
 // order.
-// Precision: Kr, Qr, Vr are exact bf16 operands. Every fp32 operand on the state path (S, -A, M', P, the
-// diagonal inverses, Z, V') is split into bf16 hi + lo and multiplied in three passes (hi.hi + hi.lo + lo.hi,
-// error ~2^-16 relative), or two when the other operand is exact bf16, so the state keeps fp32-level accuracy.
+// Precision: Kr, Qr, Vr are exact bf16 values (and exact in fp16, which holds bf16's 8-bit significands). The
+// prep kernel forms M' in fp32 throughout (fp32 MFMA for the block substitution). On the state path every fp32
+// operand (S, Z, V', W, and the M', P planes) is scaled by a power of two that puts its largest magnitude just
+// below 2^14, then split into fp16 hi + fp16 lo of the remainder (x 2^s = hi + lo + O(2^-22 |x 2^s|)), and
+// multiplied in three fp16 MFMA passes (lo.hi + hi.lo + hi.hi), or two when the other operand is an exact
+// input row; the accumulator is scaled back by 2^-s (exact). That keeps every product within ~2^-22 of fp32
+// (a bf16 hi + lo split reaches only ~2^-17, which moved one bf16 output in 300 instead of one in 10,000).
 // Two code-generation rules these kernels keep on gfx950:
 //   * one MFMA accumulation chain uses one MFMA shape: a 16x16x16 product accumulating directly onto the
 //     result of a 16x16x32 product lost part of that result (found by bisecting a wrong output), so odd
 //     blocks are zero-padded 16x16x32 products;
 //   * the global prefetch is unconditional (clamped row pointer): a conditional load was compiled as a load
-//     through a selected pointer to a stack zero, which forced a full memory wait every chunk.
+//     through a selected pointer to a stack zero, which forced a full memory wait every chunk;
+//   * every value one lane stores to LDS and another lane of the same wave reads passes a fenced barrier in
+//     between: the compiler orders LDS accesses per lane only, and moved a read above another lane's store.
 #include <math.h>
 
 #include "hsg_common.h"
@@ -53,22 +59,26 @@ constexpr int VD = 128;
 constexpr int CH = 64;             // tokens per chunk
 constexpr int BV = 64;             // value columns per workgroup
 constexpr int KS = KD + 8;         // Ks / Qs row stride (bf16): token-major rows of keys
-constexpr int TS = CH + 4;         // row stride (bf16) of the prep kernel's -A plane in LDS
+constexpr int AS = CH + 4;         // row stride (fp32) of the prep kernel's -A in LDS: a row read of 16 lanes x
+                                   // 4 k-slots hits 64 distinct banks
 constexpr int VS = BV + 16;        // Vs row stride (bf16): 40 dwords, so the 4 x 4 pieces of a transpose read
                                    // fall in 16 distinct bank pairs
 constexpr int DS = 20;             // diagonal-block row stride (fp32) and diagonal-inverse row stride (bf16)
 constexpr int PW = CH;             // row width (bf16) of the workspace planes M', P (swizzled rows, see swz)
 constexpr int PL = CH * PW;        // one 64 x 64 bf16 plane of the workspace (also the state kernel's LDS layout)
 constexpr int VEC = 256;           // per-token factor floats of a workspace unit: e^G rk, rq e^G, rk e^(G_C-G),
-                                   // then e^(G_C) and padding
+                                   // then e^(G_C), the inverse scale of the M' planes and padding
 // one workspace unit per (row, chunk, value head): planes M'hi, M'lo, Phi, Plo, then the factors
 constexpr int UNIT_BYTES = 4 * PL * 2 + VEC * 4;
 constexpr int ORDER_MAX = 4096;    // rows ranked by the order kernel (more rows keep their given order)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 typedef __attribute__((ext_vector_type(8))) short s16x8;
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) float f32x8;
 
 struct ChunkParams {
   const uint16_t* qkv;
@@ -101,68 +111,72 @@ struct ChunkParams {
   uint16_t* out;
 };
 
-__device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
+// bf16 operands (the prep kernel's Gram tiles of the raw rows)
 __device__ __forceinline__ f32x4 mma32(s16x8 a, s16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                  c, 0, 0, 0);
 }
 
-__device__ __forceinline__ s16x8 cat(s16x4 x, s16x4 y) { return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7); }
-
-// x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), both round-to-nearest-even, on the packed hardware
-// conversion (three VALU instructions per element instead of seven for the integer rounding)
-__device__ __forceinline__ void split4(f32x4 x, s16x4& hi, s16x4& lo) {
-  const uint32_t h01 = pack_bf16x2(x[0], x[1]), h23 = pack_bf16x2(x[2], x[3]);
-  const uint32_t l01 = pack_bf16x2(x[0] - __uint_as_float(h01 << 16), x[1] - __uint_as_float(h01 & 0xffff0000u));
-  const uint32_t l23 = pack_bf16x2(x[2] - __uint_as_float(h23 << 16), x[3] - __uint_as_float(h23 & 0xffff0000u));
-  hi = __builtin_bit_cast(s16x4, (uint64_t)h01 | ((uint64_t)h23 << 32));
-  lo = __builtin_bit_cast(s16x4, (uint64_t)l01 | ((uint64_t)l23 << 32));
+// fp16 operands (the state kernel's products)
+__device__ __forceinline__ f32x4 mmh32(s16x8 a, s16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
 }
+
+// fp32 operands, one k-slot per lane group (the prep kernel's block substitution): lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16] of a 16 x 4 by 4 x 16 product
+__device__ __forceinline__ f32x4 mmf4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// 2^e as a float and its inverse, e chosen so that amax * 2^e lies in [2^13, 2^14): the scaled values stay well inside
+// fp16's range (65504) and the fp16 remainders of all values down to ~2^-17 of the largest stay normal. amax 0, NaN
+// or infinite: scale 1. e is clamped to [-100, 100].
+__device__ __forceinline__ float pow2_scale(float amax, float* inv) {
+  int e = 0;
+  if (amax > 0.f && amax < INFINITY) e = 140 - (int)((__float_as_uint(amax) >> 23) & 0xffu);
+  e = e < -100 ? -100 : (e > 100 ? 100 : e);
+  *inv = __uint_as_float((uint32_t)(127 - e) << 23);
+  return __uint_as_float((uint32_t)(127 + e) << 23);
+}
+
+// y = x * scale (scale a power of two) as fp16 hi + fp16 lo of the remainder: y = hi + lo + O(2^-22 |y|)
+__device__ __forceinline__ void split4h(f32x4 x, float scale, s16x4& hi, s16x4& lo) {
+  const f32x4 y = x * scale;
+  const f16x4 h = __builtin_convertvector(y, f16x4);
+  const f16x4 l = __builtin_convertvector(y - __builtin_convertvector(h, f32x4), f16x4);
+  hi = __builtin_bit_cast(s16x4, h);
+  lo = __builtin_bit_cast(s16x4, l);
+}
+
+__device__ __forceinline__ float absmax4(f32x4 x, float m) {
+  return fmaxf(fmaxf(m, fmaxf(fabsf(x[0]), fabsf(x[1]))), fmaxf(fabsf(x[2]), fabsf(x[3])));
+}
+
+// 8 raw bf16 values (one 16-byte piece of a K or Q row) as 8 fp16 values: exact, fp16 holds bf16's significands
+// (magnitudes below 2^-14 become fp16 subnormals; their products are below fp32 resolution of the sums they join)
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 w) {
+  f32x8 f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+  return __builtin_bit_cast(u32x4, __builtin_convertvector(f, f16x8));
+}
+
+__device__ __forceinline__ s16x8 cat(s16x4 x, s16x4 y) { return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7); }
 
 __device__ __forceinline__ f32x4 ld4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ s16x4 ld4h(const uint16_t* p) { return *reinterpret_cast<const s16x4*>(p); }
 
-// acc += sum_{J < NJ} M[row block I][col block J] . B_J for a matrix M kept in LDS as bf16 hi / lo planes, read
-// at hrow = &Mh[16I + m][4 g], lrow = &Ml[16I + m][4 g] (lane m = l%16, g = l/16); B_J are split bf16 pairs in
-// B layout. Three passes per product (hi.hi + hi.lo + lo.hi). TR: the same operands with the MFMA operand
-// order swapped, which yields the transposed product (sum_J B_J^T M_IJ^T) in accumulator layout.
-template <int NJ, bool TR = false>
-__device__ __forceinline__ f32x4 split_product(const uint16_t* hrow, const uint16_t* lrow, const s16x4* bh,
-                                               const s16x4* bl, f32x4 acc) {
-  auto mm = [](s16x8 m, s16x8 b, f32x4 c) { return TR ? mma32(b, m, c) : mma32(m, b, c); };
-#pragma unroll
-  for (int J = 0; J + 1 < NJ; J += 2) {
-    const s16x8 ah = cat(ld4h(hrow + 16 * J), ld4h(hrow + 16 * J + 16));
-    const s16x8 al = cat(ld4h(lrow + 16 * J), ld4h(lrow + 16 * J + 16));
-    const s16x8 b_h = cat(bh[J], bh[J + 1]), b_l = cat(bl[J], bl[J + 1]);
-    acc = mm(al, b_h, acc);
-    acc = mm(ah, b_l, acc);
-    acc = mm(ah, b_h, acc);
-  }
-  if constexpr (NJ % 2 == 1) {
-    // the odd block rides in a 16x16x32 product with zero upper k-slots: one accumulation chain never mixes
-    // MFMA shapes (a 16x16x16 accumulating onto a 16x16x32 result lost that result in some rows)
-    constexpr int J = NJ - 1;
-    const s16x4 z = {0, 0, 0, 0};
-    const s16x8 ah = cat(ld4h(hrow + 16 * J), z), al = cat(ld4h(lrow + 16 * J), z);
-    const s16x8 b_h = cat(bh[J], z), b_l = cat(bl[J], z);
-    acc = mm(al, b_h, acc);
-    acc = mm(ah, b_l, acc);
-    acc = mm(ah, b_h, acc);
-  }
-  return acc;
-}
-
-// e^x for x <= 0 on the hardware exp2 (v_exp_f32, 1 ulp): 2^(x log2 e)
-__device__ __forceinline__ float exp_nonpos(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-
-__device__ __forceinline__ void store_split(uint16_t* hi, uint16_t* lo, float x) {
-  const uint32_t h = pack_bf16x2(x, 0.f);
-  *hi = (uint16_t)h;
-  *lo = (uint16_t)pack_bf16x2(x - __uint_as_float(h << 16), 0.f);
+// e^x for x <= 0 given in fp64, on the hardware exp2 (v_exp_f32, 1 ulp): x log2 e = n + f is split in fp64 (n
+// integer, 0 <= f < 1) and e^x = 2^f 2^n, so the fp32 rounding of the argument costs ~2^-25 relative whatever |x|
+// is (rounding x log2 e itself to fp32 costs ~|x| 2^-24, 3e-6 at |x| = 50)
+__device__ __forceinline__ float exp_nonpos_d(double x) {
+  const double y = x * 1.4426950408889634;
+  const double n = floor(y);
+  return ldexpf(__builtin_amdgcn_exp2f((float)(y - n)), (int)n);
 }
 
 // workgroup barrier that orders LDS only (outstanding global prefetches stay in flight)
@@ -192,12 +206,17 @@ __device__ __forceinline__ int swz_at(int r, int c) { return r * KD + 4 * (c ^ s
 // the same for the 64-column planes M' and P (16 pieces per row; the XOR permutes all of them)
 __device__ __forceinline__ int pw_at(int r, int c) { return r * PW + 4 * (c ^ swz(r)); }
 
-// split_product on a swizzled plane pair: hrow / lrow = row 16 I + m of the hi / lo planes, po[J] = offset of
-// the lane's logical piece 4 J + g in that row (rows 16 I + m share swz(m))
+// acc += sum_{J < NJ} M[row block I][col block J] . B_J for a matrix M kept in LDS as scaled fp16 hi / lo planes
+// (swizzled rows): hrow / lrow = row 16 I + m of the hi / lo planes, po[J] = offset of the lane's logical piece
+// 4 J + g in that row (rows 16 I + m share swz(m)); B_J are scaled fp16 hi / lo pairs in B layout. Three passes per
+// product (lo.hi + hi.lo + hi.hi). TR: the same operands with the MFMA operand order swapped, which yields the
+// transposed product (sum_J B_J^T M_IJ^T) in accumulator layout. The odd block rides in a 16x16x32 product with
+// zero upper k-slots: one accumulation chain never mixes MFMA shapes (a 16x16x16 accumulating onto a 16x16x32
+// result lost that result in some rows).
 template <int NJ, bool TR = false>
 __device__ __forceinline__ f32x4 split_product_sw(const uint16_t* hrow, const uint16_t* lrow, const int* po,
                                                   const s16x4* bh, const s16x4* bl, f32x4 acc) {
-  auto mm = [](s16x8 m, s16x8 b, f32x4 c) { return TR ? mma32(b, m, c) : mma32(m, b, c); };
+  auto mm = [](s16x8 m, s16x8 b, f32x4 c) { return TR ? mmh32(b, m, c) : mmh32(m, b, c); };
 #pragma unroll
   for (int J = 0; J + 1 < NJ; J += 2) {
     const s16x8 ah = cat(ld4h(hrow + po[J]), ld4h(hrow + po[J + 1]));
@@ -269,14 +288,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
   uint16_t* Pl_g = Mh_g + 3 * PL;
   float* vec_g = reinterpret_cast<float*>(unit + 4 * PL * 2);
 
-  // Ks is reused for the M' output planes and Qs for -A once the Gram tiles are done (a barrier apart)
+  // Once the Gram tiles are done (a barrier apart) Qs holds -A in fp32 and Ks the substitution's M blocks in fp32,
+  // then the M' output planes
   __shared__ __align__(16) uint16_t Ks[CH * KS];
   __shared__ __align__(16) uint16_t Qs[CH * KS];
-  uint16_t* const Ah = Qs;                                       // -A (strictly lower), bf16 hi / lo
-  uint16_t* const Al = Qs + CH * TS;
+  float* const nA = reinterpret_cast<float*>(Qs);                // -A (strictly lower), fp32, row stride AS
   __shared__ __align__(16) float Dg[4 * 16 * DS];                // fp32 diagonal 16 x 16 blocks of -A
-  __shared__ __align__(16) uint16_t Th[CH * DS], Tl[CH * DS];    // their inverses (rows 16w + i of block w)
-  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], G_s[CH], fa_s[CH];
+  __shared__ __align__(16) float Tf[CH * DS];                    // their inverses, fp32 (rows 16w + i of block w)
+  __shared__ __align__(16) float rk_s[CH], rq_s[CH], g_s[CH], b_s[CH], fa_s[CH];
+  __shared__ __align__(16) double G_s[CH];   // in-chunk cumulative log-decay (see the scan below)
+  __shared__ float red_s[4];
 
   // ---- stage token st_t: raw K, Q rows into LDS, l2-norm factors, gates. Past the row's end the chunk's
   // first token is read instead and its zero beta, rk and rq cancel it everywhere. ----
@@ -327,22 +348,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
   }
   lds_barrier();
 
-  // ---- in-chunk cumulative decay and the per-token factors (wave 0) ----
+  // ---- in-chunk cumulative decay and the per-token factors (wave 0). G is summed, differenced and exponentiated
+  // in fp64 (exp_nonpos_d): |G| reaches ~50 within a chunk, where an fp32 sum carries ~4e-6 absolute error, and
+  // every e^(G_i - G_j) of A and P would inherit it as relative error even between neighbouring tokens (the
+  // recurrence applies each token's decay on its own, with no such loss). Emulated in fp64 on the test inputs, the
+  // fp32 G alone moves ~3e-4 of the bf16 outputs, against ~2e-5 for the rest of the chunk form in fp32. ----
   if (wave == 0) {
-    float x = g_s[lane];
+    double x = g_s[lane];
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      const float y = __shfl_up(x, d, 64);
+      const double y = __shfl_up(x, d, 64);
       if (lane >= d) x += y;
     }
-    const float GC = __shfl(x, 63, 64);
-    const float eg = exp_nonpos(x);
+    const double GC = __shfl(x, 63, 64);
+    const float eg = exp_nonpos_d(x);
     G_s[lane] = x;
     fa_s[lane] = b_s[lane] * rk_s[lane];
     vec_g[lane] = eg * rk_s[lane];
     vec_g[CH + lane] = rq_s[lane] * eg;
-    vec_g[2 * CH + lane] = rk_s[lane] * exp_nonpos(GC - x);
-    vec_g[3 * CH + lane] = lane == 0 ? exp_nonpos(GC) : 0.f;
+    vec_g[2 * CH + lane] = rk_s[lane] * exp_nonpos_d(GC - x);
+    if (lane != 1) vec_g[3 * CH + lane] = lane == 0 ? exp_nonpos_d(GC) : 0.f;   // lane 1 later: M''s inverse scale
   }
 
   // ---- Kr Kr^T and Qr Kr^T on the 10 lower 16 x 16 tiles each; tile u of wave w is number w + 4u. Each
@@ -366,12 +391,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
   }
   lds_barrier();  // per-token factors are in LDS; Qs is free for -A
 
-  // ---- scale the Gram tiles into -A (LDS) and P (workspace). Only P's diagonal tiles need the causal mask:
-  // the substitution reads A's off-diagonal tiles only and the diagonal inverses read below the diagonal only;
-  // P's tiles above the diagonal are never read. ----
+  // ---- scale the Gram tiles into -A (LDS, fp32) and P (workspace: fp16 hi / lo planes of P 2^sP). Only P's
+  // diagonal tiles need the causal mask: the substitution reads A's off-diagonal tiles only and the diagonal
+  // inverses read below the diagonal only; P's tiles above the diagonal are never read. |P| <= scale (unit q and
+  // k directions, decays <= 1), so its power-of-two scale follows from the scale alone. ----
   {
-    float fr[5], Gr[5];
-    f32x4 rkc[5], Gc[5];
+    float inv_p;
+    const float sp = pow2_scale(p.scale, &inv_p);
+    float fr[5];
+    double Gr[5], Gc[5][4];
+    f32x4 rkc[5];
 #pragma unroll
     for (int u = 0; u < 5; ++u) {
       const int tau = wave + 4 * u;
@@ -384,7 +413,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
       fr[u] = qk ? rq_s[i] : fa_s[i];
       Gr[u] = G_s[i];
       rkc[u] = ld4f(&rk_s[j0]);
-      Gc[u] = ld4f(&G_s[j0]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Gc[u][r] = G_s[j0 + r];
     }
 #pragma unroll
     for (int u = 0; u < 5; ++u) {
@@ -398,17 +428,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
       f32x4 v;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        v[r] = fr[u] * rkc[u][r] * exp_nonpos(fminf(Gr[u] - Gc[u][r], 0.f)) * gt[u][r];
+        v[r] = fr[u] * rkc[u][r] * exp_nonpos_d(fmin(Gr[u] - Gc[u][r], 0.0)) * gt[u][r];
         // inside a diagonal tile of P keep row >= column (sign bit of column - row - 1)
         if (qk && I == J) v[r] *= (float)((uint32_t)((4 * g4 + r) - m16 - 1) >> 31);
       }
-      s16x4 vh, vl;
-      split4(qk ? v : -v, vh, vl);
       if (!qk) {
-        *reinterpret_cast<s16x4*>(&Ah[i * TS + j0]) = vh;
-        *reinterpret_cast<s16x4*>(&Al[i * TS + j0]) = vl;
+        *reinterpret_cast<f32x4*>(&nA[i * AS + j0]) = -v;
         if (I == J) *reinterpret_cast<f32x4*>(&Dg[i * DS + 4 * g4]) = -v;
       } else {
+        s16x4 vh, vl;
+        split4h(v, sp, vh, vl);
         *reinterpret_cast<s16x4*>(&Ph_g[pw_at(i, j0 >> 2)]) = vh;
         *reinterpret_cast<s16x4*>(&Pl_g[pw_at(i, j0 >> 2)]) = vl;
       }
@@ -433,44 +462,76 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
       }
       t[i] = (s0 + s1) + (s2 + s3);
     }
-    // every lane group computed the same column; group g4 writes rows 4 g4 .. 4 g4 + 3 of it
+    // every lane group computed the same column; group 0 writes it (constant indices only: a select of t[4 g4 + i]
+    // by lane group was lowered to branches over a scratch copy of t and stored row 11 as row 15)
+    if (g4 == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ti = g4 == 0 ? t[i] : g4 == 1 ? t[4 + i] : g4 == 2 ? t[8 + i] : t[12 + i];
-      store_split(&Th[(wave * 16 + 4 * g4 + i) * DS + m16], &Tl[(wave * 16 + 4 * g4 + i) * DS + m16], ti);
+      for (int i = 0; i < 16; ++i) Tf[(wave * 16 + i) * DS + m16] = t[i];
     }
   }
   lds_barrier();  // diagonal inverses are complete
 
-  // ---- M_I = T_II (E_I - sum_{J<I} A_IJ M_J) for this wave's columns 16w + m16 (E = identity), then
-  // M' = M diag(beta), transposed through LDS (the Ks area) into 16-byte stores to the workspace ----
-  uint16_t* const Mh_s = Ks;
-  uint16_t* const Ml_s = Ks + PL;
+  // ---- M_I = T_II (E_I + sum_{J<I} (-A)_IJ M_J) for this wave's columns 16w + m16 (E = identity), in fp32 on
+  // 16x16x4 fp32 MFMAs (lane: row / column m16, k-slot g4). Every operand is read back in B layout by other lanes
+  // of the wave, so each block goes through LDS: x_I in the wave's 16 x 16 slice of Dg (free once the diagonal
+  // inverses are done), M_I in its 64 x 16 slice of Ks. Each hand-off is a fenced workgroup barrier (all waves run
+  // this loop): without an ordering point the compiler may hoist a lane's read of M_J above the stores of other
+  // lanes whenever the lane's own store addresses provably differ, and the read then returns the stale x_J.
+  // Then M' = M diag(beta). ----
+  float* const Mf = reinterpret_cast<float*>(Ks) + wave * (CH * 16);
+  float* const Xf = Dg + wave * (16 * DS);
+  f32x4 mp[4];
   {
     const float bcol = b_s[16 * wave + m16];
-    s16x4 Mh[4], Ml[4];
+    float amax = 0.f;
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const int arow = (16 * I + m16) * TS + 4 * g4;
-      if (I == 1) acc = split_product<1>(Ah + arow, Al + arow, Mh, Ml, acc);
-      if (I == 2) acc = split_product<2>(Ah + arow, Al + arow, Mh, Ml, acc);
-      if (I == 3) acc = split_product<3>(Ah + arow, Al + arow, Mh, Ml, acc);
-      f32x4 x;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = acc[r] + ((I == wave && 4 * g4 + r == m16) ? 1.f : 0.f);
-      s16x4 xh, xl;
-      split4(x, xh, xl);
-      const s16x4 th = ld4h(&Th[(I * 16 + m16) * DS + 4 * g4]), tl = ld4h(&Tl[(I * 16 + m16) * DS + 4 * g4]);
+      for (int J = 0; J < I; ++J)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = 16 * J + 4 * j + g4;
+          acc = mmf4(nA[(16 * I + m16) * AS + k], Mf[k * 16 + m16], acc);
+        }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[r] += (I == wave && 4 * g4 + r == m16) ? 1.f : 0.f;
+        Xf[(4 * g4 + r) * DS + m16] = acc[r];
+      }
+      lds_barrier();   // x_I is complete (and the previous block's reads of Xf are done)
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      v = mma16(tl, xh, v);
-      v = mma16(th, xl, v);
-      v = mma16(th, xh, v);
-      split4(v, Mh[I], Ml[I]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v = mmf4(Tf[(16 * I + m16) * DS + 4 * j + g4], Xf[(4 * j + g4) * DS + m16], v);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Mf[(16 * I + 4 * g4 + r) * 16 + m16] = v[r];
+      lds_barrier();   // M_I is complete before the next block reads it, and x_I has been read
+      mp[I] = v * bcol;
+      amax = absmax4(mp[I], amax);
+    }
+    amax = wave_max(amax);
+    if (lane == 0) red_s[wave] = amax;
+  }
+  lds_barrier();  // every wave's M' block is done (Ks is free for the planes) and its largest magnitude is in red_s
+
+  // ---- M' 2^sM as fp16 hi / lo planes, transposed through LDS (the Ks area) into 16-byte stores to the
+  // workspace; the inverse scale 2^-sM goes to the factor area ----
+  uint16_t* const Mh_s = Ks;
+  uint16_t* const Ml_s = Ks + PL;
+  {
+    float inv_m;
+    const float sm = pow2_scale(fmaxf(fmaxf(red_s[0], red_s[1]), fmaxf(red_s[2], red_s[3])), &inv_m);
+    if (threadIdx.x == 1) vec_g[3 * CH + 1] = inv_m;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      s16x4 hi, lo;
+      split4h(mp[I], sm, hi, lo);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int at = pw_at(16 * I + 4 * g4 + r, 4 * wave + (m16 >> 2)) + (m16 & 3);
-        store_split(&Mh_s[at], &Ml_s[at], v[r] * bcol);
+        Mh_s[at] = (uint16_t)hi[r];
+        Ml_s[at] = (uint16_t)lo[r];
       }
     }
   }
@@ -564,7 +625,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
   __shared__ __align__(16) uint16_t Ks[2][CH * KD];
   __shared__ __align__(16) uint16_t Qs[CH * KD];
   __shared__ __align__(16) uint16_t Vs[CH * VS];
-  // M' and P (two buffers) as bf16 hi / lo planes of swizzled token-major rows (lower triangles used)
+  // M' and P (two buffers) as scaled fp16 hi / lo planes of swizzled token-major rows (lower triangles used)
   __shared__ __align__(16) uint16_t Ms[2 * PL];
   __shared__ __align__(16) uint16_t Ps[2][2 * PL];
   __shared__ __align__(16) float vec_s[2][VEC];
@@ -572,6 +633,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
   // Sx[w][2 mt + hl] = split S block mt of column group w, Vx[w][2 I + hl] = split V' token block I
   __shared__ __align__(16) uint16_t Sx[4 * 16 * XP];
   __shared__ __align__(16) uint16_t Vx[4 * 8 * XP];
+  // the inverse power-of-two scales of the handed-over S and V' fragments, per column group
+  __shared__ float s_inv[4], v_inv[4];
 
   // ---- state S[:, vcol] in accumulator layout (chain waves): block mt holds keys 16 mt + 4 g4 + r ----
   ST* sbase = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * (int64_t)KD) * VD + vcol;
@@ -628,13 +691,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
   const bool third = rx + 512 < 2 * TRI_SLOTS;
   auto row_of = [&](int c0) { return p.qkv + (tok0 + (c0 + st_t < ntok ? c0 + st_t : 0)) * p.qkv_stride; };
   // 16-byte piece j of a K / Q row holds logical 8-byte pieces 2j, 2j + 1: it lands in 16-byte slot
-  // j ^ (swz >> 1), its halves exchanged when swz is odd
+  // j ^ (swz >> 1), its halves exchanged when swz is odd. The raw bf16 values are staged as fp16 (exact).
   auto stage_rows = [&](uint16_t* tile, const u32x4* pr) {
     const int sg = swz(st_t);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int at = st_t * KD + 8 * ((sp + 4 * j) ^ (sg >> 1));
-      *reinterpret_cast<u32x4*>(&tile[at]) = (sg & 1) ? pr[j].zwxy : pr[j];
+      const u32x4 h = bf16x8_to_f16x8(pr[j]);
+      *reinterpret_cast<u32x4*>(&tile[at]) = (sg & 1) ? h.zwxy : h;
     }
   };
   uint16_t* const sx = Sx + w * 16 * XP + 4 * lane;
@@ -669,17 +733,25 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
       const float* const vec = vec_s[cb];
       // the next chunk (or this one again after the last: staged into idle buffers and never read)
       fetch(c0 + CH < ntok ? c0 + CH : c0);
+      // S 2^sS as fp16 hi / lo (sS from the largest |S| of this wave's 16 columns), handed over with 2^-sS
       s16x4 Sh[8], Sl[8];
+      float amax = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) amax = absmax4(S[mt], amax);
+      float inv_s;
+      const float ss = pow2_scale(wave_max(amax), &inv_s);
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
-        split4(S[mt], Sh[mt], Sl[mt]);
+        split4h(S[mt], ss, Sh[mt], Sl[mt]);
         *reinterpret_cast<s16x4*>(sx + (2 * mt) * XP) = Sh[mt];
         *reinterpret_cast<s16x4*>(sx + (2 * mt + 1) * XP) = Sl[mt];
       }
+      if (lane == 0) s_inv[w] = inv_s;
       lds_barrier();  // B1: split S handed over
 
       // ---- Y = Kr S for this wave's 16 value columns: S split hi / lo, key blocks paired ----
       f32x4 Y[4];
+      float inv_mz;
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         f32x4 y = {0.f, 0.f, 0.f, 0.f};
@@ -688,25 +760,34 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
           const int a0 = yo[2 * (q2 & 1)] + 64 * (q2 >> 1) + 16 * I * KD;
           const int a1 = yo[2 * (q2 & 1) + 1] + 64 * (q2 >> 1) + 16 * I * KD;
           const s16x8 ka = cat(ld4h(K_ + a0), ld4h(K_ + a1));
-          y = mma32(ka, cat(Sl[2 * q2], Sl[2 * q2 + 1]), y);
-          y = mma32(ka, cat(Sh[2 * q2], Sh[2 * q2 + 1]), y);
+          y = mmh32(ka, cat(Sl[2 * q2], Sl[2 * q2 + 1]), y);
+          y = mmh32(ka, cat(Sh[2 * q2], Sh[2 * q2 + 1]), y);
         }
-        Y[I] = y;
+        Y[I] = y * inv_s;
       }
       // ---- Z = Vr - e^G rk . Y, split (V[16 I + 4 g4 + r][column 16 w + m16] by a transpose read) ----
       s16x4 Zh[4], Zl[4];
-      const uint16_t* vfrag = Vs + (4 * g4 + (m16 >> 2)) * VS + w * 16 + 4 * (m16 & 3);
+      {
+        const uint16_t* vfrag = Vs + (4 * g4 + (m16 >> 2)) * VS + w * 16 + 4 * (m16 & 3);
+        f32x4 z[4];
+        float zmax = 0.f;
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        const f32x4 e1 = ld4f(&vec[16 * I + 4 * g4]);
-        const s16x4 v4 = ld4h_tr(vfrag + 16 * I * VS);
-        f32x4 z;
+        for (int I = 0; I < 4; ++I) {
+          const f32x4 e1 = ld4f(&vec[16 * I + 4 * g4]);
+          const s16x4 v4 = ld4h_tr(vfrag + 16 * I * VS);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) z[r] = bf2f((uint16_t)v4[r]) - e1[r] * Y[I][r];
-        split4(z, Zh[I], Zl[I]);
+          for (int r = 0; r < 4; ++r) z[I][r] = bf2f((uint16_t)v4[r]) - e1[r] * Y[I][r];
+          zmax = absmax4(z[I], zmax);
+        }
+        float inv_z;
+        const float sz = pow2_scale(wave_max(zmax), &inv_z);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) split4h(z[I], sz, Zh[I], Zl[I]);
+        inv_mz = vec[3 * CH + 1] * inv_z;   // the M' planes' inverse scale times Z's
       }
       // ---- V'_I = sum_{J<=I} M'_IJ Z_J (M' lower triangular), handed over split ----
       f32x4 Vp[4];
+      float vmax = 0.f;
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -716,18 +797,38 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         if (I == 1) acc = split_product_sw<2>(mh, ml, po, Zh, Zl, acc);
         if (I == 2) acc = split_product_sw<3>(mh, ml, po, Zh, Zl, acc);
         if (I == 3) acc = split_product_sw<4>(mh, ml, po, Zh, Zl, acc);
-        Vp[I] = acc;
-        s16x4 vh, vl;
-        split4(acc, vh, vl);
-        *reinterpret_cast<s16x4*>(vx + (2 * I) * XP) = vh;
-        *reinterpret_cast<s16x4*>(vx + (2 * I + 1) * XP) = vl;
+        Vp[I] = acc * inv_mz;
+        vmax = absmax4(Vp[I], vmax);
+      }
+      {
+        float inv_v;
+        const float sv = pow2_scale(wave_max(vmax), &inv_v);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          s16x4 vh, vl;
+          split4h(Vp[I], sv, vh, vl);
+          *reinterpret_cast<s16x4*>(vx + (2 * I) * XP) = vh;
+          *reinterpret_cast<s16x4*>(vx + (2 * I + 1) * XP) = vl;
+        }
+        if (lane == 0) v_inv[w] = inv_v;
       }
       lds_barrier();  // B2: split V' handed over; Q, V and M' of this chunk are no longer read
 
       // ---- S <- e^(G_C) S + Kr^T W,  W = rk e^(G_C - G) . V' (token blocks paired) ----
       s16x4 Wh[4], Wl[4];
+      float inv_w;
+      {
+        f32x4 wv[4];
+        float wmax = 0.f;
 #pragma unroll
-      for (int J = 0; J < 4; ++J) split4(Vp[J] * ld4f(&vec[2 * CH + 16 * J + 4 * g4]), Wh[J], Wl[J]);
+        for (int J = 0; J < 4; ++J) {
+          wv[J] = Vp[J] * ld4f(&vec[2 * CH + 16 * J + 4 * g4]);
+          wmax = absmax4(wv[J], wmax);
+        }
+        const float sw = pow2_scale(wave_max(wmax), &inv_w);
+#pragma unroll
+        for (int J = 0; J < 4; ++J) split4h(wv[J], sw, Wh[J], Wl[J]);
+      }
       const float gc = vec[3 * CH];
       // K^T operand: lane m16 of group g4 gets key 16 mt + m16 of tokens 16 J + 4 g4 .. +3 (transpose read)
 #pragma unroll
@@ -737,10 +838,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
 #pragma unroll
         for (int J = 0; J < 4; J += 2) {
           const s16x8 ka = cat(ld4h_tr(K_ + ka0 + 16 * J * KD), ld4h_tr(K_ + ka0 + 16 * (J + 1) * KD));
-          acc = mma32(ka, cat(Wl[J], Wl[J + 1]), acc);
-          acc = mma32(ka, cat(Wh[J], Wh[J + 1]), acc);
+          acc = mmh32(ka, cat(Wl[J], Wl[J + 1]), acc);
+          acc = mmh32(ka, cat(Wh[J], Wh[J + 1]), acc);
         }
-        S[mt] = S[mt] * gc + acc;
+        S[mt] = S[mt] * gc + acc * inv_w;
       }
       stage(cb ^ 1);
       lds_barrier();  // B0: the next chunk is staged
@@ -750,6 +851,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
 #pragma unroll
       for (int r = 0; r < 4; ++r) store_state(sbase + (int64_t)(16 * mt + 4 * g4 + r) * VD, S[mt][r]);
   } else {
+    float inv_p;
+    pow2_scale(p.scale, &inv_p);   // the P planes carry P 2^sP (gdn_chunk_prep_kernel)
     u32x4 pq[4], pv[2], pp[3];
     auto fetch = [&](int c0) {
       const uint16_t* row = row_of(c0);
@@ -787,6 +890,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         Sh[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt) * XP);
         Sl[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt + 1) * XP);
       }
+      const float inv_s = s_inv[w];
       f32x4 X[4];
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
@@ -796,10 +900,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
           const int a0 = yo[2 * (q2 & 1)] + 64 * (q2 >> 1) + 16 * I * KD;
           const int a1 = yo[2 * (q2 & 1) + 1] + 64 * (q2 >> 1) + 16 * I * KD;
           const s16x8 qa = cat(ld4h(Qs + a0), ld4h(Qs + a1));
-          qs = mma32(cat(Sl[2 * q2], Sl[2 * q2 + 1]), qa, qs);
-          qs = mma32(cat(Sh[2 * q2], Sh[2 * q2 + 1]), qa, qs);
+          qs = mmh32(cat(Sl[2 * q2], Sl[2 * q2 + 1]), qa, qs);
+          qs = mmh32(cat(Sh[2 * q2], Sh[2 * q2 + 1]), qa, qs);
         }
-        X[I] = qs;
+        X[I] = qs * inv_s;
       }
       lds_barrier();  // B2: split V' handed over
 
@@ -811,6 +915,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         Vh[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I) * XP);
         Vl[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I + 1) * XP);
       }
+      const float inv_pv = inv_p * v_inv[w];   // the P planes' and V''s inverse scales
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         const int t = 16 * I + m16;
@@ -822,7 +927,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         if (I == 1) acc = split_product_sw<2, true>(ph, pl, po, Vh, Vl, acc);
         if (I == 2) acc = split_product_sw<3, true>(ph, pl, po, Vh, Vl, acc);
         if (I == 3) acc = split_product_sw<4, true>(ph, pl, po, Vh, Vl, acc);
-        X[I] = X[I] * qe + acc;
+        X[I] = X[I] * qe + acc * inv_pv;
       }
       // stage before storing: waiting for the staged loads would also wait for stores issued before it
       stage(cb ^ 1);

@@ -179,7 +179,7 @@ class SlotStreamEngine(PreparedWeights):
     slot of padding rows)."""
 
     def __init__(self, model: GuardModel, max_slots, state_dtype="float32", use_graphs=True, roles=ROLES,
-                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=0, fuse_conv=True):
+                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=16, fuse_conv=True):
         if not isinstance(max_slots, int) or max_slots < 1:
             raise ValueError("max_slots must be a positive integer")
         if state_dtype not in STATE_DTYPES:
@@ -188,17 +188,17 @@ class SlotStreamEngine(PreparedWeights):
             raise ValueError("max_tick_tokens must be in [1, 64]")
         if chunk_min_tokens < 0:
             raise ValueError("chunk_min_tokens must be >= 0")
-        # GDN rows of at least this many tokens go to the chunked kernels (0, the default: every row to the slot
-        # step). The chunk path's split-bf16 products are accurate to ~2^-18 relative against the recurrence's
-        # fp32 (one bf16 output in 300 rounds the other way instead of one in 10,000), which on the matched-GEMM
-        # engine test moves cut scores by up to 2.7e-3 against the oracle, past the 2e-3 bar, so it is opt-in.
+        # In prefill-like ticks (at least 8 tokens per row on average: initial contexts and re-prefills) the GDN
+        # rows of at least chunk_min_tokens tokens go to the chunked kernels (WY/UT form on MFMA, one launch set
+        # for the tick's long rows); every other row, and every row of a mixed or decode tick, runs the slot step.
+        # 0 keeps every row on the slot step. In a mixed tick the few long rows do not repay the chunk path's
+        # extra launches (conv, prep, order, state, gate per layer), so those stay with the slot step.
         self.chunk_min_tokens = chunk_min_tokens
         lib()  # fail loudly here if the HIP library is missing
         cfg = model.config
         # the GDN layers' causal conv runs inside the slot step (hsg_gdn_conv_slot_step_gated) when every value
-        # head has its own key head and no rows go to the chunk kernels; otherwise as its own kernel first
-        self.fuse_conv = bool(fuse_conv) and chunk_min_tokens == 0 and \
-            cfg.linear_num_value_heads == cfg.linear_num_key_heads
+        # head has its own key head and no rows of the tick go to the chunk kernels; otherwise as its own kernel
+        self.fuse_conv = bool(fuse_conv) and cfg.linear_num_value_heads == cfg.linear_num_key_heads
         self.model, self.cfg = model, cfg
         self.max_slots, self.roles, self.use_graphs = max_slots, tuple(roles), use_graphs
         self.window = cfg.window_tokens
@@ -343,7 +343,10 @@ class SlotStreamEngine(PreparedWeights):
                 torch.mm(normed, Lw["w_in"].t(), out=proj)
                 out = self._view("mid", tb, cfg.value_dim)
                 base = proj.data_ptr()
-                if self.fuse_conv:
+                # rows are packed longest first: in a prefill-like tick the rows of >= chunk_min_tokens tokens go
+                # to the chunked kernels (one WY/UT chunk each), the rest to the slot step
+                R = self._chunk_rows(nb, tb)
+                if self.fuse_conv and R == 0:
                     # causal conv + SiLU inside the slot step, from the raw projection and the conv history pool
                     check(L.hsg_gdn_conv_slot_step_gated(
                         base, self.gdn_in, 0, cfg.key_dim, 2 * cfg.key_dim, Lw["conv_w"].data_ptr(),
@@ -358,9 +361,6 @@ class SlotStreamEngine(PreparedWeights):
                                                  Lw["conv_w"].data_ptr(), cfg.linear_conv_kernel_dim,
                                                  slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb, 0, C,
                                                  conv.data_ptr(), C, st), "hsg_conv_silu_update")
-                    # rows are packed longest first: the rows of >= chunk_min_tokens tokens among the first R go
-                    # to the chunked kernels (one WY/UT chunk each), the rest to the slot step
-                    R = self._chunk_rows(nb, tb)
                     check(L.hsg_gdn_slot_step_gated(
                         conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,
                         base + 2 * (C + cfg.value_dim + hv), base + 2 * (C + cfg.value_dim), self.gdn_in,
@@ -435,11 +435,10 @@ class SlotStreamEngine(PreparedWeights):
 
     def _chunk_rows(self, nb, tb):
         """How many leading rows of an (nb, tb) tick may take the chunked GDN path (a constant per graph): every
-        row when the tick is prefill-like (>= 8 tokens per row on average), else at most 64 (a mixed tick has a
-        few long rows, packed first)."""
-        if not self.chunk_min_tokens:
+        row when the tick is prefill-like (>= 8 tokens per row on average), else none."""
+        if not self.chunk_min_tokens or tb < 8 * nb:
             return 0
-        return nb if tb >= 8 * nb else min(nb, 64)
+        return nb
 
     def _static(self, nb, tb):
         key = (nb, tb)

@@ -105,6 +105,31 @@ def test_engine_matches_oracle_matched_gemms(setup2):
         oring.ring_attention_v8 = orig
 
 
+def test_engine_chunk_route_matches_oracle_matched_gemms(setup2):
+    """The engine with the chunked GDN kernels on (chunk_min_tokens 2: in the schedule's prefill-like ticks every
+    row of two or more tokens goes through hsg_gdn_chunk_prefill_gated, single tokens and the mixed ticks through
+    the slot step) against the oracle with matched GEMMs, at the same 2e-3 bar as the slot-step route."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from oracle.backbone import StreamOracle
+    cfg, model, weights = setup2
+    print("[engine] chunk route vs oracle, matched GEMMs", flush=True)
+    eng = SlotStreamEngine(model, 4, use_graphs=False, chunk_min_tokens=2)
+    orc = StreamOracle(weights, cfg, 4)
+    gemm = _matched_gemm(eng)
+    worst = 0.0
+    for t, tick in enumerate(_schedule(np.random.default_rng(0), cfg.vocab_size)):
+        diff = _max_diff(eng.step(tick), orc.step(tick, gemm=gemm))
+        worst = max(worst, diff)
+        assert diff <= PROB_TOL, f"tick {t}: prob diff {diff:.2e}"
+    print(f"[engine] chunk route worst prob diff {worst:.2e}", flush=True)
+    np.testing.assert_array_equal(eng.length, orc.length)
+    np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
+    rec = eng.rec.double().cpu().numpy()
+    for s in range(4):
+        rel = np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
+        assert rel < 1e-3, f"slot {s} state rel err {rel:.2e}"
+
+
 def test_engine_matches_oracle(setup):
     from hs_guard.engine.slot_engine import SlotStreamEngine
     from oracle.backbone import StreamOracle

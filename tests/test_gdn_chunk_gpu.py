@@ -29,7 +29,8 @@ def _out_close(got, ref, rtol=2.0 ** -8, atol_frac=1e-3):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     atol = atol_frac * max(np.abs(ref).max(), 1e-30)
-    bad = np.abs(got - ref) > rtol * np.abs(ref) + atol
+    # steps counted in the binade of the larger magnitude: one step of the upper binade is two of the lower
+    bad = np.abs(got - ref) > rtol * np.maximum(np.abs(ref), np.abs(got)) + atol
     return int(bad.sum()), float(np.abs(got - ref).max())
 
 
@@ -242,13 +243,70 @@ def test_tick_split_between_slot_step_and_chunk():
     torch.cuda.synchronize()
     chunk_rows = [n for n in range(R) if lens[n] >= THR]
     assert chunk_rows == [0, 1, 3]
+    # the gated output is bf16(bf16(w * bf16(o * r)) * silu(z)): a one-step difference of bf16(o * r) between the
+    # two paths can become two steps of the output, so all within 2**-6 and almost all within 2**-7
+    far = 0
     for n in range(7):   # the skip filter left exactly the chunk rows to the chunk kernels
         ln_n, off = int(lens[n]), int(offsets[n])
         if ln_n == 0:
             continue
-        bad, worst = _out_close(_np(o_split[off:off + ln_n]), _np(o_ref[off:off + ln_n]), rtol=2.0 ** -7)
+        bad, worst = _out_close(_np(o_split[off:off + ln_n]), _np(o_ref[off:off + ln_n]), rtol=2.0 ** -6)
         assert bad == 0, f"row {n}: {bad} outputs off (max diff {worst:.3e})"
+        far += _out_close(_np(o_split[off:off + ln_n]), _np(o_ref[off:off + ln_n]), rtol=2.0 ** -7)[0]
+    assert far <= 1e-4 * T * HV * K, f"{far} outputs beyond two bf16 steps"
     for s in range(8):
         rel, mx = _state_err(_np(s_split[s]), _np(s_ref[s]))
         assert rel <= STATE_TOL and mx <= STATE_TOL, f"slot {s}: state error norm {rel:.2e} max {mx:.2e}"
     np.testing.assert_array_equal(_np(s_split[5]), _np(state0[5]))   # unused slot
+
+
+def test_chunk_output_rounding_rate_matches_slot_step():
+    """Precision of the chunk path: over 4 rows of 512 tokens from a random state, the fraction of bf16 outputs
+    whose rounding differs from the float64 recurrence's must stay within 1.5 times the slot-step kernel's (fp32
+    FMA recurrence) on the same rows (measured: 1.2e-4 against 1.4e-4); the state within 1e-6 relative (1.2e-7).
+    What this rate exposes: a bf16 hi + lo split of the state path's operands (~2^-17) flipped one output in 400,
+    and an fp32 in-chunk cumulative decay, whose rounding every e^(G_i - G_j) inherits, one in 2,500."""
+    from hs_guard.engine.kernels import gdn_chunk_prefill, gdn_slot_v8
+    from oracle.bf16 import bf16
+    print("[chunk] output rounding rate vs slot step", flush=True)
+    gen = torch.Generator().manual_seed(17)
+    H = HV = 16
+    K = 128
+    N, L = 4, 512
+    C = 2 * H * K + HV * K
+    packed = (torch.randn(N, L, C, generator=gen) * 0.5).to(torch.bfloat16)
+    a = torch.randn(N, L, HV, generator=gen).to(torch.bfloat16)
+    b = torch.randn(N, L, HV, generator=gen).to(torch.bfloat16)
+    A_log = (torch.rand(HV, generator=gen) - 0.5).to(torch.bfloat16)
+    dt = (torch.randn(HV, generator=gen) * 0.3).to(torch.bfloat16)
+    state0 = torch.randn(N + 1, HV, K, K, generator=gen) * 0.02
+    dev = torch.device("cuda:0")
+    slots = torch.arange(N, device=dev)
+    lens = torch.full((N,), L, dtype=torch.long, device=dev)
+    pd, ad, bd, Ad, dd = packed.to(dev), a.to(dev), b.to(dev), A_log.to(dev), dt.to(dev)
+    s_chunk = state0.to(dev)
+    o_chunk, _ = gdn_chunk_prefill(pd, H * K, H, K, HV, K, ad, bd, Ad, dd, s_chunk, slots, lens)
+    s_step = state0.to(dev)
+    outs = []
+    for t0 in range(0, L, 64):
+        o, _ = gdn_slot_v8(pd[:, t0:t0 + 64].contiguous(), H * K, H, K, HV, K, ad[:, t0:t0 + 64].contiguous(),
+                           bd[:, t0:t0 + 64].contiguous(), Ad, dd, s_step, slots,
+                           torch.full((N,), 64, dtype=torch.long, device=dev))
+        outs.append(o)
+    o_step = torch.cat(outs, 1)
+    torch.cuda.synchronize()
+    flips = {"chunk": 0, "step": 0}
+    worst = 0.0
+    for n in range(N):
+        o_ref, s_ref = _row_reference(_np(packed[n]), _np(a[n]), _np(b[n]), _np(A_log), _np(dt), _np(state0[n]),
+                                      H, HV, K, chunk=True)
+        ref = bf16(o_ref)
+        flips["chunk"] += int((_np(o_chunk[n]) != ref).sum())
+        flips["step"] += int((_np(o_step[n]) != ref).sum())
+        worst = max(worst, _state_err(_np(s_chunk[n]), s_ref)[0])
+    total = N * L * HV * K
+    rate = {k: v / total for k, v in flips.items()}
+    print(f"[chunk] bf16 flips vs float64: chunk {rate['chunk']:.2e}, slot step {rate['step']:.2e}; "
+          f"chunk state rel {worst:.2e}", flush=True)
+    assert rate["chunk"] <= 1.5 * rate["step"]
+    assert worst <= 1e-6
