@@ -3,8 +3,10 @@
 Workload (config 5, mixed serving): 352 concurrent slots on the full random-init backbone (hidden 1024,
 24 layers 3 GDN : 1 attention, GDN 16x128, attention 16q/4kv/256, MLP 3584, vocab 151,936, bf16 weights
 N(0, 0.02)), fp32 recurrent state. Every slot first gets an initial context drawn uniformly from
-{512, 2048, 8000} tokens (untimed prefill). Each step every slot appends c tokens, c = 1 (p 0.8),
-U{2..16} (p 0.15), U{17..64} (p 0.05); the step is one engine tick under hipGraph through step_packed, the
+{512, 2048, 8000} tokens, prefilled through step() outside the timed steps (reported as
+prefill_352_contexts: once cold, capturing each tick shape's graph, then again into reset slots with the same
+lengths, warm). Each step every slot appends c tokens, c = 1 (p 0.8), U{2..16} (p 0.15), U{17..64} (p 0.05);
+the step is one engine tick under hipGraph through step_packed, the
 call the reference's serving backend makes (examples/demo/runtime_v10.py:114): H2D of the packed tick, graph
 replay, D2H of both roles' probabilities, stream sync, probabilities on the host as [R, n, lb, 3]. The same
 load through step() (one CPU tensor per request and role, StreamingGuard's call) is reported as api_step.
@@ -97,6 +99,49 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     return {"kernel": "gdn_step_kernel conv variant (hsg_gdn_conv_slot_step_gated)",
             "shape": f"{rows} rows x 1 token x 16 heads", "avg_us": round(us, 2), "alg_bytes_per_launch": traffic_alg,
             "achieved_gbs": round(gbs, 1)}
+
+
+def lone_row_rate(torch, lib, tokens=64, iters=20):
+    """The conv + gated GDN slot step (hsg_gdn_conv_slot_step_gated) on one row of ``tokens`` tokens, 16 heads x
+    128, fp32 state, every other row of an 8-row grid empty: a mixed tick's critical path when its longest row
+    runs on the slot step (the chip otherwise idle). HIP events on the launch stream around ``iters`` launches."""
+    dev = torch.device("cuda:0")
+    N, H, K = 8, 16, 128
+    C = 3 * H * K
+    stride = C + H * K + 2 * H + 64
+    gen = torch.Generator(device=dev).manual_seed(2)
+    proj = torch.randn(tokens, stride, generator=gen, device=dev).bfloat16()
+    out = torch.empty(tokens, H * K, device=dev, dtype=torch.bfloat16)
+    state = torch.randn(N + 1, H, K, K, generator=gen, device=dev) * 0.02
+    pool = torch.randn(N + 1, 3, C, generator=gen, device=dev).bfloat16()
+    conv_w = (torch.randn(C, 4, generator=gen, device=dev) * 0.3).bfloat16()
+    A = torch.zeros(H, dtype=torch.bfloat16, device=dev)
+    w = torch.ones(K, dtype=torch.bfloat16, device=dev)
+    slots = torch.arange(N, device=dev)
+    lens = torch.zeros(N, dtype=torch.long, device=dev)
+    lens[0] = tokens
+    offs = torch.zeros(N, dtype=torch.long, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    base = proj.data_ptr()
+
+    def launch():
+        rc = lib.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, conv_w.data_ptr(), pool.data_ptr(),
+                                              C, base + 2 * (C + H * K + H), base + 2 * (C + H * K), stride,
+                                              A.data_ptr(), A.data_ptr(), state.data_ptr(), 0, N + 1,
+                                              slots.data_ptr(), lens.data_ptr(), offs.data_ptr(), N, H, H, K, K,
+                                              K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(),
+                                              stream.cuda_stream)
+        assert rc == 0, rc
+    launch()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(iters):
+        launch()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / iters
+    return {"tokens": tokens, "avg_us": round(us, 2), "us_per_token": round(us / tokens, 3)}
 
 
 def measured_traffic(rows, state_dtype):
@@ -360,10 +405,15 @@ def main():
                     help="only the config-4 chunked-prefill measurement (profiled under rocprofv3)")
     ap.add_argument("--ring-only", action="store_true",
                     help="only the 352 x 1-token split-K ring decode measurement (profiled under rocprofv3)")
+    ap.add_argument("--lone-row-only", action="store_true",
+                    help="only the GDN slot step on one 64-token row (profiled under rocprofv3 --pmc)")
     ap.add_argument("--mixed-only", action="store_true",
                     help="only the prefill and the mixed steps (no kernel legs, decode legs, context sweep or CPU "
                          "baseline): the command whose kernel statistics give the per-step kernel breakdown")
     ap.add_argument("--reset-p", type=float, default=0.01, help="per-slot reset probability after each step")
+    ap.add_argument("--chunk-min-tokens", type=int, default=None,
+                    help="SlotStreamEngine's chunk_min_tokens (default: the engine's; 0 puts every GDN row on the "
+                         "slot step)")
     ap.add_argument("--sweep-steps", type=int, default=60,
                     help="timed mixed steps per initial-context length in the per-context latency sweep (0: skip)")
     args = ap.parse_args()
@@ -384,6 +434,9 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(0)}")
     state_code = 0 if args.state_dtype == "float32" else 1
+    if args.lone_row_only:
+        print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib())}), flush=True)
+        return
     if args.chunk_only or args.ring_only:
         leg = chunk_prefill_rate(torch) if args.chunk_only else ring_decode_rate(torch, rows=args.slots)
         print(json.dumps({"chunk_prefill_cfg4" if args.chunk_only else "ring_decode_352": leg}), flush=True)
@@ -391,7 +444,7 @@ def main():
     if args.mixed_only:
         args.sweep_steps = 0
         args.no_cpu_baseline = True
-        roof = ring = chunk = None
+        roof = ring = chunk = lone = None
     else:
         roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
         log(f"GDN roofline {roof}")
@@ -409,22 +462,41 @@ def main():
         log(f"ring decode {ring}")
         chunk = chunk_prefill_rate(torch)
         log(f"chunk prefill config 4 {chunk}")
+        lone = lone_row_rate(torch, lib())
+        log(f"GDN slot step, one 64-token row {lone}")
 
     cfg = GuardConfig.baseline()
     t0 = time.time()
     model = GuardModel.random(cfg, seed=args.seed, device=dev, gen_device=dev)
     log(f"model {model.num_parameters() / 1e6:.1f}M params in {time.time() - t0:.1f}s")
-    eng = SlotStreamEngine(model, args.slots, state_dtype=args.state_dtype)
+    extra = {} if args.chunk_min_tokens is None else {"chunk_min_tokens": args.chunk_min_tokens}
+    eng = SlotStreamEngine(model, args.slots, state_dtype=args.state_dtype, **extra)
     load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
                             contexts=tuple(int(x) for x in args.contexts.split(",")), reset_p=args.reset_p)
 
-    # ---- untimed initial contexts ----
-    t0 = time.time()
+    # ---- initial contexts through step() (outside the timed steps): first cold (every tick shape captured
+    # into its graph on first use), then, into reset slots, the same lengths with fresh token ids (warm) ----
+    t0 = time.perf_counter()
     ctx = [(s, load.context()) for s in range(args.slots)]
     eng.step(ctx)
     torch.cuda.synchronize()
-    log(f"prefilled {sum(len(c) for _, c in ctx)} context tokens in {time.time() - t0:.1f}s "
-        f"({eng.stats['captures']} graphs)")
+    cold_s = time.perf_counter() - t0
+    captures = eng.stats["captures"]
+    ctx_tokens = sum(len(c) for _, c in ctx)
+    log(f"prefilled {ctx_tokens} context tokens in {cold_s:.2f}s ({captures} graphs)")
+    rng_ctx = np.random.default_rng(args.seed + 3)
+    ctx = [(s, rng_ctx.integers(0, cfg.vocab_size, len(c)).tolist()) for s, c in ctx]
+    eng.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.step(ctx)
+    torch.cuda.synchronize()
+    warm_s = time.perf_counter() - t0
+    prefill = {"contexts": args.slots, "tokens": ctx_tokens, "ticks": max(-(-len(c) // eng.max_tick_tokens)
+                                                                          for _, c in ctx),
+               "cold_s": round(cold_s, 3), "graphs_captured": captures, "warm_s": round(warm_s, 3),
+               "warm_tokens_per_s": round(ctx_tokens / warm_s, 1), "chunk_min_tokens": eng.chunk_min_tokens}
+    log(f"prefill {prefill}")
 
     def reprefill(slots):
         if slots:
@@ -490,6 +562,7 @@ def main():
     log(f"step() leg {api_step}")
     if args.mixed_only:
         print(json.dumps({"mixed_only": True, "value": round(value, 1), "unit": "tokens/s", "steps": args.steps,
+                          "prefill_352_contexts": prefill,
                           "tokens": tokens, "ms_per_step": round(total / args.steps * 1e3, 4),
                           "latency_ms": {"p50": round(percentile(step_ms, 50), 3),
                                          "p95": round(percentile(step_ms, 95), 3)}, "api_step": api_step}),
@@ -599,6 +672,8 @@ def main():
                      "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
         "ring_decode_352": ring,
         "chunk_prefill_cfg4": chunk,
+        "gdn_lone_row_64": lone,
+        "prefill_352_contexts": prefill,
         "complete_message_8000": {"ms": round(whole_ms, 2), "tokens_per_s": round(8000 / whole_ms * 1e3, 1)},
         "v10_geometry": v10,
         "cpu_baseline": cpu,
