@@ -144,6 +144,17 @@ def lone_row_rate(torch, lib, tokens=64, iters=20):
     return {"tokens": tokens, "avg_us": round(us, 2), "us_per_token": round(us / tokens, 3)}
 
 
+def calibration_copy(torch, dev):
+    """Three plain 512 MiB device-to-device copies (512 MiB read + 512 MiB written each): the known-size kernel
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings of the same run into bytes."""
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def measured_traffic(rows, state_dtype):
     """HBM bytes per launch of the GDN slot step at the decode shape, as rocprofv3's FETCH_SIZE and WRITE_SIZE
     counters read it (each scaled by the same counter's reading for a device copy of known size). The counter
@@ -159,9 +170,9 @@ def measured_traffic(rows, state_dtype):
 
 
 def ring_decode_rate(torch, rows=352, iters=50):
-    """Split-K ring attention (hsg_ring_decode, three launches) at the 352 x 1-token decode shape, HIP events
-    on the launch stream: config 2's ring fills (uniform in [1, 512]) scaled to 352 rows, and full rings (the
-    steady state of a live session). Algorithmic bytes: the visible keys and values (n 256 dims x 2 B x 2),
+    """Decode ring attention (hsg_ring_decode: one fused launch at 4 query heads per kv head) at the 352 x 1-token
+    decode shape, HIP events on the launch stream: config 2's ring fills (uniform in [1, 512]) scaled to 352 rows,
+    and full rings (the steady state of a live session). Algorithmic bytes: the visible keys and values (n 256 dims x 2 B x 2),
     their positions (8 B each), q, gate and out (3 x 16 heads x 512 B), the new key and value read and
     written to the ring (4 kv heads x 512 B x 4)."""
     from hs_guard.engine.kernels import ring_attention_v8
@@ -439,7 +450,9 @@ def main():
         return
     if args.chunk_only or args.ring_only:
         leg = chunk_prefill_rate(torch) if args.chunk_only else ring_decode_rate(torch, rows=args.slots)
-        print(json.dumps({"chunk_prefill_cfg4" if args.chunk_only else "ring_decode_352": leg}), flush=True)
+        calibration_copy(torch, dev)
+        print(json.dumps({"chunk_prefill_cfg4" if args.chunk_only else "ring_decode_352": leg,
+                          "calibration_copy_bytes": 512 << 20}), flush=True)
         return
     if args.mixed_only:
         args.sweep_steps = 0
@@ -449,12 +462,7 @@ def main():
         roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
         log(f"GDN roofline {roof}")
     if args.roofline_only:
-        # calibration for HBM-traffic counters: a plain 512 MiB device-to-device copy (512 MiB read + written)
-        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        calibration_copy(torch, dev)
         print(json.dumps({"roofline_only": roof, "calibration_copy_bytes": 512 << 20}), flush=True)
         return
     if not args.mixed_only:

@@ -179,12 +179,6 @@ __device__ __forceinline__ float exp_nonpos_d(double x) {
   return ldexpf(__builtin_amdgcn_exp2f((float)(y - n)), (int)n);
 }
 
-// workgroup barrier that orders LDS only (outstanding global prefetches stay in flight)
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // LDS transpose read (ds_read_b64_tr_b16): within each group of 16 lanes, lane 4q + e receives element e of
 // the 4-element (8-byte) vectors addressed by lanes q, q + 4, q + 8, q + 12 of its group. With a row-major

@@ -135,6 +135,13 @@ __device__ __forceinline__ float wave_max(float x) {
   return max_pair32(max_pair16(x));
 }
 
+// workgroup barrier that orders LDS only (outstanding global loads stay in flight across it)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 inline int launch_status() {

@@ -1,4 +1,4 @@
-// Split-K window-W GQA ring attention for decode steps (one query position per row) on gfx950.
+// Window-W GQA ring attention for decode steps (one query position per row) on gfx950.
 //
 // Contract and numerics: those of hsg_ring_attention (src/hs_guard/engine/fused_kernels.py:288-376 and the
 // torch reference src/hs_guard/engine/ring_attention_kernel.py:7-26) for rows with lens[n] == 1: keys in
@@ -6,16 +6,19 @@
 // probabilities p = exp(s - m_b) rounded to bf16 in the P.V product and summed unrounded, output / sum
 // rounded to bf16, times bf16(sigmoid(gate)). The running max of block b is the prefix maximum of the block
 // maxima, and the reference's rescaling chain multiplies block b's P.V and sum by exp(m_b - m_final), so the
-// key range can be split across workgroups without changing where any bf16 rounding happens:
+// blocks can be processed by different waves or workgroups without changing where any bf16 rounding happens.
+//
+// Up to 8 query heads per kv head: decode_fused_kernel, one launch, one workgroup per (row, kv head) with every
+// score and partial sum in LDS (no workspace traffic). More heads per kv head: three split-K launches over a
+// workspace:
 //   A (scores):  (row, kv head, split) -> s = scale * q.k for the split's ring blocks (masked -inf) and each
 //                block's maximum per query head, into the workspace; the last split adds the step's own key.
 //   B (values):  (row, kv head, split) -> prefix maxima from all block maxima, then for each of its blocks
 //                exp(m_b - m_final) * sum_k bf16(exp(s_k - m_b)) v_k and the matching unrounded sum.
 //   C (combine): (row, kv head) -> sum over splits, divide, gate, store; then the in-place ring write of the
 //                step's key and value (every read of this ring finished in B).
-// Blocks with no visible key are skipped in A and B (no K or V traffic). The split is over the 512 ring
-// columns: 4 splits of 4 blocks, one block per wave, so a decode step of R rows runs 16 R workgroups per
-// launch instead of R (latency hidden across workgroups, not inside one).
+// Blocks with no visible key are skipped (no K or V traffic) on both paths. The split is over the 512 ring
+// columns: 4 splits of 4 blocks, one block per wave.
 #include <math.h>
 
 #include <mutex>
@@ -32,6 +35,7 @@ constexpr int W_MAX = 512;
 constexpr int G_MAX = 16;          // query heads per kv head
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
 // exp of a softmax argument or rescale exponent on the hardware exp2 (v_exp_f32): exp(x) = 2^(x log2 e), as the
@@ -396,6 +400,325 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecParams p) 
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Fused decode (groups <= 8): one workgroup of 8 waves per (row, kv head), wave w owning ring blocks w and w + 8,
+// so every score, block maximum and partial sum stays in LDS and the whole step is one launch. The numerics are
+// those of the three split-K kernels above (same block maxima, prefix maxima, bf16 probabilities and block
+// weights); only the fp32 summation order of the partial P.V sums differs (keys in order within a block, the
+// wave's two blocks in order, then a fixed tree over the waves). Memory: round trip 1 issues the blocks'
+// positions, the queries (into LDS) and the step's own key and value; then each visible block's keys, one block
+// at a time; the first block's values go out as soon as the scores are done and are in flight across the
+// block-maximum barrier, the second block's after the first block's P.V. At about 90 VGPRs two or more of these
+// workgroups share a CU, so one workgroup's loads cover the other's barriers and arithmetic.
+template <int GT>
+__global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
+  constexpr int NWV = 4;                       // waves
+  constexpr int BPW = W_MAX / KB / NWV;        // ring blocks per wave (4)
+  constexpr int NBK = W_MAX / KB;              // ring blocks (16)
+  constexpr int GR = (GT + 3) / 4;             // rounds of 4 heads for the probabilities
+  __shared__ __align__(16) uint16_t q_s[GT * D];            // queries of the kv head's group, head-major
+  __shared__ __align__(16) float sc_s[GT][W_MAX];           // scale q.k per ring column (-inf where masked)
+  __shared__ float bm_s[GT][NBK + 1];                       // block maxima; column RB: the step's own key
+  __shared__ float own_s[GT];                               // the step's own-key score
+  __shared__ __align__(16) uint32_t pb_s[NBK][GT][KB / 2];  // bf16 probabilities, key pairs (2 j, 2 j + 1)
+  __shared__ __align__(16) float red_s[NWV / 2][GT][D];     // reduction tree of the per-wave P.V partials
+  __shared__ float lsum_s[NWV][GT];                         // per-wave weighted normalisers
+  __shared__ uint2 vown_s[64];                              // the step's own value (lane: dims 4 lane .. +3)
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m16 = lane & 15, g4 = lane >> 4;
+  const int u = blockIdx.x;
+  const int n = u / p.hkv, h = u - n * p.hkv;
+  const RowInfo ri = row_info(p, n);
+  const int W = p.W, G = p.G, RB = W / KB;
+  if (!ri.live) {
+    // padded layout: a row without a live step (lens 0 or a rejected slot) owns an output row of zeros
+    if (p.offsets == nullptr) {
+      for (int e = threadIdx.x; e < G * (D / 4); e += 64 * NWV) {
+        const int g = e / (D / 4), d = 4 * (e - g * (D / 4));
+        const float z[4] = {0.f, 0.f, 0.f, 0.f};
+        store4_bf16(p.out + (int64_t)n * p.o_sn + h * p.o_sh + g * p.o_sg + d, z);
+      }
+    }
+    return;
+  }
+  const int64_t qpos = ri.start;
+  const uint16_t* qrow = p.q + row_base(p, p.q_sn, p.q_sl, n, ri.tok) + h * p.q_sh;
+  const int64_t ring_at = (ri.slot * p.hkv + h) * (int64_t)(W + 1);
+
+  // ---- round trip 1: queries into LDS, the blocks' positions, the step's own key and value ----
+  if (threadIdx.x < GT * D / 8) {
+    const int g = threadIdx.x / (D / 8), c = threadIdx.x - g * (D / 8);
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (g < G) w = *reinterpret_cast<const uint4*>(qrow + g * p.q_sg + 8 * c);
+    *reinterpret_cast<uint4*>(&q_s[g * D + 8 * c]) = w;
+  }
+  uint32_t okbits = 0;   // bit 8 i + 4 t + r: key 16 t + 4 g4 + r of block i is visible
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int b = wave + NWV * i;
+    if (b < RB) {
+      const int64_t* rpos = p.ring_pos + ri.slot * (int64_t)(W + 1) + b * KB;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t kp = rpos[16 * t + 4 * g4 + r];
+          okbits |= (uint32_t)(kp >= 0 && kp <= qpos && kp > qpos - W) << (8 * i + 4 * t + r);
+        }
+    }
+  }
+  const bool own_wave = wave == NWV - 1;
+  uint2 kown = make_uint2(0u, 0u);
+  if (own_wave) {
+    kown = *reinterpret_cast<const uint2*>(p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh +
+                                           4 * lane);
+    // parked in LDS until the end, where it is the last value added
+    vown_s[lane] = *reinterpret_cast<const uint2*>(p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) +
+                                                   h * p.nv_sh + 4 * lane);
+  }
+  bool has[BPW];   // wave-uniform: block i has a visible key (false past the ring)
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) has[i] = __ballot(((okbits >> (8 * i)) & 0xffu) != 0) != 0;
+  lds_barrier();   // B0: queries in LDS
+
+  // ---- scores, one block at a time (A: keys, lane keys 16 t + m16, dims 32 ks + 8 g4 ..; B: queries m16 < G
+  // from LDS): lane (query m16, keys 16 t + 4 g4 + r) ----
+  uint2 vr[KB];    // values of the block in P.V, lane: dims 4 lane .. +3 of key k
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int b = wave + NWV * i;
+    if (has[i]) {
+      const uint16_t* kbase = p.ring_k + (ring_at + b * KB) * D;
+      uint4 ka[2][D / 32];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks)
+          ka[t][ks] = *reinterpret_cast<const uint4*>(kbase + (16 * t + m16) * D + 32 * ks + 8 * g4);
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+          uint4 w = make_uint4(0u, 0u, 0u, 0u);
+          if (m16 < GT) w = *reinterpret_cast<const uint4*>(&q_s[m16 * D + 32 * ks + 8 * g4]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[t][ks]),
+                                                        __builtin_bit_cast(bf16x8, w), acc, 0, 0, 0);
+        }
+        f32x4 sv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sv[r] = ((okbits >> (8 * i + 4 * t + r)) & 1u) ? acc[r] * p.scale : -INFINITY;
+          bmax = fmaxf(bmax, sv[r]);
+        }
+        if (m16 < G) *reinterpret_cast<f32x4*>(&sc_s[m16][b * KB + 16 * t + 4 * g4]) = sv;
+      }
+      bmax = max_pair32(max_pair16(bmax));   // over g4 (lane xor 16, 32)
+      if (g4 == 0 && m16 < G) bm_s[m16][b] = bmax;
+    } else if (b < RB && lane < G) {
+      bm_s[lane][b] = -INFINITY;
+    }
+  }
+  if (has[0]) {
+    // the first block's values go out now (the keys' registers are free) and arrive across the barriers
+    const uint16_t* vbase = p.ring_v + (ring_at + wave * KB) * D + 4 * lane;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) vr[k] = *reinterpret_cast<const uint2*>(vbase + k * D);
+  }
+  if (own_wave) {
+    // the step's own key: block RB, one key, always visible to its own query
+    float k4[4];
+    unpack2(kown.x, k4[0], k4[1]);
+    unpack2(kown.y, k4[2], k4[3]);
+    for (int g = 0; g < G; ++g) {
+      const uint2 qw = *reinterpret_cast<const uint2*>(&q_s[g * D + 4 * lane]);
+      float q4[4];
+      unpack2(qw.x, q4[0], q4[1]);
+      unpack2(qw.y, q4[2], q4[3]);
+      const float part = q4[0] * k4[0] + q4[1] * k4[1] + q4[2] * k4[2] + q4[3] * k4[3];
+      const float v = wave_sum(part) * p.scale;
+      if (lane == 0) {
+        own_s[g] = v;
+        bm_s[g][RB] = v;
+      }
+    }
+  }
+  lds_barrier();   // B1: every score and block maximum is in LDS
+
+  // ---- lane g < G: running max through each of the wave's blocks (m_b) and over all blocks and the own key
+  // (m_final); then each block's probabilities into LDS and its weight exp(m_b - m_final) ----
+  float mb[BPW], mf = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) mb[i] = -INFINITY;
+  if (lane < G) {
+    for (int j = 0; j <= RB; ++j) {
+      mf = fmaxf(mf, bm_s[lane][j]);
+#pragma unroll
+      for (int i = 0; i < BPW; ++i)
+        if (j == wave + NWV * i) mb[i] = mf;
+    }
+  }
+  float lpart = 0.f;   // lane g < G: this wave's weighted normaliser for head g
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int b = wave + NWV * i;
+    if (!has[i]) continue;
+    const float wgt = (lane < G && mb[i] != -INFINITY) ? exp_fast(mb[i] - mf) : 0.f;
+    float li = 0.f;
+#pragma unroll
+    for (int gr = 0; gr < GR; ++gr) {
+      const int g0 = 4 * gr;
+      const int g = g0 + (lane >> 4);
+      const int key = 2 * (lane & 15);
+      const float m_g = __shfl(mb[i], g < G ? g : 0, 64);
+      float p0 = 0.f, p1 = 0.f;
+      if (g < G && m_g != -INFINITY) {
+        const float2 sv = *reinterpret_cast<const float2*>(&sc_s[g][b * KB + key]);
+        p0 = sv.x == -INFINITY ? 0.f : exp_fast(sv.x - m_g);
+        p1 = sv.y == -INFINITY ? 0.f : exp_fast(sv.y - m_g);
+      }
+      // bf16 probabilities as key pairs (rows g >= G hold zeros, so P.V runs over all GT rows without a
+      // per-head test)
+      pb_s[b][g][lane & 15] = pack_bf16x2(p0, p1);
+      float ps = p0 + p1;   // unrounded, as the reference's row sum
+      ps = sum16_dpp(ps);
+      // lane 16 j holds the sum for head g0 + j; move it to lane g0 + j
+      const float got = __shfl(ps, 16 * ((lane - g0) & 3), 64);
+      if (lane >= g0 && lane < g0 + 4 && lane < G) li = got;
+    }
+    lpart += li * wgt;
+  }
+  lds_barrier();   // B2: the probabilities are in LDS (read back by every lane of the wave)
+
+  // ---- P.V, lane: dims 4 lane .. +3. The wave's blocks are chained as in the reference's rescaling:
+  // acc <- acc exp(m_prev - m_b) + P_b.V_b, then one final factor exp(m_last - m_final), so each block's sum is
+  // weighted by exp(m_b - m_final). Two keys per v_dot2_f32_bf16: probabilities (p_2j, p_2j+1) against values
+  // (v_2j[d], v_2j+1[d]), the value pairs assembled with byte permutes. ----
+  float acc[GT][4];
+#pragma unroll
+  for (int g = 0; g < GT; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[g][e] = 0.f;
+  float mprev = -INFINITY;   // lane g < G: running max of the last block added
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int b = wave + NWV * i;
+    if (!has[i]) continue;
+    if (i > 0) {
+      const uint16_t* vbase = p.ring_v + (ring_at + b * KB) * D + 4 * lane;
+#pragma unroll
+      for (int k = 0; k < KB; ++k) vr[k] = *reinterpret_cast<const uint2*>(vbase + k * D);
+    }
+    const float alpha = (lane < G && mb[i] != -INFINITY) ? exp_fast(mprev - mb[i]) : 0.f;
+    if (lane < G) mprev = mb[i];
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float a_g = readlane_f(alpha, g < G ? g : 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] *= a_g;
+    }
+#pragma unroll
+    for (int j2 = 0; j2 < KB / 2; j2 += 2) {
+      uint2 pp[GT];
+#pragma unroll
+      for (int g = 0; g < GT; ++g) pp[g] = *reinterpret_cast<const uint2*>(&pb_s[b][g][j2]);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const uint2 a = vr[2 * (j2 + jj)], c = vr[2 * (j2 + jj) + 1];
+        const uint32_t vp[4] = {__builtin_amdgcn_perm(c.x, a.x, 0x05040100u), __builtin_amdgcn_perm(c.x, a.x, 0x07060302u),
+                                __builtin_amdgcn_perm(c.y, a.y, 0x05040100u), __builtin_amdgcn_perm(c.y, a.y, 0x07060302u)};
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+          const uint32_t pg = jj == 0 ? pp[g].x : pp[g].y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[g][e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pg),
+                                                        __builtin_bit_cast(bf16x2, vp[e]), acc[g][e], false);
+        }
+      }
+    }
+  }
+  {
+    const float wl = (lane < G && mprev != -INFINITY) ? exp_fast(mprev - mf) : 0.f;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float w_g = readlane_f(wl, g < G ? g : 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] *= w_g;
+    }
+  }
+  if (own_wave) {
+    // the own key's running max is m_final and its weight 1
+    float pown = 0.f;
+    if (lane < G) pown = exp_fast(own_s[lane] - mf);
+    lpart += pown;
+    const uint2 vo = vown_s[lane];
+    float v[4];
+    unpack2(vo.x, v[0], v[1]);
+    unpack2(vo.y, v[2], v[3]);
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      const float pk = rbf(readlane_f(pown, g));   // 0 for g >= G
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[g][e] += pk * v[e];
+    }
+  }
+  if (lane < G) lsum_s[wave][lane] = lpart;
+
+  // ---- fixed reduction tree over the waves: wave w + half adds into wave w ----
+#pragma unroll
+  for (int half = NWV / 2; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+        *reinterpret_cast<f32x4*>(&red_s[wave - half][g][4 * lane]) =
+            (f32x4){acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+    }
+    lds_barrier();
+    if (wave < half) {
+#pragma unroll
+      for (int g = 0; g < GT; ++g) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(&red_s[wave][g][4 * lane]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[g][e] += x[e];
+      }
+    }
+    lds_barrier();
+  }
+
+  // ---- wave 0: normalise, gate, store; wave 1: the in-place ring write (every read of this ring is done) ----
+  if (wave == 0) {
+    uint16_t* orow = p.out + row_base(p, p.o_sn, p.o_sl, n, ri.tok) + h * p.o_sh;
+    const uint16_t* grow = p.gate ? p.gate + row_base(p, p.g_sn, p.g_sl, n, ri.tok) + h * p.g_sh + p.g_off
+                                  : nullptr;
+#pragma unroll
+    for (int g = 0; g < GT; ++g) {
+      if (g < G) {
+        float l = 0.f;
+        for (int w = 0; w < NWV; ++w) l += lsum_s[w][g];
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = l > 0.f ? rbf(acc[g][e] / l) : 0.f;
+        if (grow) {
+          float gt[4];
+          load4_bf16(grow + g * p.g_sg + 4 * lane, gt);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = y[e] * rbf(1.0f / (1.0f + expf(-gt[e])));
+        }
+        store4_bf16(orow + g * p.o_sg + 4 * lane, y);
+      }
+    }
+  } else if (wave == 1 && p.write_ring) {
+    const int64_t dst = (ring_at + ri.start % W) * D + 4 * lane;
+    const uint16_t* kn = p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh + 4 * lane;
+    const uint16_t* vn = p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) + h * p.nv_sh + 4 * lane;
+    *reinterpret_cast<uint2*>(p.ring_k + dst) = *reinterpret_cast<const uint2*>(kn);
+    *reinterpret_cast<uint2*>(p.ring_v + dst) = *reinterpret_cast<const uint2*>(vn);
+  }
+}
+
 }  // namespace
 }  // namespace hsg
 
@@ -447,6 +770,11 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   p.sc_stride = window + KB;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned units = (unsigned)(n_rows * hkv);
+  if (groups <= 8) {
+    if (groups <= 4) hipLaunchKernelGGL(decode_fused_kernel<4>, dim3(units), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(decode_fused_kernel<8>, dim3(units), dim3(256), 0, st, p);
+    return launch_status();
+  }
   hipLaunchKernelGGL(decode_scores_kernel, dim3(units * NS), dim3(256), 0, st, p);
   if (groups <= 4) hipLaunchKernelGGL(decode_values_kernel<4>, dim3(units * NS), dim3(256), 0, st, p);
   else if (groups <= 8) hipLaunchKernelGGL(decode_values_kernel<8>, dim3(units * NS), dim3(256), 0, st, p);
@@ -503,8 +831,9 @@ extern "C" int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl
   void* ws = nullptr;
   const int rc = current_scratch(&ws);
   if (rc != HSG_OK) return rc;
-  // the kernels write every workspace word they read (scores of visible blocks, every block maximum, every
-  // split's partial sums), so nothing left by an earlier call is read and nothing needs clearing
+  // the fused kernel (up to 8 query heads per kv head) does not touch the workspace; the split-K kernels write
+  // every workspace word they read (scores of visible blocks, every block maximum, every split's partial sums),
+  // so nothing left by an earlier call is read and nothing needs clearing
   return hsg_ring_decode(q, q_sn, q_sl, q_sh, q_sg, ring_k, ring_v, ring_rows, window, new_k, nk_sn, nk_sl, nk_sh,
                          new_v, nv_sn, nv_sl, nv_sh, gate, g_sn, g_sl, g_sh, g_sg, g_off, ring_pos, slots, starts,
                          lens, offsets, n_rows, hkv, groups, head_dim, scale, write_ring, out, o_sn, o_sl, o_sh,

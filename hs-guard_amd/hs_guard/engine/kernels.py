@@ -124,7 +124,7 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
     (v_proj output, strided rows allowed); gate: q_proj output [N, Lb, Hq*2D] (gate = second half of each
     head). Returns out * sigmoid(gate) as [N, Lb, Hq*D] bf16. write_ring (Lb == 1 only, as the
     reference): also writes this tick's key/value into ring column start % window. Decode ticks (Lb == 1)
-    run the split-K kernels (hsg_ring_decode) unless split_k is False."""
+    run the decode kernel (hsg_ring_decode) unless split_k is False."""
     n, hkv, m, d = q.shape
     lb = new_k.shape[2]
     groups = m // lb

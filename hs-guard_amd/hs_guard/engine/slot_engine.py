@@ -256,7 +256,7 @@ class SlotStreamEngine(PreparedWeights):
             "probs": torch.zeros(len(self.roles) * T * 3, dtype=torch.float32, device=dev),
             "inputs": torch.zeros(2 * T + 4 * self.max_rows, dtype=torch.long, device=dev),
         }
-        # split-K decode scratch (scores, block maxima, partial sums) for the single-step rows of a tick
+        # decode workspace for the single-step rows of a tick (used by hsg_ring_decode above 8 query heads per kv head)
         ws = lib().hsg_ring_decode_workspace_bytes(self.max_rows, hkv, hq // hkv, self.window)
         self.ring_ws = torch.empty(max(int(ws), 16), dtype=torch.uint8, device=dev)
         # chunked-GDN scratch for the long rows of a tick (one 64-token chunk per row) and their raw outputs
@@ -390,7 +390,7 @@ class SlotStreamEngine(PreparedWeights):
                                       k.data_ptr(), hkv * D, D, pos.data_ptr(), self.inv_freq.data_ptr(),
                                       cfg.rotary_dim, tb, D, st), "hsg_norm_rope")
                 att = self._view("mid", tb, hq * D)
-                # single-step rows: split-K decode; rows of two or more steps: the tiled kernel (min_len 2)
+                # single-step rows: hsg_ring_decode; rows of two or more steps: the tiled kernel (min_len 2)
                 check(L.hsg_ring_decode(
                     q.data_ptr(), 0, hq * D, G * D, D,
                     self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,

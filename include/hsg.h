@@ -170,17 +170,18 @@ int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, 
                        int64_t o_sn, int64_t o_sl, int64_t o_sh, int64_t o_sg, void* stream);
 
 /*
- * Split-K ring attention for decode steps: the same contract and numerics as hsg_ring_attention for rows with
+ * Ring attention for decode steps: the same contract and numerics as hsg_ring_attention for rows with
  * lens[n] == 1 (one query position; lb is 1 and the padded layout is [n_rows, 1, ...]). Replaces
  * ring_attention_v8 at its decode shape (src/hs_guard/engine/fused_kernels.py:358-376 with Lb == 1,
- * write_ring True, the reference's per-token streaming step). Three launches on `stream`: scores and 32-key
- * block maxima per (row, kv head, quarter of the ring columns); per-block probabilities with the running
- * maximum recovered as the prefix maximum of the block maxima, times values; combine, gate, ring write.
- * Packed layout: rows with lens[n] != 1 are not touched. Padded layout: rows with lens[n] == 0 (or a slot
- * outside [0, ring_rows)) get zero outputs. workspace: device memory of at least
- * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes, 16-byte aligned; its contents need
- * no initialisation and are garbage afterwards. Supported: head_dim == 256, window <= 512 and a multiple of
- * 32, groups <= 16.
+ * write_ring True, the reference's per-token streaming step). The running maximum of each 32-key block is
+ * recovered as the prefix maximum of the block maxima, so the blocks are processed in parallel. groups <= 8:
+ * one launch on `stream` (one workgroup per row and kv head, scores in LDS, the workspace untouched); groups
+ * 9..16: three launches (scores and block maxima per quarter of the ring columns into the workspace; per-block
+ * probabilities times values; combine, gate, ring write). Packed layout: rows with lens[n] != 1 are not
+ * touched. Padded layout: rows with lens[n] == 0 (or a slot outside [0, ring_rows)) get zero outputs.
+ * workspace: device memory of at least hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes,
+ * 16-byte aligned; its contents need no initialisation and are garbage afterwards. Supported: head_dim == 256,
+ * window <= 512 and a multiple of 32, groups <= 16.
  */
 size_t hsg_ring_decode_workspace_bytes(int32_t n_rows, int32_t hkv, int32_t groups, int32_t window);
 int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,
@@ -195,9 +196,10 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
 /*
  * hsg_ring_decode without the workspace argument: it allocates nothing. No counterpart in the reference; it is
  * for callers that cannot allocate device memory (code under hipGraph capture, allocation-free serving loops,
- * harnesses that forbid hipMalloc). The split-K scratch is the library's own static device array of
- * HSG_RING_DECODE_SCRATCH_BYTES, one copy per GPU, held until the process ends; its device address is looked up
- * on the first call made on each device (make that first call outside graph capture). Arguments, outputs and
+ * harnesses that forbid hipMalloc). The workspace (used by the split-K path, groups > 8) is the library's own
+ * static device array of HSG_RING_DECODE_SCRATCH_BYTES, one copy per GPU, held until the process ends; its
+ * device address is looked up on the first call made on each device (make that first call outside graph
+ * capture). Arguments, outputs and
  * numerics are those of hsg_ring_decode, bit for bit. Returns HSG_ERR_SHAPE when
  * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 486 rows at 4 kv
  * heads, G = 4, W = 512). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams,

@@ -121,11 +121,11 @@ def _decode_case(seed, N, Hkv, G, W, S, fills, lens, D=256):
     return q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, torch.tensor(lens, dtype=torch.long)
 
 
-@pytest.mark.parametrize("G,W", [(4, 512), (1, 64), (2, 128), (8, 512)])
+@pytest.mark.parametrize("G,W", [(4, 512), (1, 64), (2, 128), (8, 512), (16, 256)])
 def test_split_k_decode_matches_oracle_and_tiled_kernel(G, W):
-    """hsg_ring_decode (split-K) against the blockwise oracle and against the tiled kernel on the same decode
-    tick: full, partial and empty rings (only the step's own key visible), a row with lens 0 (zeros), ring
-    write bit-exact."""
+    """hsg_ring_decode against the blockwise oracle and against the tiled kernel on the same decode tick: full,
+    partial and empty rings (only the step's own key visible), a row with lens 0 (zeros), ring write bit-exact.
+    Groups <= 8 run the fused one-launch kernel, G = 16 the three split-K kernels."""
     from hs_guard.engine.kernels import ring_attention_v8
     print(f"[ring] split-K decode G={G} W={W}", flush=True)
     N, Hkv, S, D = 6, 2, 8, 256
