@@ -1,0 +1,197 @@
+// The step's projection GEMMs on hipBLASLt with a fixed algorithm per problem.
+//
+// torch.mm hands every call to hipBLASLt's first heuristic candidate. Faster solutions exist for the step's shapes
+// (about 10-15 % on the mixed step's products), but a choice made by timing at start-up differs between processes,
+// and solutions differ in accumulation order, so results would change from run to run. Here the solution is a
+// caller-given hipBLASLt solution index, taken from a plan table generated once and committed
+// (hs_guard/engine/gemm_plan.py); index -1 is the heuristic's first candidate. The reference's products are the
+// nn.Linear layers of its backbone (src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89).
+//
+// Layout: D[M, N] = A[M, K] . W[N, K]^T, all row-major bf16 with row strides lda, ldw, ldd; fp32 accumulation. In
+// hipBLASLt's column-major terms that is D^T (N x M) = op_T(W^T as K x N) . A^T (K x M).
+#include <hipblaslt/hipblaslt-ext.hpp>
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "hsg_common.h"
+
+namespace {
+
+struct Plan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, ld = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t workspace = 0;
+};
+
+using PlanKey = std::tuple<int32_t, int32_t, int32_t, int64_t, int64_t, int64_t, int32_t>;
+
+struct DeviceCtx {
+  hipblasLtHandle_t handle = nullptr;
+  std::map<PlanKey, Plan> plans;
+};
+
+constexpr int kMaxDevices = 64;
+std::mutex ctx_mu;
+DeviceCtx ctx[kMaxDevices];
+
+// hipBLASLt status -> library code (HIP errors are positive, argument errors negative)
+int blas_status(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? HSG_OK : HSG_ERR_BLAS; }
+
+// the current device's context, its handle created on first use (call it outside graph capture first)
+int device_ctx(DeviceCtx** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return HSG_ERR_ARG;
+  DeviceCtx& c = ctx[dev];
+  if (c.handle == nullptr && hipblasLtCreate(&c.handle) != HIPBLAS_STATUS_SUCCESS) {
+    c.handle = nullptr;
+    return HSG_ERR_BLAS;
+  }
+  *out = &c;
+  return HSG_OK;
+}
+
+void destroy_plan(Plan& p) {
+  if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+  if (p.lw) hipblasLtMatrixLayoutDestroy(p.lw);
+  if (p.ld) hipblasLtMatrixLayoutDestroy(p.ld);
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  p = Plan{};
+}
+
+// descriptor and layouts of one problem (no algorithm yet)
+int describe(int32_t M, int32_t N, int32_t K, int64_t lda, int64_t ldw, int64_t ldd, Plan& p) {
+  const hipblasOperation_t op_w = HIPBLAS_OP_T, op_a = HIPBLAS_OP_N;
+  if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_w, sizeof(op_w)) !=
+          HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_a, sizeof(op_a)) !=
+          HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, K, N, ldw) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, K, M, lda) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.ld, HIP_R_16BF, N, M, ldd) != HIPBLAS_STATUS_SUCCESS) {
+    destroy_plan(p);
+    return HSG_ERR_BLAS;
+  }
+  return HSG_OK;
+}
+
+// up to `count` heuristic candidates for a described problem, in hipBLASLt's order, with workspace <= limit
+int heuristic(DeviceCtx& c, Plan& p, size_t limit, int count, std::vector<hipblasLtMatmulHeuristicResult_t>& out) {
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return HSG_ERR_BLAS;
+  uint64_t lim = limit;
+  hipblasStatus_t s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &lim,
+                                                            sizeof(lim));
+  out.assign(count, hipblasLtMatmulHeuristicResult_t{});
+  int found = 0;
+  if (s == HIPBLAS_STATUS_SUCCESS)
+    s = hipblasLtMatmulAlgoGetHeuristic(c.handle, p.desc, p.lw, p.la, p.ld, p.ld, pref, count, out.data(), &found);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (s != HIPBLAS_STATUS_SUCCESS || found <= 0) return HSG_ERR_BLAS;
+  out.resize(found);
+  return HSG_OK;
+}
+
+// the plan of a problem with the given solution (-1: first heuristic candidate), cached per device
+int get_plan(DeviceCtx& c, int32_t M, int32_t N, int32_t K, int64_t lda, int64_t ldw, int64_t ldd, int32_t index,
+             size_t limit, Plan** out) {
+  const PlanKey key{M, N, K, lda, ldw, ldd, index};
+  auto it = c.plans.find(key);
+  if (it != c.plans.end()) {
+    *out = &it->second;
+    return HSG_OK;
+  }
+  Plan p;
+  int rc = describe(M, N, K, lda, ldw, ldd, p);
+  if (rc != HSG_OK) return rc;
+  if (index < 0) {
+    std::vector<hipblasLtMatmulHeuristicResult_t> res;
+    rc = heuristic(c, p, limit, 1, res);
+    if (rc != HSG_OK) {
+      destroy_plan(p);
+      return rc;
+    }
+    p.algo = res[0].algo;
+    p.workspace = res[0].workspaceSize;
+  } else {
+    std::vector<int> idx{index};
+    std::vector<hipblasLtMatmulHeuristicResult_t> res;
+    const float alpha = 1.f, beta = 0.f;
+    size_t ws = 0;
+    if (hipblaslt_ext::getAlgosFromIndex(c.handle, idx, res) != HIPBLAS_STATUS_SUCCESS || res.empty() ||
+        hipblaslt_ext::matmulIsAlgoSupported(c.handle, p.desc, &alpha, p.lw, p.la, &beta, p.ld, p.ld, res[0].algo,
+                                             ws) != HIPBLAS_STATUS_SUCCESS) {
+      destroy_plan(p);
+      return HSG_ERR_SHAPE;   // the solution does not exist in this hipBLASLt or does not support the problem
+    }
+    p.algo = res[0].algo;
+    p.workspace = ws;
+  }
+  auto ins = c.plans.emplace(key, p);
+  *out = &ins.first->second;
+  return HSG_OK;
+}
+
+bool bad_problem(int32_t M, int32_t N, int32_t K, int64_t lda, int64_t ldw, int64_t ldd) {
+  return M <= 0 || N <= 0 || K <= 0 || lda < K || ldw < K || ldd < N;
+}
+
+}  // namespace
+
+extern "C" int hsg_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd,
+                             int32_t M, int32_t N, int32_t K, int32_t algo_index, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  if (!A || !W || !D || bad_problem(M, N, K, lda, ldw, ldd) || algo_index < -1) return HSG_ERR_ARG;
+  if (workspace_bytes > 0 && !workspace) return HSG_ERR_ARG;
+  std::lock_guard<std::mutex> lock(ctx_mu);
+  DeviceCtx* c = nullptr;
+  int rc = device_ctx(&c);
+  if (rc != HSG_OK) return rc;
+  Plan* p = nullptr;
+  rc = get_plan(*c, M, N, K, lda, ldw, ldd, algo_index, workspace_bytes, &p);
+  if (rc != HSG_OK) return rc;
+  if (p->workspace > workspace_bytes) return HSG_ERR_SHAPE;
+  const float alpha = 1.f, beta = 0.f;
+  const hipblasStatus_t s = hipblasLtMatmul(c->handle, p->desc, &alpha, W, p->lw, A, p->la, &beta, D, p->ld, D,
+                                            p->ld, &p->algo, workspace, p->workspace,
+                                            reinterpret_cast<hipStream_t>(stream));
+  return blas_status(s);
+}
+
+extern "C" int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_t* workspace,
+                                   int32_t max_count, size_t workspace_limit) {
+  if (!indices || max_count <= 0 || bad_problem(M, N, K, K, K, N)) return -1;
+  std::lock_guard<std::mutex> lock(ctx_mu);
+  DeviceCtx* c = nullptr;
+  if (device_ctx(&c) != HSG_OK) return -1;
+  Plan p;
+  if (describe(M, N, K, K, K, N, p) != HSG_OK) return -1;
+  std::vector<hipblasLtMatmulHeuristicResult_t> res;
+  const int rc = heuristic(*c, p, workspace_limit, max_count, res);
+  destroy_plan(p);
+  if (rc != HSG_OK) return -1;
+  int n = 0;
+  for (auto& r : res) {
+    const int idx = hipblaslt_ext::getIndexFromAlgo(r.algo);
+    if (idx < 0) continue;
+    indices[n] = idx;
+    if (workspace) workspace[n] = r.workspaceSize;
+    ++n;
+  }
+  return n;
+}
+
+extern "C" int hsg_gemm_blas_version(void) {
+  std::lock_guard<std::mutex> lock(ctx_mu);
+  DeviceCtx* c = nullptr;
+  if (device_ctx(&c) != HSG_OK) return -1;
+  int v = 0;
+  return hipblasLtGetVersion(c->handle, &v) == HIPBLAS_STATUS_SUCCESS ? v : -1;
+}

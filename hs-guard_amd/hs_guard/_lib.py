@@ -99,6 +99,10 @@ SIGNATURES = {
     "hsg_risk_head": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
     "hsg_risk_head_f32": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
     "hsg_ring_pos_update": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I32, _P]),
+    "hsg_gemm_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P, ctypes.c_size_t,
+                                     _P]),                  # A, lda, W, ldw, D, ldd, M, N, K, algo, ws, ws_bytes, stream
+    "hsg_gemm_candidates": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, ctypes.c_size_t]),
+    "hsg_gemm_blas_version": (ctypes.c_int, []),
 }
 
 _lib = None

@@ -25,6 +25,8 @@ import torch
 
 from .._lib import check, lib
 from ..model import ROLES, GuardModel
+from .gemm_plan import WORKSPACE_BYTES as GEMM_WORKSPACE_BYTES
+from .gemm_plan import GemmPlans
 
 SESSION_BUCKETS = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 160, 192, 224, 256, 320, 352, 384, 448, 512)
 STATE_DTYPES = {"float32": torch.float32, "float16": torch.float16}
@@ -256,6 +258,9 @@ class SlotStreamEngine(PreparedWeights):
             "probs": torch.zeros(len(self.roles) * T * 3, dtype=torch.float32, device=dev),
             "inputs": torch.zeros(2 * T + 4 * self.max_rows, dtype=torch.long, device=dev),
         }
+        # hipBLASLt workspace of the projection GEMMs and their committed solution table (hs_guard/engine/gemm_plan.py)
+        self.gemm_plans = GemmPlans.load()
+        self.gemm_ws = torch.empty(GEMM_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
         # decode workspace for the single-step rows of a tick (used by hsg_ring_decode above 8 query heads per kv head)
         ws = lib().hsg_ring_decode_workspace_bytes(self.max_rows, hkv, hq // hkv, self.window)
         self.ring_ws = torch.empty(max(int(ws), 16), dtype=torch.uint8, device=dev)
@@ -264,6 +269,21 @@ class SlotStreamEngine(PreparedWeights):
             ws = lib().hsg_gdn_chunk_workspace_bytes(self.max_rows, self.max_tick_tokens, cfg.linear_num_value_heads)
             self.chunk_ws = torch.empty(max(int(ws), 256), dtype=torch.uint8, device=dev)
             self.buf["gdn_o"] = torch.zeros(T * cfg.value_dim, dtype=bf16, device=dev)
+
+    def mm(self, x, w, out):
+        """out[M, N] = x[M, K] . w[N, K]^T (bf16, row-major, unit column stride) on the current stream, through
+        hsg_gemm_bf16 with the committed solution for (M, N, K) (hipBLASLt's first heuristic candidate for shapes the
+        table lacks). Every projection of the tick goes through here, so a test that wants the engine's exact
+        products calls this too."""
+        M, K = x.shape
+        N = w.shape[0]
+        if w.shape[1] != K or out.shape != (M, N) or x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
+            raise ValueError("mm: shapes or strides do not match D[M, N] = A[M, K] . W[N, K]^T")
+        check(lib().hsg_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+                                  M, N, K, self.gemm_plans.index(M, N, K), self.gemm_ws.data_ptr(),
+                                  self.gemm_ws.numel(), torch.cuda.current_stream(self.device).cuda_stream),
+              "hsg_gemm_bf16")
+        return out
 
     def _view(self, name, *shape):
         n = 1
@@ -340,7 +360,7 @@ class SlotStreamEngine(PreparedWeights):
             if kind == "linear_attention":
                 C = cfg.conv_dim
                 proj = self._view("proj", tb, self.gdn_in)
-                torch.mm(normed, Lw["w_in"].t(), out=proj)
+                self.mm(normed, Lw["w_in"], proj)
                 out = self._view("mid", tb, cfg.value_dim)
                 base = proj.data_ptr()
                 # rows are packed longest first: in a prefill-like tick the rows of >= chunk_min_tokens tokens go
@@ -378,10 +398,10 @@ class SlotStreamEngine(PreparedWeights):
                             self._view("gdn_o", tb, cfg.value_dim).data_ptr(), base + 2 * C, self.gdn_in,
                             Lw["norm_w"].data_ptr(), eps, out.data_ptr(), self.chunk_min_tokens,
                             self.chunk_ws.data_ptr(), self.chunk_ws.numel(), st), "hsg_gdn_chunk_prefill_gated")
-                torch.mm(out, Lw["w_out"].t(), out=mix)
+                self.mm(out, Lw["w_out"], mix)
             else:
                 proj = self._view("proj", tb, self.att_in)
-                torch.mm(normed, Lw["w_in"].t(), out=proj)
+                self.mm(normed, Lw["w_in"], proj)
                 q = self._view("q", tb, hq * D)
                 k = self._view("k", tb, hkv * D)
                 base = proj.data_ptr()
@@ -410,15 +430,15 @@ class SlotStreamEngine(PreparedWeights):
                     self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
                     nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
                     att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
-                torch.mm(att, Lw["w_out"].t(), out=mix)
+                self.mm(att, Lw["w_out"], mix)
             check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), Lw["post_w1"].data_ptr(), eps,
                                     normed.data_ptr(), tb, H, st), "hsg_add_rmsnorm")
             I = cfg.intermediate_size
             gu = self._view("proj", tb, 2 * I)
-            torch.mm(normed, Lw["w_gu"].t(), out=gu)
+            self.mm(normed, Lw["w_gu"], gu)
             act = self._view("mid", tb, I)
             check(L.hsg_silu_mul(gu.data_ptr(), 2 * I, I, act.data_ptr(), tb, st), "hsg_silu_mul")
-            torch.mm(act, Lw["w_down"].t(), out=mix)
+            self.mm(act, Lw["w_down"], mix)
             nxt = self.layers[i + 1]["in_w1"] if i + 1 < len(self.layers) else self.final_w1
             check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), nxt.data_ptr(), eps, normed.data_ptr(), tb, H,
                                     st), "hsg_add_rmsnorm")

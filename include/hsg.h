@@ -31,6 +31,7 @@ extern "C" {
 #define HSG_ERR_ARG (-1)     /* null pointer or non-positive / inconsistent size */
 #define HSG_ERR_ALIGN (-2)   /* pointer or stride breaks the vector-load alignment the kernel needs */
 #define HSG_ERR_SHAPE (-3)   /* head size / window outside what the kernels are built for */
+#define HSG_ERR_BLAS (-4)    /* a hipBLASLt call failed (hsg_gemm_*) */
 
 #define HSG_STATE_F32 0
 #define HSG_STATE_F16 1
@@ -309,6 +310,30 @@ int hsg_risk_head_f32(const float* y, int64_t y_stride, const float* ln_w, const
 int hsg_ring_pos_update(int64_t* ring_pos, int64_t ring_rows, int32_t window, const int64_t* slots,
                         const int64_t* starts, const int64_t* lens, int32_t n_rows, int32_t lb_max,
                         void* stream);
+
+/*
+ * Projection GEMM on hipBLASLt with a fixed solution: D[M, N] = A[M, K] . W[N, K]^T, bf16 row-major with row
+ * strides lda, ldw, ldd (elements), fp32 accumulation. Replaces the backbone's nn.Linear products
+ * (src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89). algo_index: a hipBLASLt solution index (from a
+ * committed plan table, so every process runs the same accumulation order), or -1 for hipBLASLt's first
+ * heuristic candidate (torch.mm's choice). workspace: device memory for solutions that need it. Returns
+ * HSG_ERR_SHAPE when the solution does not exist in this hipBLASLt, does not support the problem or needs more
+ * than workspace_bytes, HSG_ERR_BLAS when hipBLASLt fails. The first call on a device creates its hipBLASLt
+ * handle (make it outside graph capture); later calls are capturable.
+ */
+int hsg_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd, int32_t M,
+                  int32_t N, int32_t K, int32_t algo_index, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Up to max_count hipBLASLt heuristic candidates for the dense problem (M, N, K) of hsg_gemm_bf16, in hipBLASLt's
+ * order, as solution indices (and each one's workspace bytes, when `workspace` is non-NULL), limited to
+ * workspace_limit bytes of workspace. Returns the count, or -1. For generating a plan table.
+ */
+int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_t* workspace, int32_t max_count,
+                        size_t workspace_limit);
+
+/* hipBLASLt's version on the current device (solution indices are valid only for the version they came from). */
+int hsg_gemm_blas_version(void);
 
 #ifdef __cplusplus
 }

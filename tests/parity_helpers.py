@@ -1,10 +1,11 @@
 """Helpers shared by the engine-vs-oracle GPU tests (imported by them; holds no tests itself).
 
 ``matched_gemm(engine)`` gives the oracle (``StreamOracle.tick(..., gemm=...)``) the engine's own bf16 product:
-the same torch.mm / addmm into a [tb, N] buffer, tb the engine's token bucket, with the rows packed in the
-engine's order (longest first, ties in request order). Each output row of a hipBLASLt product is then
-bitwise the engine's for the same input row, so an engine-vs-oracle comparison checks every other kernel
-(conv, recurrence, norms, RoPE, ring attention, heads, bookkeeping) against the CPU restatement.
+the engine's ``mm`` (hsg_gemm_bf16 with the same committed hipBLASLt solution for (tb, N, K)), or torch.addmm for
+the heads' biased product, into a [tb, N] buffer, tb the engine's token bucket, with the rows packed in the
+engine's order (longest first, ties in request order). Each output row is then bitwise the engine's for the same
+input row, so an engine-vs-oracle comparison checks every other kernel (conv, recurrence, norms, RoPE, ring
+attention, heads, bookkeeping) against the CPU restatement.
 """
 import numpy as np
 import torch
@@ -34,7 +35,7 @@ def matched_gemm(eng):
         xd = torch.from_numpy(xp).to(torch.bfloat16).cuda()
         out = torch.empty(tb, W.shape[0], dtype=torch.bfloat16, device="cuda")
         if bias is None:
-            torch.mm(xd, W.t(), out=out)
+            eng.mm(xd, W, out)       # the engine's own product: same hipBLASLt solution for (tb, N, K)
         else:
             torch.addmm(torch.from_numpy(bias).to(torch.bfloat16).cuda(), xd, W.t(), out=out)
         y = out.float().cpu().numpy()[:, :w.shape[0]]

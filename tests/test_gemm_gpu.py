@@ -1,0 +1,119 @@
+"""hsg_gemm_bf16, the projections' GEMM with a fixed hipBLASLt solution, and the committed plan table.
+
+D[M, N] = A[M, K] . W[N, K]^T in bf16 with fp32 accumulation (the reference's nn.Linear products,
+src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89). Checked against the fp32 product of the same bf16
+inputs: relative Frobenius error within 2^-7 (bf16 output rounding plus accumulation order), repeated calls equal
+bit for bit, every plan-table solution runnable on its problem, and the engine's mm equal to a direct call with
+the table's solution.
+"""
+import ctypes
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(8448, 1024), (1024, 2048), (10240, 1024), (1024, 4096), (7168, 1024), (1024, 3584)]
+
+
+def _run(A, W, index, ws):
+    from hs_guard._lib import lib
+    M, K = A.shape
+    N = W.shape[0]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=A.device)
+    rc = lib().hsg_gemm_bf16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), N, M, N, K, index, ws.data_ptr(),
+                             ws.numel(), torch.cuda.current_stream().cuda_stream)
+    return rc, out
+
+
+def _inputs(M, N, K, seed=0):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    A = torch.randn(M, K, generator=gen, device="cuda").bfloat16()
+    W = (torch.randn(N, K, generator=gen, device="cuda") * 0.02).bfloat16()
+    return A, W
+
+
+def _rel(out, A, W):
+    ref = A.float() @ W.float().t()
+    return ((out.float() - ref).norm() / ref.norm()).item()
+
+
+@pytest.mark.parametrize("M", [1, 17, 352, 1536])
+def test_heuristic_solution_matches_fp32_and_repeats(M):
+    from hs_guard.engine.gemm_plan import WORKSPACE_BYTES
+    print(f"[gemm] heuristic solution M={M}", flush=True)
+    ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device="cuda")
+    for N, K in SHAPES:
+        A, W = _inputs(M, N, K)
+        rc, out = _run(A, W, -1, ws)
+        assert rc == 0, (M, N, K, rc)
+        rc2, out2 = _run(A, W, -1, ws)
+        torch.cuda.synchronize()
+        assert rc2 == 0 and torch.equal(out, out2)
+        assert _rel(out, A, W) <= 2.0 ** -7, (M, N, K)
+
+
+def test_candidates_and_rejections():
+    from hs_guard._lib import lib
+    from hs_guard.engine.gemm_plan import WORKSPACE_BYTES
+    L = lib()
+    ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device="cuda")
+    idx = (ctypes.c_int32 * 16)()
+    wsz = (ctypes.c_size_t * 16)()
+    n = L.hsg_gemm_candidates(1536, 8448, 1024, idx, wsz, 16, WORKSPACE_BYTES)
+    assert 0 < n <= 16 and all(wsz[i] <= WORKSPACE_BYTES for i in range(n))
+    A, W = _inputs(1536, 8448, 1024)
+    for i in range(min(n, 4)):
+        rc, out = _run(A, W, idx[i], ws)
+        assert rc == 0 and _rel(out, A, W) <= 2.0 ** -7
+    assert _run(A, W, 1 << 30, ws)[0] == -3          # no such solution: HSG_ERR_SHAPE, nothing launched
+    out = torch.empty(4, 4, dtype=torch.bfloat16, device="cuda")
+    assert L.hsg_gemm_bf16(A.data_ptr(), 1024, W.data_ptr(), 1024, out.data_ptr(), 8448, 0, 8448, 1024, -1,
+                           ws.data_ptr(), ws.numel(), None) == -1       # M = 0
+    assert L.hsg_gemm_bf16(A.data_ptr(), 512, W.data_ptr(), 1024, out.data_ptr(), 8448, 4, 8448, 1024, -1,
+                           ws.data_ptr(), ws.numel(), None) == -1       # lda < K
+    assert L.hsg_gemm_blas_version() > 0
+
+
+def test_plan_table_solutions_run_on_their_problems():
+    """Every committed solution of a sample of table entries (all shapes, the smallest, a middle and the largest
+    bucket) runs on its problem within the fp32 bar; the table loads for this hipBLASLt."""
+    from hs_guard.engine.gemm_plan import PLAN_PATH, WORKSPACE_BYTES, GemmPlans
+    import json
+    import os
+    if not os.path.exists(PLAN_PATH):
+        pytest.skip("no committed plan table")
+    plans = GemmPlans.load()
+    data = json.load(open(PLAN_PATH))
+    assert plans.table, f"plan table generated for hipBLASLt {data['blas_version']}, not this one"
+    ws = torch.empty(WORKSPACE_BYTES, dtype=torch.uint8, device="cuda")
+    Ms = sorted({k[0] for k in plans.table})
+    sample = {Ms[0], Ms[len(Ms) // 2], Ms[-1]}
+    checked = 0
+    for (M, N, K), index in plans.table.items():
+        if M not in sample:
+            continue
+        A, W = _inputs(M, N, K, seed=M)
+        rc, out = _run(A, W, index, ws)
+        assert rc == 0, (M, N, K, index, rc)
+        assert _rel(out, A, W) <= 2.0 ** -7, (M, N, K, index)
+        checked += 1
+    print(f"[gemm] {checked} committed solutions checked", flush=True)
+    assert checked > 0
+
+
+def test_engine_mm_uses_the_table():
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    model = GuardModel.random(cfg, seed=0, device="cuda")
+    eng = SlotStreamEngine(model, 4, use_graphs=False)
+    w = eng.layers[0]["w_in"]
+    M = 16
+    x = torch.randn(M, w.shape[1], device="cuda").bfloat16()
+    got = eng.mm(x, w, torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda"))
+    rc, ref = _run(x, w, eng.gemm_plans.index(M, w.shape[0], w.shape[1]), eng.gemm_ws)
+    torch.cuda.synchronize()
+    assert rc == 0 and torch.equal(got, ref)
