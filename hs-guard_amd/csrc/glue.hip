@@ -10,48 +10,84 @@ namespace hsg {
 namespace {
 
 // ---------------------------------------------------------------------------------------------------
-// RMSNorm over a 1024-wide row, one wave per token (16 values per lane, two 16-byte loads).
+// RMSNorm over a 1024-wide row, one wave per token. Lane l holds elements 8 l .. 8 l + 7 and 512 + 8 l .. +7, so
+// each 16-byte load or store instruction of the wave covers 1 KB of the row; every load of the token (row, mix,
+// weights) is issued before the first use, so a token costs one memory round trip.
 // add_square + rms_finish (src/hs_guard/engine/fused_kernels.py:30-72): h = bf16(res + mix) (plain fp32
 // add), out = bf16((h * rsqrt(mean(h^2) + eps)) * w1), w1 = 1 + weight in fp32.
 // Embedding variant (slot_engine_v8.py:38,42-43): h = embedding row of the token id.
 // ---------------------------------------------------------------------------------------------------
-constexpr int HID_PER_LANE = 16;
+constexpr int HID = 1024;
+typedef __attribute__((ext_vector_type(4))) float f32x4_;
+
+// 8 bf16 values of a 16-byte piece as fp32
+__device__ __forceinline__ void unpack8(const u32x4& w, float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) unpack2(w[i], x[2 * i], x[2 * i + 1]);
+}
 
 template <bool EMBED, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* hidden, const uint16_t* mix, const int64_t* ids,
                                                       const uint16_t* emb, const float* w1, float eps,
-                                                      uint16_t* normed, int tokens, int width, int64_t vocab) {
+                                                      uint16_t* normed, int tokens, int64_t vocab) {
   const int lane = threadIdx.x & 63;
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= tokens) return;
-  const int per_lane = width / 64;  // 16 for width 1024
-  const int d0 = lane * per_lane;
-  float h[HID_PER_LANE];
-  const int64_t row = (int64_t)tok * width;
+  const int64_t row = (int64_t)tok * HID;
+  const uint16_t* src = hidden + row;
   if constexpr (EMBED) {
     int64_t id = ids[tok];
     if (id < 0 || id >= vocab) id = 0;  // out-of-vocab ids are rejected on the host; never read OOB
-    const uint16_t* src = emb + id * width + d0;
-    for (int i = 0; i < per_lane; i += 8) load8_bf16(src + i, h + i);
-    for (int i = 0; i < per_lane; i += 4) {
-      *reinterpret_cast<uint2*>(hidden + row + d0 + i) = *reinterpret_cast<const uint2*>(src + i);
-    }
-  } else {
-    for (int i = 0; i < per_lane; i += 8) load8_bf16(hidden + row + d0 + i, h + i);
-    if constexpr (ADD) {
-      float m[HID_PER_LANE];
-      for (int i = 0; i < per_lane; i += 8) load8_bf16(mix + row + d0 + i, m + i);
-      for (int i = 0; i < per_lane; ++i) h[i] = rbf(__fadd_rn(h[i], m[i]));
-      for (int i = 0; i < per_lane; i += 4) store4_bf16(hidden + row + d0 + i, h + i);
+    src = emb + id * HID;
+  }
+  u32x4 hw[2], mw[2];
+  f32x4_ wv[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int d = 8 * lane + 512 * j;
+    hw[j] = *reinterpret_cast<const u32x4*>(src + d);
+    if constexpr (ADD) mw[j] = *reinterpret_cast<const u32x4*>(mix + row + d);
+    wv[2 * j] = *reinterpret_cast<const f32x4_*>(w1 + d);
+    wv[2 * j + 1] = *reinterpret_cast<const f32x4_*>(w1 + d + 4);
+  }
+  float h[16];
+  unpack8(hw[0], h);
+  unpack8(hw[1], h + 8);
+  if constexpr (ADD) {
+    float m[16];
+    unpack8(mw[0], m);
+    unpack8(mw[1], m + 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = rbf(__fadd_rn(h[i], m[i]));
+    // h is bf16-exact: its bf16 bits are the upper half of the fp32 word
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = (__float_as_uint(h[8 * j + 2 * i]) >> 16) | (__float_as_uint(h[8 * j + 2 * i + 1]) & 0xffff0000u);
+      hw[j] = o;
     }
   }
+  if constexpr (EMBED || ADD) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(hidden + row + 8 * lane + 512 * j) = hw[j];
+  }
   float ss = 0.f;
-  for (int i = 0; i < per_lane; ++i) ss += h[i] * h[i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss += h[i] * h[i];
   ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)width + eps);
-  float y[HID_PER_LANE];
-  for (int i = 0; i < per_lane; ++i) y[i] = (h[i] * r) * w1[d0 + i];
-  for (int i = 0; i < per_lane; i += 4) store4_bf16(normed + row + d0 + i, y + i);
+  const float r = rsqrtf(ss / (float)HID + eps);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_ w = wv[2 * j + (i >> 1)];
+      o[i] = pack_bf16x2((h[8 * j + 2 * i] * r) * w[(2 * i) & 3], (h[8 * j + 2 * i + 1] * r) * w[(2 * i + 1) & 3]);
+    }
+    *reinterpret_cast<u32x4*>(normed + row + 8 * lane + 512 * j) = o;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -149,8 +185,9 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* x, i
 // square_rows + norm_rope (src/hs_guard/engine/fused_kernels.py:237-284) with the rotary cos/sin of the
 // Qwen3.5 rotary embedding computed in-kernel: freq = pos * inv_freq[i] (fp32), cos/sin rounded to bf16.
 // y = bf16(x * rsqrt(mean(x^2)+eps) * w1); for d < rot: out = bf16(bf16(y*cos) + bf16(rot_half(y)*sin)).
-// The token's rot/2 cos/sin pairs are computed once into LDS (every head of the token shares them); wave w
-// then normalises heads w, w+4, ... of q followed by k, 4 dims per lane.
+// One workgroup per token; wave w handles heads w, w + 4, ... of q followed by k, 4 dims per lane. The rotary
+// inputs are loaded first and every head row of the wave right after, all before the token's rot/2 cos/sin pairs
+// are computed into LDS (every head of the token shares them), so one memory round trip covers the token.
 // ---------------------------------------------------------------------------------------------------
 struct RopeTensor {
   const uint16_t* src; int64_t src_row, src_head; int heads;
@@ -158,6 +195,10 @@ struct RopeTensor {
   uint16_t* out; int64_t out_row, out_head;
 };
 
+constexpr int ROPE_HEADS_PER_WAVE = 8;   // heads of q and k together per token: at most 4 x 8 = 32
+
+// PM: the lane distance of a dim's rotate-half partner (rot / 8), 0 when only known at run time
+template <int PM>
 __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor b, const int64_t* pos,
                                                         const float* inv_freq, int rot, float eps_a, float eps_b,
                                                         int tokens, int D) {
@@ -166,50 +207,72 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
   const int tok = blockIdx.x;
   const int half = rot / 2;
   __shared__ float cs_[128], sn_[128];   // rot <= D = 256
+  const int heads_total = a.heads + b.heads;
+  const int d0 = lane * 4;   // D / 64 = 4 dims per lane
+  // loads retire in order, so the cos/sin wait only for the rotary inputs; rows past the last head reload the
+  // last one and are not stored
+  const float fpos = (float)pos[tok];
+  const float ifreq = inv_freq[threadIdx.x & (half - 1)];
+  uint2 xw[ROPE_HEADS_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < ROPE_HEADS_PER_WAVE; ++i) {
+    const int head = min(wave + 4 * i, heads_total - 1);
+    const bool is_a = head < a.heads;
+    const int hh = is_a ? head : head - a.heads;
+    const uint16_t* src = is_a ? a.src + tok * a.src_row + hh * a.src_head : b.src + tok * b.src_row + hh * b.src_head;
+    xw[i] = *reinterpret_cast<const uint2*>(src + d0);
+  }
+  f32x4_ wa = {0.f, 0.f, 0.f, 0.f}, wb = {0.f, 0.f, 0.f, 0.f};
+  if (a.heads) wa = *reinterpret_cast<const f32x4_*>(a.w1 + d0);
+  if (b.heads) wb = *reinterpret_cast<const f32x4_*>(b.w1 + d0);
   if (threadIdx.x < half) {
-    const float f = (float)pos[tok] * inv_freq[threadIdx.x];
+    const float f = fpos * ifreq;
     cs_[threadIdx.x] = rbf(cosf(f));
     sn_[threadIdx.x] = rbf(sinf(f));
   }
-  __syncthreads();
-  const int heads_total = a.heads + b.heads;
-  const int d0 = lane * 4;   // D / 64 = 4 dims per lane
+  lds_barrier();
   // the partner of dim d (d +- half) sits in lane ^ (half / 4) at the same slot
-  const int pmask = half / 4;
-  for (int head = wave; head < heads_total; head += 4) {
-    const bool is_a = head < a.heads;
-    const uint16_t* src = is_a ? a.src : b.src;
-    const int64_t src_row = is_a ? a.src_row : b.src_row, src_head = is_a ? a.src_head : b.src_head;
-    const float* w1 = is_a ? a.w1 : b.w1;
-    uint16_t* dst = is_a ? a.out : b.out;
-    const int64_t out_row = is_a ? a.out_row : b.out_row, out_head = is_a ? a.out_head : b.out_head;
-    const int hh = is_a ? head : head - a.heads;
-    const float eps = is_a ? eps_a : eps_b;
-    float x[4];
-    load4_bf16(src + tok * src_row + hh * src_head + d0, x);
-    const float4 w4 = *reinterpret_cast<const float4*>(w1 + d0);
-    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-    const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
-    const float r = rsqrtf(ss / (float)D + eps);
-    float y[4];
+  const int pmask = PM ? PM : half / 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = rbf((x[i] * r) * wv[i]);
-    float yp[4];
+  for (int i = 0; i < ROPE_HEADS_PER_WAVE; ++i) {
+    const int head = wave + 4 * i;
+    if (head < heads_total) {
+      const bool is_a = head < a.heads;
+      const int hh = is_a ? head : head - a.heads;
+      const f32x4_ w4 = is_a ? wa : wb;
+      const float eps = is_a ? eps_a : eps_b;
+      float x[4];
+      unpack2(xw[i].x, x[0], x[1]);
+      unpack2(xw[i].y, x[2], x[3]);
+      const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+      // D == 256 (the entry point rejects others): ss / D is exactly ss * 2^-8
+      const float r = rsqrtf(ss * (1.0f / 256.0f) + eps);
+      float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) yp[i] = __shfl_xor(y[i], pmask, 64);
-    float o[4];
+      for (int e = 0; e < 4; ++e) y[e] = rbf((x[e] * r) * w4[e]);
+      float yp[4];
+      if constexpr (PM == 8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = d0 + i;
-      if (d < rot) {
-        const int fi = d < half ? d : d - half;
-        const float rh = d < half ? -yp[i] : yp[i];
-        o[i] = __fadd_rn(rbf(y[i] * cs_[fi]), rbf(rh * sn_[fi]));
+        for (int e = 0; e < 4; ++e) yp[e] = dpp_<0x128>(y[e]);   // row_ror:8 is lane xor 8 within a 16-lane row
       } else {
-        o[i] = y[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yp[e] = __shfl_xor(y[e], pmask, 64);
       }
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = d0 + e;
+        if (d < rot) {
+          const int fi = d < half ? d : d - half;
+          const float rh = d < half ? -yp[e] : yp[e];
+          o[e] = __fadd_rn(rbf(y[e] * cs_[fi]), rbf(rh * sn_[fi]));
+        } else {
+          o[e] = y[e];
+        }
+      }
+      uint16_t* dst = is_a ? a.out + tok * a.out_row + hh * a.out_head : b.out + tok * b.out_row + hh * b.out_head;
+      store4_bf16(dst + d0, o);
     }
-    store4_bf16(dst + tok * out_row + hh * out_head + d0, o);
   }
 }
 
@@ -332,10 +395,10 @@ extern "C" int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vo
   if (tokens < 0 || width != 1024 || vocab <= 0) return tokens < 0 || vocab <= 0 ? HSG_ERR_ARG : HSG_ERR_SHAPE;
   if (tokens == 0) return HSG_OK;
   if (!ids || !emb || !w1 || !hidden || !normed) return HSG_ERR_ARG;
-  if (!aligned(emb, 16) || !aligned(hidden, 16) || !aligned(normed, 16)) return HSG_ERR_ALIGN;
+  if (!aligned(emb, 16) || !aligned(hidden, 16) || !aligned(normed, 16) || !aligned(w1, 16)) return HSG_ERR_ALIGN;
   hipLaunchKernelGGL((rmsnorm_kernel<true, false>), dim3((tokens + 3) / 4), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<uint16_t*>(hidden), nullptr, ids,
-                     static_cast<const uint16_t*>(emb), w1, eps, static_cast<uint16_t*>(normed), tokens, width, vocab);
+                     static_cast<const uint16_t*>(emb), w1, eps, static_cast<uint16_t*>(normed), tokens, vocab);
   return launch_status();
 }
 
@@ -345,16 +408,17 @@ extern "C" int hsg_add_rmsnorm(void* hidden, const void* mix, const float* w1, f
   if (width != 1024) return HSG_ERR_SHAPE;
   if (tokens == 0) return HSG_OK;
   if (!hidden || !w1 || !normed) return HSG_ERR_ARG;
-  if (!aligned(hidden, 16) || (mix && !aligned(mix, 16)) || !aligned(normed, 16)) return HSG_ERR_ALIGN;
+  if (!aligned(hidden, 16) || (mix && !aligned(mix, 16)) || !aligned(normed, 16) || !aligned(w1, 16))
+    return HSG_ERR_ALIGN;
   const dim3 grid((tokens + 3) / 4);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (mix)
     hipLaunchKernelGGL((rmsnorm_kernel<false, true>), grid, dim3(256), 0, s, static_cast<uint16_t*>(hidden),
                        static_cast<const uint16_t*>(mix), nullptr, nullptr, w1, eps, static_cast<uint16_t*>(normed),
-                       tokens, width, (int64_t)0);
+                       tokens, (int64_t)0);
   else
     hipLaunchKernelGGL((rmsnorm_kernel<false, false>), grid, dim3(256), 0, s, static_cast<uint16_t*>(hidden),
-                       nullptr, nullptr, nullptr, w1, eps, static_cast<uint16_t*>(normed), tokens, width, (int64_t)0);
+                       nullptr, nullptr, nullptr, w1, eps, static_cast<uint16_t*>(normed), tokens, (int64_t)0);
   return launch_status();
 }
 
@@ -400,6 +464,7 @@ extern "C" int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, i
   if (tokens < 0 || q_heads < 0 || k_heads < 0) return HSG_ERR_ARG;
   if (head_dim != 256 || rot <= 0 || rot > head_dim || rot % 8 != 0 || ((rot / 8) & (rot / 8 - 1)) != 0)
     return HSG_ERR_SHAPE;
+  if (q_heads + k_heads > 32) return HSG_ERR_SHAPE;
   if (tokens == 0 || q_heads + k_heads == 0) return HSG_OK;
   if (!pos || !inv_freq || (q_heads && (!q_src || !q_w1 || !q_out)) || (k_heads && (!k_src || !k_w1 || !k_out)))
     return HSG_ERR_ARG;
@@ -411,8 +476,14 @@ extern "C" int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, i
                q_out_row, q_out_head};
   RopeTensor b{static_cast<const uint16_t*>(k_src), k_row, k_head, k_heads, k_w1, static_cast<uint16_t*>(k_out),
                k_out_row, k_out_head};
-  hipLaunchKernelGGL(norm_rope_kernel, dim3((unsigned)tokens), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a,
-                     b, pos, inv_freq, rot, q_eps, k_eps, tokens, head_dim);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)tokens);
+  if (rot == 64)
+    hipLaunchKernelGGL(norm_rope_kernel<8>, grid, dim3(256), 0, st, a, b, pos, inv_freq, rot, q_eps, k_eps, tokens,
+                       head_dim);
+  else
+    hipLaunchKernelGGL(norm_rope_kernel<0>, grid, dim3(256), 0, st, a, b, pos, inv_freq, rot, q_eps, k_eps, tokens,
+                       head_dim);
   return launch_status();
 }
 

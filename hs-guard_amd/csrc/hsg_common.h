@@ -14,27 +14,21 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 // ---- bf16 / fp16 scalar conversions (bf16 stored as uint16_t; round to nearest even like torch) ----
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
-
-// round-to-nearest-even fp32 -> bf16 without the NaN case (callers pass finite values), branch-free
-__device__ __forceinline__ uint16_t f2bf_finite(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
-
-// two finite fp32 values -> packed bf16 pair (a in the low half), round to nearest even: one v_cvt_pk_bf16_f32
+// two fp32 values -> packed bf16 pair (a in the low half), round to nearest even like torch: one
+// v_cvt_pk_bf16_f32 (a NaN stays a NaN)
 typedef __attribute__((ext_vector_type(2))) float f32x2_;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_;
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_){a, b}, bf16x2_));
 }
+
+// fp32 -> bf16 on the same hardware conversion (branch-free)
+__device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)pack_bf16x2(f, f); }
+
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// the same for values known to be finite (kept for call sites that state it)
+__device__ __forceinline__ uint16_t f2bf_finite(float f) { return f2bf(f); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }

@@ -221,7 +221,8 @@ int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl, int64_t q
  * (src/hs_guard/engine/slot_engine_v8.py:38,42-43; fused_kernels.py:30-72):
  *   hidden[t] = emb[ids[t]];  normed[t] = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1)
  *   emb [vocab, width] bf16, w1 [width] fp32 (= 1 + weight), hidden/normed [tokens, width] bf16.
- * Supported: width == 1024. Ids outside [0, vocab) read row 0 (the host rejects them first).
+ * Supported: width == 1024; emb, hidden, normed and w1 16-byte aligned. Ids outside [0, vocab) read row 0 (the
+ * host rejects them first).
  */
 int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vocab, const float* w1, float eps,
                       void* hidden, void* normed, int32_t tokens, int32_t width, void* stream);
@@ -230,7 +231,8 @@ int hsg_embed_rmsnorm(const int64_t* ids, const void* emb, int64_t vocab, const 
  * Residual add + RMSNorm. Replaces add_square + sq.mean + rms_finish
  * (src/hs_guard/engine/fused_kernels.py:30-72; slot_engine_v8.py:49-55):
  *   hidden = bf16(hidden + mix) (in place; mix may be NULL: no add);
- *   normed = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1). Supported: width == 1024.
+ *   normed = bf16((hidden * rsqrt(mean(hidden^2) + eps)) * w1). Supported: width == 1024; hidden, mix, normed
+ *   and w1 16-byte aligned.
  */
 int hsg_add_rmsnorm(void* hidden, const void* mix, const float* w1, float eps, void* normed, int32_t tokens,
                     int32_t width, void* stream);
@@ -265,7 +267,7 @@ int hsg_conv_silu_update(const void* qkv, int64_t qkv_stride, void* pool, int64_
  * rotary cos/sin of the backbone (slot_engine_v8.py:39): cos/sin = bf16(cos/sin(pos[t] * inv_freq[i])).
  *   x[t, h, :] at src + t*row + h*head;  out[t, h, :] at out + t*out_row + h*out_head (bf16).
  *   w1 [head_dim] fp32 per tensor (16-byte aligned); inv_freq [rot/2] fp32; pos [tokens] int64.
- * Supported: head_dim == 256, rot a power of two in [8, 256].
+ * Supported: head_dim == 256, rot a power of two in [8, 256], q_heads + k_heads <= 32.
  */
 int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_heads, const float* q_w1,
                   float q_eps, void* q_out, int64_t q_out_row, int64_t q_out_head, const void* k_src,
