@@ -330,13 +330,34 @@ __global__ __launch_bounds__(256) void ring_write_kernel(const RingParams p) {
   const int64_t nk_row = padded ? n * p.nk_sn : base_tok * p.nk_sl;
   const int64_t nv_row = padded ? n * p.nv_sn : base_tok * p.nv_sl;
   const int64_t ring_base = ((slot * p.hkv + h) * (int64_t)(p.W + 1)) * D;
-  for (int e = threadIdx.x; e < (int)len * (D / 4); e += 256) {
-    const int j = e / (D / 4);
-    const int d = (e - j * (D / 4)) * 4;
-    const int64_t col = (p.starts[n] + j) % p.W;
-    const int64_t dst = ring_base + col * D + d;
-    *reinterpret_cast<uint2*>(p.ring_k + dst) = *reinterpret_cast<const uint2*>(p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh + d);
-    *reinterpret_cast<uint2*>(p.ring_v + dst) = *reinterpret_cast<const uint2*>(p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh + d);
+  const int c0 = (int)(p.starts[n] % p.W);   // ring column of the tick's first step; j < len <= W follow it
+  // 8-byte pieces e = (token j, dims 4 i ..): a thread's pieces are loaded in batches of WB before any of them
+  // is stored (the ring and the new rows could alias as far as the compiler knows, so a load after a store
+  // would wait for it)
+  constexpr int WB = 8;
+  const int total = (int)len * (D / 4);
+  for (int e0 = threadIdx.x; e0 < total; e0 += 256 * WB) {
+    uint2 kw[WB], vw[WB];
+#pragma unroll
+    for (int u = 0; u < WB; ++u) {
+      const int e = min(e0 + 256 * u, total - 1);
+      const int j = e / (D / 4);
+      const int d = (e - j * (D / 4)) * 4;
+      kw[u] = *reinterpret_cast<const uint2*>(p.new_k + nk_row + j * p.nk_sl + h * p.nk_sh + d);
+      vw[u] = *reinterpret_cast<const uint2*>(p.new_v + nv_row + j * p.nv_sl + h * p.nv_sh + d);
+    }
+#pragma unroll
+    for (int u = 0; u < WB; ++u) {
+      const int e = e0 + 256 * u;
+      if (e < total) {
+        const int j = e / (D / 4);
+        const int d = (e - j * (D / 4)) * 4;
+        const int col = c0 + j < p.W ? c0 + j : c0 + j - p.W;
+        const int64_t dst = ring_base + (int64_t)col * D + d;
+        *reinterpret_cast<uint2*>(p.ring_k + dst) = kw[u];
+        *reinterpret_cast<uint2*>(p.ring_v + dst) = vw[u];
+      }
+    }
   }
 }
 
