@@ -33,6 +33,17 @@ __device__ __forceinline__ uint16_t f2bf_finite(float f) { return f2bf(f); }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// ---- streaming loads of data read once per step (ring keys and values): the non-temporal hint, which on
+// MI355X measured faster for these reads than ordinary loads (fused ring decode 142.0 -> 135.6 us at
+// 352 x 1 on full rings) ----
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+__device__ __forceinline__ uint4 ld_stream16(const uint16_t* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
+__device__ __forceinline__ uint2 ld_stream8(const uint16_t* p) {
+  return __builtin_bit_cast(uint2, __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p)));
+}
+
 // ---- vector loads of bf16 (addresses must be 16 / 8 byte aligned; the C-ABI checks) ----
 __device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
   lo = __uint_as_float(w << 16);

@@ -495,7 +495,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks)
-          ka[t][ks] = *reinterpret_cast<const uint4*>(kbase + (16 * t + m16) * D + 32 * ks + 8 * g4);
+          ka[t][ks] = ld_stream16(kbase + (16 * t + m16) * D + 32 * ks + 8 * g4);
       float bmax = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
     // the first block's values go out now (the keys' registers are free) and arrive across the barriers
     const uint16_t* vbase = p.ring_v + (ring_at + wave * KB) * D + 4 * lane;
 #pragma unroll
-    for (int k = 0; k < KB; ++k) vr[k] = *reinterpret_cast<const uint2*>(vbase + k * D);
+    for (int k = 0; k < KB; ++k) vr[k] = ld_stream8(vbase + k * D);
   }
   if (own_wave) {
     // the step's own key: block RB, one key, always visible to its own query
@@ -609,7 +609,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
     if (i > 0) {
       const uint16_t* vbase = p.ring_v + (ring_at + b * KB) * D + 4 * lane;
 #pragma unroll
-      for (int k = 0; k < KB; ++k) vr[k] = *reinterpret_cast<const uint2*>(vbase + k * D);
+      for (int k = 0; k < KB; ++k) vr[k] = ld_stream8(vbase + k * D);
     }
     const float alpha = (lane < G && mb[i] != -INFINITY) ? exp_fast(mprev - mb[i]) : 0.f;
     if (lane < G) mprev = mb[i];
