@@ -12,9 +12,10 @@
 // launch (ring_write_kernel) after all reads. All key positions of the ring and the tick go to LDS first, and
 // fills (64 keys) whose positions are outside every query's window of the workgroup are skipped. Per fill the
 // workgroup stages K and V row-major in LDS from registers loaded during the previous fill (each load
-// instruction of a wave reads two whole 512-byte key rows); then for each of the fill's two 32-key softmax
-// blocks each wave runs on v_mfma_f32_16x16x32_bf16:
+// instruction of a wave reads two whole 512-byte key rows); then each wave runs on v_mfma_f32_16x16x32_bf16
 //   S^T[key, m] = K . Q^T   (A = K rows from LDS, B = Q from registers; 2 key tiles x 8 d-steps)
+// for both of the fill's 32-key softmax blocks first (four independent accumulation chains instead of two:
+// the fill's critical path is this chain, then the softmax, then P.V), and then, block by block,
 //   O^T[d, m] += V^T . P^T  (A = V^T by LDS transpose reads of the row-major V, B = P straight from the S^T
 //                            accumulators: the k order of the product is the lane's own key order, so P
 //                            never leaves registers)
@@ -230,22 +231,29 @@ __global__ __launch_bounds__(NW * 64, 2) void ring_attn_mfma_kernel(const RingPa
       if (fnext < n_fills) prefetch(fnext);
       __syncthreads();
       if (!has_tile) continue;
-#pragma unroll 1
-      for (int sb = 0; sb < nb; ++sb) {
-        const int kb = sb * KB;   // softmax block within the fill
-        // ---- S^T = K . Q^T for keys kb + [16 kt, 16 kt + 16) ----
-        f32x4 S[2];
+      // ---- S^T = K . Q^T for both softmax blocks of the fill first (four independent accumulation chains) ----
+      f32x4 Sall[SB][2];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          const uint16_t* krow = &Ks[(kb + 16 * kt + mcol) * KS_STRIDE + 8 * q4];
+      for (int sb = 0; sb < SB; ++sb) {
+        if (sb < nb) {
 #pragma unroll
-          for (int ks = 0; ks < D / 32; ++ks) {
-            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * ks));
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[ks], acc, 0, 0, 0);
+          for (int kt = 0; kt < 2; ++kt) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const uint16_t* krow = &Ks[(sb * KB + 16 * kt + mcol) * KS_STRIDE + 8 * q4];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+              const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(krow + 32 * ks));
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[ks], acc, 0, 0, 0);
+            }
+            Sall[sb][kt] = acc;
           }
-          S[kt] = acc;
         }
+      }
+#pragma unroll
+      for (int sb = 0; sb < SB; ++sb) {
+        if (sb >= nb) break;
+        const int kb = sb * KB;   // softmax block within the fill
+        const f32x4 S[2] = {Sall[sb][0], Sall[sb][1]};
         // ---- mask, online softmax over the block (the lane's 8 keys: 4 q4 + i and 16 + 4 q4 + i) ----
         float s[8];
         float bmax = -INFINITY;
