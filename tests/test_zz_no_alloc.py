@@ -2,8 +2,9 @@
 against hsg_ring_decode with a caller-allocated workspace, through the C ABI.
 
 Both entry points run the same kernels on the same inputs, so outputs and ring writes must be bitwise equal.
-Two calls in a row on one GPU, the second with fewer rows, check that the second call reads nothing the first
-left in the shared scratch.
+With 16 query heads per kv head the split-K kernels run and keep their scores, block maxima and partial sums in
+the scratch; with 4 the one-launch fused kernel runs and reads nothing from it. Two calls in a row on one GPU, the
+second with fewer rows, check that the second call reads nothing the first left in the shared scratch.
 """
 import numpy as np
 import pytest
@@ -11,10 +12,10 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-HKV, G, D, W = 4, 4, 256, 512
+HKV, D, W = 4, 256, 512
 
 
-def _case(seed, n, slots_total):
+def _case(seed, n, slots_total, G):
     gen = torch.Generator().manual_seed(seed)
     q = torch.randn(n, HKV, G, D, generator=gen).to(torch.bfloat16)
     ring_k = torch.randn(slots_total, HKV, W + 1, D, generator=gen).to(torch.bfloat16)
@@ -39,7 +40,7 @@ def _call(inp, noalloc):
     L = lib()
     dev = torch.device("cuda:0")
     d = {k: v.to(dev) for k, v in inp.items()}
-    n = d["q"].shape[0]
+    n, G = d["q"].shape[0], d["q"].shape[2]
     out = torch.full((n, 1, HKV * G * D), 7.0, dtype=torch.bfloat16, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     args = (d["q"].data_ptr(), HKV * G * D, D, G * D, D,
@@ -60,10 +61,14 @@ def _call(inp, noalloc):
     return out.cpu(), d["ring_k"].cpu(), d["ring_v"].cpu()
 
 
-def test_noalloc_equals_workspace_entry_point():
-    for seed, n, slots_total in ((0, 352, 360), (1, 24, 40)):
-        print(f"[noalloc] seed {seed}: {n} rows, then the workspace entry point", flush=True)
-        inp = _case(seed, n, slots_total)
+@pytest.mark.parametrize("groups", [16, 4])
+def test_noalloc_equals_workspace_entry_point(groups):
+    from hs_guard._lib import lib
+    # the largest first call that fits the scratch at this geometry, then a much smaller one
+    first = min(352, (48 << 20) // lib().hsg_ring_decode_workspace_bytes(1, HKV, groups, W))
+    for seed, n, slots_total in ((0, first, first + 8), (1, 24, 40)):
+        print(f"[noalloc] G {groups}, seed {seed}: {n} rows, then the workspace entry point", flush=True)
+        inp = _case(seed, n, slots_total, groups)
         a = _call(inp, noalloc=True)
         b = _call(inp, noalloc=False)
         for x, y, what in zip(a, b, ("out", "ring_k", "ring_v")):
@@ -73,7 +78,9 @@ def test_noalloc_equals_workspace_entry_point():
         assert np.all(a[0][~live].float().numpy() == 0)  # rows without a step get zeros (padded layout)
 
 
-def test_noalloc_rejects_sizes_beyond_the_scratch():
+@pytest.mark.parametrize("G", [16, 4])
+def test_noalloc_rejects_sizes_beyond_the_scratch(G):
+    """The size check comes before any pointer is read, so placeholder pointers are never dereferenced."""
     from hs_guard._lib import lib
     L = lib()
     cap = 48 << 20
