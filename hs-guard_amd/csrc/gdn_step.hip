@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   };
   // prefetched burst -> LDS: q <- q / sqrt(|q|^2 + 1e-6) * scale and k <- k / sqrt(|k|^2 + 1e-6) once per token
   // (|x|^2 summed over the 16 lanes holding the vector), v and z as loaded, exp(g) and beta by thread u
-  // CONV: raw rows -> LDS, then each (token, 8 channels) of the burst gets acc = sum_k w[c, k] x[t - 3 + k] in
+  // CONV: raw rows -> LDS, then each (token, 4 channels) of the burst gets acc = sum_k w[c, k] x[t - 3 + k] in
   // fp32 (as conv_silu_kernel) and bf16(silu(bf16(acc))), then q and k are normalised from those outputs
   // (later bursts: hist holds the previous burst's raw rows CT .. CT + 2, read by threads < 144)
   u32x4 hist;
@@ -293,17 +293,19 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       }
     }
     __syncthreads();
+    // items of 4 channels of one token: CT * 96 of them, 3 per thread at CT = 8, so every wave has the same
+    // share (items of 8 channels gave two waves twice the work of the other two)
 #pragma unroll
-    for (int i = 0; i < (CT * 48 + 255) / 256; ++i) {
+    for (int i = 0; i < (CT * 96 + 255) / 256; ++i) {
       const int item = tid + 256 * i;
-      const int u = item / 48, c0 = (item % 48) * 8;
+      const int u = item / 96, c0 = (item % 96) * 4;
       if (u < nt) {
-        u32x4 xr[CKS];
+        u32x2 xr[CKS];
 #pragma unroll
-        for (int k = 0; k < CKS; ++k) xr[k] = *reinterpret_cast<const u32x4*>(&rw_[CONV ? u + k : 0][c0]);
-        u32x4 y;
+        for (int k = 0; k < CKS; ++k) xr[k] = *reinterpret_cast<const u32x2*>(&rw_[CONV ? u + k : 0][c0]);
+        u32x2 y;
 #pragma unroll
-        for (int j = 0; j < 8; j += 2) {
+        for (int j = 0; j < 4; j += 2) {
           float rr[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
           }
           y[j >> 1] = (uint32_t)f2bf(rr[0]) | ((uint32_t)f2bf(rr[1]) << 16);
         }
-        *reinterpret_cast<u32x4*>(&co_[CONV ? u : 0][c0]) = y;
+        *reinterpret_cast<u32x2*>(&co_[CONV ? u : 0][c0]) = y;
       }
     }
     __syncthreads();
