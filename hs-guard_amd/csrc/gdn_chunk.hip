@@ -35,7 +35,7 @@
 // Precision: Kr, Qr, Vr are exact bf16 values (and exact in fp16, which holds bf16's 8-bit significands). The
 // prep kernel forms M' in fp32 throughout (fp32 MFMA for the block substitution). On the state path every fp32
 // operand (S, Z, V', W, and the M', P planes) is scaled by a power of two that puts its largest magnitude just
-// below 2^14, then split into fp16 hi + fp16 lo of the remainder (x 2^s = hi + lo + O(2^-22 |x 2^s|)), and
+// below 2^14 (S, Z, V', W: per value column, the direction every product using them reduces along), then split into fp16 hi + fp16 lo of the remainder (x 2^s = hi + lo + O(2^-22 |x 2^s|)), and
 // multiplied in three fp16 MFMA passes (lo.hi + hi.lo + hi.hi), or two when the other operand is an exact
 // input row; the accumulator is scaled back by 2^-s (exact). That keeps every product within ~2^-22 of fp32
 // (a bf16 hi + lo split reaches only ~2^-17, which moved one bf16 output in 300 instead of one in 10,000).
@@ -148,6 +148,11 @@ __device__ __forceinline__ void split4h(f32x4 x, float scale, s16x4& hi, s16x4& 
   hi = __builtin_bit_cast(s16x4, h);
   lo = __builtin_bit_cast(s16x4, l);
 }
+
+// largest value over the four lanes of one accumulator column (lanes l, l ^ 16, l ^ 32, l ^ 48): the scale of a
+// split operand is shared by the values of one column, which is all that a product reducing along the column
+// (over keys or over tokens) needs
+__device__ __forceinline__ float col_max(float x) { return max_pair32(max_pair16(x)); }
 
 __device__ __forceinline__ float absmax4(f32x4 x, float m) {
   return fmaxf(fmaxf(m, fmaxf(fabsf(x[0]), fabsf(x[1]))), fmaxf(fabsf(x[2]), fabsf(x[3])));
@@ -627,8 +632,8 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
   // Sx[w][2 mt + hl] = split S block mt of column group w, Vx[w][2 I + hl] = split V' token block I
   __shared__ __align__(16) uint16_t Sx[4 * 16 * XP];
   __shared__ __align__(16) uint16_t Vx[4 * 8 * XP];
-  // the inverse power-of-two scales of the handed-over S and V' fragments, per column group
-  __shared__ float s_inv[4], v_inv[4];
+  // the inverse power-of-two scales of the handed-over S and V' fragments, per value column of the block
+  __shared__ __align__(16) float s_inv[BV], v_inv[BV];
 
   // ---- state S[:, vcol] in accumulator layout (chain waves): block mt holds keys 16 mt + 4 g4 + r ----
   ST* sbase = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * (int64_t)KD) * VD + vcol;
@@ -733,14 +738,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) amax = absmax4(S[mt], amax);
       float inv_s;
-      const float ss = pow2_scale(wave_max(amax), &inv_s);
+      const float ss = pow2_scale(col_max(amax), &inv_s);
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt) {
         split4h(S[mt], ss, Sh[mt], Sl[mt]);
         *reinterpret_cast<s16x4*>(sx + (2 * mt) * XP) = Sh[mt];
         *reinterpret_cast<s16x4*>(sx + (2 * mt + 1) * XP) = Sl[mt];
       }
-      if (lane == 0) s_inv[w] = inv_s;
+      if (g4 == 0) s_inv[w * 16 + m16] = inv_s;
       lds_barrier();  // B1: split S handed over
 
       // ---- Y = Kr S for this wave's 16 value columns: S split hi / lo, key blocks paired ----
@@ -774,7 +779,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
           zmax = absmax4(z[I], zmax);
         }
         float inv_z;
-        const float sz = pow2_scale(wave_max(zmax), &inv_z);
+        const float sz = pow2_scale(col_max(zmax), &inv_z);
 #pragma unroll
         for (int I = 0; I < 4; ++I) split4h(z[I], sz, Zh[I], Zl[I]);
         inv_mz = vec[3 * CH + 1] * inv_z;   // the M' planes' inverse scale times Z's
@@ -796,7 +801,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
       }
       {
         float inv_v;
-        const float sv = pow2_scale(wave_max(vmax), &inv_v);
+        const float sv = pow2_scale(col_max(vmax), &inv_v);
 #pragma unroll
         for (int I = 0; I < 4; ++I) {
           s16x4 vh, vl;
@@ -804,7 +809,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
           *reinterpret_cast<s16x4*>(vx + (2 * I) * XP) = vh;
           *reinterpret_cast<s16x4*>(vx + (2 * I + 1) * XP) = vl;
         }
-        if (lane == 0) v_inv[w] = inv_v;
+        if (g4 == 0) v_inv[w * 16 + m16] = inv_v;
       }
       lds_barrier();  // B2: split V' handed over; Q, V and M' of this chunk are no longer read
 
@@ -819,7 +824,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
           wv[J] = Vp[J] * ld4f(&vec[2 * CH + 16 * J + 4 * g4]);
           wmax = absmax4(wv[J], wmax);
         }
-        const float sw = pow2_scale(wave_max(wmax), &inv_w);
+        const float sw = pow2_scale(col_max(wmax), &inv_w);
 #pragma unroll
         for (int J = 0; J < 4; ++J) split4h(wv[J], sw, Wh[J], Wl[J]);
       }
@@ -884,7 +889,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         Sh[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt) * XP);
         Sl[mt] = *reinterpret_cast<const s16x4*>(sx + (2 * mt + 1) * XP);
       }
-      const float inv_s = s_inv[w];
+      const f32x4 inv_s = ld4f(&s_inv[w * 16 + 4 * g4]);   // the scales of this lane's columns 4 g4 .. +3
       f32x4 X[4];
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
@@ -909,7 +914,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
         Vh[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I) * XP);
         Vl[I] = *reinterpret_cast<const s16x4*>(vx + (2 * I + 1) * XP);
       }
-      const float inv_pv = inv_p * v_inv[w];   // the P planes' and V''s inverse scales
+      const f32x4 inv_pv = inv_p * ld4f(&v_inv[w * 16 + 4 * g4]);   // the P planes' and V''s inverse scales
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
         const int t = 16 * I + m16;
