@@ -203,7 +203,7 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
  * capture). Arguments, outputs and
  * numerics are those of hsg_ring_decode, bit for bit. Returns HSG_ERR_SHAPE when
  * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 486 rows at 4 kv
- * heads, G = 4, W = 512). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams,
+ * heads, G = 4, W = 512; 122 rows at G = 16). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams,
  * or two threads) race and must be serialised by the caller; nothing left by an earlier call is read.
  */
 #define HSG_RING_DECODE_SCRATCH_BYTES (48u << 20)
