@@ -212,6 +212,70 @@ def ring_decode_rate(torch, rows=352, iters=50):
     return out
 
 
+def ring_tick_rate(torch, rows=352, iters=50, seed=5):
+    """The tiled ring attention (hsg_ring_attention with min_len 2: the multi-token rows of a tick; the engine gives
+    the single-token rows to hsg_ring_decode) on a config-5 mixed tick: 352 rows, chunk lengths 1 (p 0.8), 2-16
+    (p 0.15), 17-64 (p 0.05), packed layout, 16 q / 4 kv heads of 256, full 512-column rings, ring write off (the
+    engine's separate ring_write_kernel). HIP events on the launch stream around ``iters`` launches. Algorithmic
+    bytes per multi-token row and kv head: its ring keys and values (512 x 256 x 2 B x 2) and positions (512 x 8 B),
+    and per token its new key and value (2 x 512 B), 4 queries and gates in and 4 outputs out (12 x 512 B)."""
+    import numpy as np
+    from hs_guard._lib import lib
+    L = lib()
+    dev = torch.device("cuda:0")
+    hq, hkv, D, W = 16, 4, 256, 512
+    G = hq // hkv
+    rng = np.random.default_rng(seed)
+    u = rng.random(rows)
+    lens_h = np.where(u < 0.8, 1, np.where(u < 0.95, rng.integers(2, 17, rows), rng.integers(17, 65, rows)))
+    lens_h = np.sort(lens_h)[::-1].copy()                  # the engine packs rows longest first
+    T = int(lens_h.sum())
+    offs_h = np.concatenate([[0], np.cumsum(lens_h)[:-1]])
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    att_in = hq * 2 * D + 2 * hkv * D                     # projection row: q | gate interleaved per head, k, v
+    proj = torch.randn(T, att_in, generator=gen, device=dev).bfloat16()
+    q = torch.randn(T, hq * D, generator=gen, device=dev).bfloat16()
+    k = torch.randn(T, hkv * D, generator=gen, device=dev).bfloat16()
+    ring_k = torch.randn(rows + 1, hkv, W + 1, D, generator=gen, device=dev).bfloat16()
+    ring_v = torch.randn(rows + 1, hkv, W + 1, D, generator=gen, device=dev).bfloat16()
+    starts_h = rng.integers(W, 4 * W, rows)
+    ring_pos = torch.full((rows + 1, W + 1), -1, dtype=torch.long)
+    for i in range(rows):
+        cols = np.arange(starts_h[i] - W, starts_h[i])
+        ring_pos[i, cols % W] = torch.from_numpy(cols)
+    ring_pos = ring_pos.to(dev)
+    slots = torch.arange(rows, device=dev)
+    starts = torch.from_numpy(starts_h).to(dev)
+    lens = torch.from_numpy(lens_h).to(dev)
+    offs = torch.from_numpy(offs_h).to(dev)
+    out = torch.empty(T, hq * D, dtype=torch.bfloat16, device=dev)
+    base = proj.data_ptr()
+    stream = torch.cuda.current_stream(dev)
+
+    def run():
+        rc = L.hsg_ring_attention(q.data_ptr(), 0, hq * D, G * D, D, ring_k.data_ptr(), ring_v.data_ptr(), rows + 1,
+                                  W, k.data_ptr(), 0, hkv * D, D, base + 2 * (hq * 2 * D + hkv * D), 0, att_in, D,
+                                  base, 0, att_in, G * 2 * D, 2 * D, D, ring_pos.data_ptr(), slots.data_ptr(),
+                                  starts.data_ptr(), lens.data_ptr(), offs.data_ptr(), rows, 64, hkv, G, D, D ** -0.5,
+                                  0, 2, out.data_ptr(), 0, hq * D, G * D, D, stream.cuda_stream)
+        assert rc == 0, rc
+    for _ in range(5):
+        run()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(iters):
+        run()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / iters
+    multi = lens_h[lens_h >= 2]
+    alg = int(len(multi) * hkv * (W * D * 2 * 2 + W * 8) + int(multi.sum()) * hkv * (2 * 512 + 12 * 512))
+    return {"kernel": "ring_attn_mfma_kernel (hsg_ring_attention, min_len 2)", "rows": int(len(multi)),
+            "tokens": int(multi.sum()), "avg_us": round(us, 2), "alg_bytes_per_launch": alg,
+            "achieved_gbs": round(alg / (us * 1e-6) / 1e9, 1), "hbm_frac": round(alg / (us * 1e-6) / 8e12, 3)}
+
+
 def chunk_prefill_rate(torch, iters=10):
     """Config 4 on hsg_gdn_chunk_prefill: 16 rows of 512/2048/8000 tokens (53,312 tokens, 833 chunks of 64),
     16 heads x 128, fp32 state; HIP events on the launch stream. Algorithmic work per chunk-head
@@ -414,6 +478,8 @@ def main():
                     help="only the dominant-kernel measurement (the command profiled under rocprofv3)")
     ap.add_argument("--chunk-only", action="store_true",
                     help="only the config-4 chunked-prefill measurement (profiled under rocprofv3)")
+    ap.add_argument("--ring-tick-only", action="store_true",
+                    help="only the tiled ring attention on a config-5 mixed tick's multi-token rows")
     ap.add_argument("--ring-only", action="store_true",
                     help="only the 352 x 1-token split-K ring decode measurement (profiled under rocprofv3)")
     ap.add_argument("--lone-row-only", action="store_true",
@@ -448,6 +514,9 @@ def main():
     if args.lone_row_only:
         print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib())}), flush=True)
         return
+    if args.ring_tick_only:
+        print(json.dumps({"ring_attn_tick": ring_tick_rate(torch, rows=args.slots)}), flush=True)
+        return
     if args.chunk_only or args.ring_only:
         leg = chunk_prefill_rate(torch) if args.chunk_only else ring_decode_rate(torch, rows=args.slots)
         calibration_copy(torch, dev)
@@ -457,7 +526,7 @@ def main():
     if args.mixed_only:
         args.sweep_steps = 0
         args.no_cpu_baseline = True
-        roof = ring = chunk = lone = None
+        roof = ring = chunk = lone = tick = None
     else:
         roof = gdn_roofline(torch, lib(), rows=args.slots, state_dtype=state_code)
         log(f"GDN roofline {roof}")
@@ -468,6 +537,8 @@ def main():
     if not args.mixed_only:
         ring = ring_decode_rate(torch, rows=args.slots)
         log(f"ring decode {ring}")
+        tick = ring_tick_rate(torch, rows=args.slots)
+        log(f"tiled ring attention, mixed tick {tick}")
         chunk = chunk_prefill_rate(torch)
         log(f"chunk prefill config 4 {chunk}")
         lone = lone_row_rate(torch, lib())
@@ -679,6 +750,7 @@ def main():
                      "kernel": roof["kernel"], "shape": roof["shape"], "avg_us": roof["avg_us"],
                      "alg_bytes_per_launch": roof["alg_bytes_per_launch"]},
         "ring_decode_352": ring,
+        "ring_attn_tick": tick,
         "chunk_prefill_cfg4": chunk,
         "gdn_lone_row_64": lone,
         "prefill_352_contexts": prefill,
