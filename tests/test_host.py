@@ -188,3 +188,55 @@ def test_padded_rows_scatters_each_request():
     one = padded_rows(flat, lens[:1], offsets[:1], 64)
     assert np.array_equal(one[:, 0, :lens[0]], flat[:, offsets[0]:offsets[0] + lens[0]])
     assert not one[:, 0, lens[0]:].any()
+
+
+def test_native_host_packing_matches_numpy_route():
+    """hs_guard._hostpack (the packing step_packed runs) against the numpy route it replaces: pack_ticks with the
+    rows longest first (stable) and padded_rows, bit for bit, on random config-5-like ticks with ties, ids given
+    as lists, tuples and numpy integers; and scan's verdicts against the engine's request checks."""
+    import numpy as np
+
+    from hs_guard import _hostpack
+    from hs_guard.engine.slot_engine import pack_ticks, padded_rows
+
+    rng = np.random.default_rng(3)
+    max_slots = 40
+    for trial in range(30):
+        n = int(rng.integers(1, max_slots + 1))
+        slots = rng.permutation(max_slots)[:n]
+        lens = np.where(rng.random(n) < 0.7, 1, rng.integers(1, 65, n))
+        chunks = [list(map(int, rng.integers(0, 151936, int(l)))) for l in lens]
+        reqs = []
+        for i, (s, c) in enumerate(zip(slots, chunks)):
+            ids = c if i % 3 == 0 else tuple(c) if i % 3 == 1 else [np.int64(x) for x in c]
+            reqs.append((int(s) if i % 2 else np.int64(s), ids))
+        length = rng.integers(0, 9000, max_slots).astype(np.int64)
+        total = int(lens.sum())
+        assert _hostpack.scan(reqs, max_slots) == (n, total, int(lens.max()))
+        nb, tb = n + int(rng.integers(0, 5)), total + int(rng.integers(0, 40))
+        ref = np.full(2 * tb + 4 * nb, -7, dtype=np.int64)
+        order = np.argsort(-lens, kind="stable")
+        lens_p, offs_p = pack_ticks([chunks[r] for r in order], slots[order], length, nb, tb, max_slots, ref)
+        got = np.full(2 * tb + 4 * nb, -7, dtype=np.int64)
+        g_lens, g_offs, g_slots = (np.empty(n, dtype=np.int64) for _ in range(3))
+        _hostpack.fill(reqs, length, nb, tb, max_slots, got, g_lens, g_offs, g_slots)
+        np.testing.assert_array_equal(got, ref)
+        np.testing.assert_array_equal(g_lens, lens)
+        np.testing.assert_array_equal(g_slots, slots)
+        offs = np.empty(n, dtype=np.int64)
+        offs[order] = offs_p
+        np.testing.assert_array_equal(g_offs, offs)
+        flat = rng.standard_normal((2, tb, 3)).astype(np.float32)
+        for lb in (64, int(lens.max())):
+            want = padded_rows(flat[:, :total].copy(), lens, offs, lb)
+            out = np.full((2, n, lb, 3), np.nan, dtype=np.float32)
+            _hostpack.scatter_padded(flat, 2, tb, g_lens, g_offs, lb, out)
+            np.testing.assert_array_equal(out, want)
+    # requests the engine's checks reject (or that the native route leaves to the numpy route): scan says None
+    ok = [(0, [1, 2]), (3, [4])]
+    assert _hostpack.scan(ok, 4) == (2, 3, 2)
+    for bad in ([(0, [1]), (0, [2])], [(4, [1])], [(-1, [1])], [(1, [])], [(1.0, [2])], [(1, (x for x in [2]))]):
+        assert _hostpack.scan(bad, 4) is None, bad
+    with pytest.raises(ValueError):
+        _hostpack.scatter_padded(np.zeros((2, 4, 3), np.float32), 2, 4, np.array([3], np.int64),
+                                 np.array([2], np.int64), 4, np.zeros((2, 1, 4, 3), np.float32))
