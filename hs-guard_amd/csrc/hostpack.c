@@ -17,6 +17,9 @@
  *   scatter_padded(flat, R, T, lens, offsets, lb, out) -> None
  *       flat [R, T, 3] float32 (the tick's packed outputs), out [R, n, lb, 3] float32: request r's outputs at
  *       out[:, r, :lens[r]] and zeros after (padded_rows).
+ *   gather_rows(flat, R, T, lens, offsets, out) -> None
+ *       out [R, sum(lens), 3] float32: the requests' outputs one after another in request order
+ *       (request_order).
  *
  * Token ids and slots are read with the integer protocol (Python ints, numpy integers); ids may be any
  * sequence. Arrays are passed as writable / readable C-contiguous buffers of the stated item size.
@@ -266,10 +269,56 @@ done:
   return result;
 }
 
+static PyObject* gather_rows(PyObject* self, PyObject* args) {
+  PyObject *flat_o, *lens_o, *offs_o, *out_o;
+  Py_ssize_t R, T;
+  if (!PyArg_ParseTuple(args, "OnnOOO", &flat_o, &R, &T, &lens_o, &offs_o, &out_o)) return NULL;
+  Py_buffer flat_b, lens_b, offs_b, out_b;
+  if (get_buffer(lens_o, &lens_b, 8, 0, 0, "lens") != 0) return NULL;
+  const Py_ssize_t n = lens_b.len / 8;
+  const int64_t* lens = (const int64_t*)lens_b.buf;
+  PyObject* result = NULL;
+  int have = 1;
+  Py_ssize_t total = 0;
+  for (Py_ssize_t i = 0; i < n; ++i) total += lens[i];
+  if (get_buffer(offs_o, &offs_b, 8, n, 0, "offsets") != 0) goto done;
+  have = 2;
+  if (get_buffer(flat_o, &flat_b, 4, R * T * 3, 0, "flat") != 0) goto done;
+  have = 3;
+  if (get_buffer(out_o, &out_b, 4, R * total * 3, 1, "out") != 0) goto done;
+  have = 4;
+  {
+    const int64_t* offs = (const int64_t*)offs_b.buf;
+    const float* flat = (const float*)flat_b.buf;
+    float* out = (float*)out_b.buf;
+    for (Py_ssize_t i = 0; i < n; ++i)
+      if (lens[i] < 0 || offs[i] < 0 || offs[i] + lens[i] > T) {
+        PyErr_SetString(PyExc_ValueError, "gather_rows: a row lies outside the packed outputs");
+        goto done;
+      }
+    for (Py_ssize_t r = 0; r < R; ++r) {
+      float* dst = out + r * total * 3;
+      for (Py_ssize_t i = 0; i < n; ++i) {
+        memcpy(dst, flat + (r * T + offs[i]) * 3, (size_t)lens[i] * 3 * sizeof(float));
+        dst += lens[i] * 3;
+      }
+    }
+  }
+  Py_INCREF(Py_None);
+  result = Py_None;
+done:
+  if (have >= 4) PyBuffer_Release(&out_b);
+  if (have >= 3) PyBuffer_Release(&flat_b);
+  if (have >= 2) PyBuffer_Release(&offs_b);
+  PyBuffer_Release(&lens_b);
+  return result;
+}
+
 static PyMethodDef methods[] = {
     {"scan", scan, METH_VARARGS, "(n, total, max_len) of a tick's requests, or None if a check would fail"},
     {"fill", fill, METH_VARARGS, "pack a tick's requests into the packed layout (rows longest first)"},
     {"scatter_padded", scatter_padded, METH_VARARGS, "packed outputs [R, T, 3] -> padded [R, n, lb, 3]"},
+    {"gather_rows", gather_rows, METH_VARARGS, "packed outputs [R, T, 3] -> request order [R, sum(lens), 3]"},
     {NULL, NULL, 0, NULL}};
 
 static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_hostpack",

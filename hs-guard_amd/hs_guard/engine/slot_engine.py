@@ -544,6 +544,21 @@ class SlotStreamEngine(PreparedWeights):
         host_out.copy_(probs, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
 
+    def _run_native(self, requests, n, total):
+        """One tick of requests that passed _hostpack.scan (n rows, total tokens, within the tick limits), packed
+        by _hostpack.fill. Returns (outputs [R, tb, 3] numpy, valid until the next tick of the same shape, tb,
+        lens [n], offsets [n]) with request r's outputs at [:, offsets[r] : offsets[r] + lens[r]]."""
+        nb = bucket(n, self.session_buckets)
+        tb = bucket(total, self.token_buckets)
+        graph, inp, probs, host_in, host_np, host_out, out_np = self._static(nb, tb)
+        lens = np.empty(n, dtype=np.int64)
+        offsets = np.empty(n, dtype=np.int64)
+        slots = np.empty(n, dtype=np.int64)
+        _hostpack.fill(requests, self.length, nb, tb, self.max_slots, host_np, lens, offsets, slots)
+        self._replay(nb, tb, graph, inp, probs, host_in, host_out)
+        self.length[slots] += lens
+        return out_np, tb, lens, offsets
+
     @torch.inference_mode()
     def step_packed(self, requests):
         """One tick without per-row objects (src/hs_guard/engine/slot_engine_v7.py:138-145): requests as
@@ -557,15 +572,7 @@ class SlotStreamEngine(PreparedWeights):
             n, total, max_len = scan
             if n > self.max_rows or max_len > self.max_tick_tokens:
                 raise ValueError("step_packed takes one tick: too many rows or tokens")
-            nb = bucket(n, self.session_buckets)
-            tb = bucket(total, self.token_buckets)
-            graph, inp, probs, host_in, host_np, host_out, out_np = self._static(nb, tb)
-            lens = np.empty(n, dtype=np.int64)
-            offsets = np.empty(n, dtype=np.int64)
-            slots = np.empty(n, dtype=np.int64)
-            _hostpack.fill(requests, self.length, nb, tb, self.max_slots, host_np, lens, offsets, slots)
-            self._replay(nb, tb, graph, inp, probs, host_in, host_out)
-            self.length[slots] += lens
+            out_np, tb, lens, offsets = self._run_native(requests, n, total)
             lb = bucket(max_len, (1, 2, 4, 8, 16, 32, 64))
             out = np.empty((len(self.roles), n, lb, 3), dtype=np.float32)
             _hostpack.scatter_padded(out_np, len(self.roles), tb, lens, offsets, lb, out)
@@ -585,6 +592,16 @@ class SlotStreamEngine(PreparedWeights):
     def step(self, requests):
         """requests: list of (slot, token_ids), each slot at most once. Returns {role: [CPU tensor [L_i, 3]]}
         (src/hs_guard/engine/slot_engine_v7.py:147-167)."""
+        scan = _hostpack.scan(requests, self.max_slots)
+        if scan is not None and 0 < scan[0] <= self.max_rows and scan[2] <= self.max_tick_tokens:
+            # one tick (the serving case), host work native: the request-ordered outputs split per role
+            n, total, _ = scan
+            out_np, tb, lens, offsets = self._run_native(requests, n, total)
+            flat = np.empty((len(self.roles), total, 3), dtype=np.float32)
+            _hostpack.gather_rows(out_np, len(self.roles), tb, lens, offsets, flat)
+            probs = torch.from_numpy(flat)
+            sizes = lens.tolist()
+            return {role: list(torch.split(probs[r], sizes)) for r, role in enumerate(self.roles)}
         self._validate(requests)
         largest, rows = self.max_tick_tokens, self.max_rows
         if len(requests) <= rows and all(len(ids) <= largest for _, ids in requests):

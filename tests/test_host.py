@@ -191,13 +191,13 @@ def test_padded_rows_scatters_each_request():
 
 
 def test_native_host_packing_matches_numpy_route():
-    """hs_guard._hostpack (the packing step_packed runs) against the numpy route it replaces: pack_ticks with the
-    rows longest first (stable) and padded_rows, bit for bit, on random config-5-like ticks with ties, ids given
+    """hs_guard._hostpack (the packing step_packed and step run) against the numpy route it replaces: pack_ticks
+    with the rows longest first (stable), padded_rows and request_order, bit for bit, on random config-5-like ticks with ties, ids given
     as lists, tuples and numpy integers; and scan's verdicts against the engine's request checks."""
     import numpy as np
 
     from hs_guard import _hostpack
-    from hs_guard.engine.slot_engine import pack_ticks, padded_rows
+    from hs_guard.engine.slot_engine import pack_ticks, padded_rows, request_order
 
     rng = np.random.default_rng(3)
     max_slots = 40
@@ -232,6 +232,10 @@ def test_native_host_packing_matches_numpy_route():
             out = np.full((2, n, lb, 3), np.nan, dtype=np.float32)
             _hostpack.scatter_padded(flat, 2, tb, g_lens, g_offs, lb, out)
             np.testing.assert_array_equal(out, want)
+        want = request_order(flat, lens, offs)
+        got_o = np.full((2, total, 3), np.nan, dtype=np.float32)
+        _hostpack.gather_rows(flat, 2, tb, g_lens, g_offs, got_o)
+        np.testing.assert_array_equal(got_o, want)
     # requests the engine's checks reject (or that the native route leaves to the numpy route): scan says None
     ok = [(0, [1, 2]), (3, [4])]
     assert _hostpack.scan(ok, 4) == (2, 3, 2)
