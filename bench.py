@@ -316,6 +316,54 @@ def chunk_prefill_rate(torch, iters=10):
             "roof_tflops": round(ridge, 1), "roof_frac": round(tflops / ridge, 4)}
 
 
+def host_phases(torch, eng, load, steps=100):
+    """Where a step_packed tick's host-to-host time goes, on the engine's own calls in the order step_packed makes
+    them (requests checked and packed by hs_guard._hostpack, inputs copied, graph replayed, outputs copied, wait,
+    padded result): the median per phase in microseconds, and the graph's GPU time between HIP events on the
+    launch stream. Mixed config-5 ticks without resets; the engine's graphs are already captured."""
+    import numpy as np
+    from hs_guard import _hostpack
+    from hs_guard.engine.slot_engine import bucket
+    names = ("pack", "input_copy", "graph_launch_call", "output_copy", "wait", "result", "total")
+    ph = {k: [] for k in names}
+    gpu = []
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.inference_mode():
+        for i in range(steps):
+            req = load.step_requests()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            n, total, max_len = _hostpack.scan(req, eng.max_slots)
+            nb, tb = bucket(n, eng.session_buckets), bucket(total, eng.token_buckets)
+            graph, inp, probs, host_in, host_np, host_out, out_np = eng._static(nb, tb)
+            lens, offs, slots = (np.empty(n, dtype=np.int64) for _ in range(3))
+            _hostpack.fill(req, eng.length, nb, tb, eng.max_slots, host_np, lens, offs, slots)
+            t1 = time.perf_counter()
+            inp["all"].copy_(host_in, non_blocking=True)
+            t2 = time.perf_counter()
+            e0.record(st)
+            graph.replay()
+            e1.record(st)
+            t3 = time.perf_counter()
+            host_out.copy_(probs, non_blocking=True)
+            t4 = time.perf_counter()
+            st.synchronize()
+            t5 = time.perf_counter()
+            eng.length[slots] += lens
+            lb = bucket(max_len, (1, 2, 4, 8, 16, 32, 64))
+            out = np.empty((len(eng.roles), n, lb, 3), dtype=np.float32)
+            _hostpack.scatter_padded(out_np, len(eng.roles), tb, lens, offs, lb, out)
+            t6 = time.perf_counter()
+            for k, a, b in zip(names, (t0, t1, t2, t3, t4, t5, t0), (t1, t2, t3, t4, t5, t6, t6)):
+                ph[k].append((b - a) * 1e6)
+            gpu.append(e0.elapsed_time(e1) * 1e3)
+    out = {k: round(float(np.median(v)), 1) for k, v in ph.items()}
+    out["graph_gpu"] = round(float(np.median(gpu)), 1)
+    out["steps"] = steps
+    return out
+
+
 def v10_leg(torch, slots=352, steps=60, warmup=10, seed=0, state_dtype="float32"):
     """The config-5 mixed load on the released v10 geometry (8 q / 2 kv attention heads, vocab 248,320; 754.5M
     parameters, docs/evaluation.json:623) instead of the BASELINE geometry: random-init weights, contexts
@@ -639,12 +687,16 @@ def main():
                 "p50": round(percentile([t * 1e3 for t in api_t], 50), 3),
                 "p95": round(percentile([t * 1e3 for t in api_t], 95), 3)}
     log(f"step() leg {api_step}")
+    phases = host_phases(torch, eng, MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed + 3,
+                                                      reset_p=0.0))
+    log(f"host phases of a tick (us) {phases}")
     if args.mixed_only:
         print(json.dumps({"mixed_only": True, "value": round(value, 1), "unit": "tokens/s", "steps": args.steps,
                           "prefill_352_contexts": prefill,
                           "tokens": tokens, "ms_per_step": round(total / args.steps * 1e3, 4),
                           "latency_ms": {"p50": round(percentile(step_ms, 50), 3),
-                                         "p95": round(percentile(step_ms, 95), 3)}, "api_step": api_step}),
+                                         "p95": round(percentile(step_ms, 95), 3)}, "api_step": api_step,
+                          "host_phases_us": phases}),
               flush=True)
         return
 
@@ -740,6 +792,7 @@ def main():
                        "max": round(max(step_ms), 3)},
         "latency_by_context_ms": by_context,
         "api_step": api_step,
+        "host_phases_us": phases,
         "decode_352x1_ms": {"p50": round(percentile(dec, 50), 3), "p95": round(percentile(dec, 95), 3),
                             "tokens_per_s": round(args.slots / (np.mean(dec) / 1e3), 1)},
         "single_token_ms": {"p50": round(percentile(one, 50), 3), "p95": round(percentile(one, 95), 3)},
