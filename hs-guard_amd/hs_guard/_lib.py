@@ -96,6 +96,13 @@ SIGNATURES = {
                                      _P, _I64, _I64, _I32, _P, _F, _P, _I64, _I64,
                                      _P, _P, _I32, _I32, _I32, _P]),
     "hsg_silu_mul": (ctypes.c_int, [_P, _I64, _I32, _P, _I32, _P]),
+    "hsg_add_square": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _P]),
+    "hsg_rms_finish": (ctypes.c_int, [_P, _P, _P, _F, _P, _I64, _I32, _P]),
+    "hsg_silu_mul_pair": (ctypes.c_int, [_P, _P, _P, _I64, _P]),
+    "hsg_gated_finish": (ctypes.c_int, [_P, _P, _P, _P, _F, _P, _I64, _I32, _P]),
+    "hsg_square_rows": (ctypes.c_int, [_P, _P, _I64, _I32, _I64, _I64, _I32, _P]),
+    "hsg_norm_rope_grouped": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _F, _I32, _I32, _I32, _I32, _I64, _I64,
+                                             _I32, _P, _I64, _I64, _I64, _P]),
     "hsg_risk_head": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
     "hsg_risk_head_f32": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _F, _I32, _I32, _P, _I32, _P]),
     "hsg_ring_pos_update": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I32, _P]),

@@ -34,6 +34,120 @@ def _gpu(*tensors):
         _require(t is None or t.is_cuda, "HS-Guard kernels take GPU tensors")
 
 
+def _bf16_in(*tensors):
+    for t in tensors:
+        _require(t.dtype == torch.bfloat16, "bf16 tensors expected")
+        _require(t.is_contiguous(), "tensors must be contiguous")
+
+
+def add_square(residual, mixed=None):
+    """Replaces fused_kernels.py:44-52: (bf16(residual + mixed), its fp32 squares); with mixed None the squares of
+    residual, returned beside residual itself."""
+    _gpu(residual, mixed)
+    _bf16_in(residual, *(() if mixed is None else (mixed,)))
+    _require(mixed is None or mixed.shape == residual.shape, "residual and mixed must have one shape")
+    n = residual.shape[-1]
+    sq = torch.empty(residual.shape, dtype=torch.float32, device=residual.device)
+    out = residual if mixed is None else torch.empty_like(residual)
+    check(lib().hsg_add_square(_ptr(residual), _ptr(mixed), None if mixed is None else _ptr(out), _ptr(sq),
+                               residual.numel() // n, n, _stream(residual.device)), "hsg_add_square")
+    return out, sq
+
+
+def rms_finish(x, var, w1, eps):
+    """Replaces fused_kernels.py:67-72: Qwen3_5RMSNorm of x given var = mean(x.float()**2, -1, keepdim=True) and
+    w1 = 1 + weight.float()."""
+    _gpu(x, var, w1)
+    _bf16_in(x)
+    n = x.shape[-1]
+    rows = x.numel() // n
+    _require(var.dtype == torch.float32 and var.is_contiguous() and var.numel() == rows, "var must be [rows] fp32")
+    _require(w1.dtype == torch.float32 and w1.is_contiguous() and w1.numel() == n, "w1 must be [width] fp32")
+    out = torch.empty_like(x)
+    check(lib().hsg_rms_finish(_ptr(x), _ptr(var), _ptr(w1), float(eps), _ptr(out), rows, n,
+                               _stream(x.device)), "hsg_rms_finish")
+    return out
+
+
+def silu_mul(gate, up):
+    """Replaces fused_kernels.py:86-90: bf16(bf16(silu(gate)) * up) on two tensors of one shape."""
+    _gpu(gate, up)
+    _bf16_in(gate, up)
+    _require(gate.shape == up.shape, "gate and up must have one shape")
+    out = torch.empty_like(gate)
+    check(lib().hsg_silu_mul_pair(_ptr(gate), _ptr(up), _ptr(out), gate.numel(), _stream(gate.device)),
+          "hsg_silu_mul_pair")
+    return out
+
+
+def conv_silu_update(qkv, pool, weight, slots, lens):
+    """Replaces fused_kernels.py:126-136: qkv [N, L, C] bf16; pool [S, K-1, C] bf16 (one layer, updated in place at
+    rows slots[n] with lens[n] > 0); weight [C, 1, K] bf16. Returns silu(causal depthwise conv) [N, L, C] bf16
+    at every position of every row, as the reference computes it."""
+    n, length, c = qkv.shape
+    ks = weight.shape[-1]
+    _require(qkv.is_contiguous() and pool.is_contiguous() and weight.is_contiguous()
+             and pool.shape[1:] == (ks - 1, c), "conv_silu_update: contiguous qkv, pool [S, K-1, C], weight [C, 1, K]")
+    _gpu(qkv, pool, weight, slots, lens)
+    _bf16_in(qkv, pool, weight)
+    out = torch.empty_like(qkv)
+    check(lib().hsg_conv_silu_update(_ptr(qkv), c, _ptr(pool), pool.shape[0], _ptr(weight), ks, _ptr(slots),
+                                     _ptr(lens), None, n, length, c, _ptr(out), c, _stream(qkv.device)),
+          "hsg_conv_silu_update")
+    return out
+
+
+def gated_finish(x, var, weight, z, eps):
+    """Replaces fused_kernels.py:228-233: Qwen3_5RMSNormGated(x, z) over the last dim given
+    var = mean(x.float()**2, -1, keepdim=True); weight bf16 (the backbone's parameter)."""
+    _gpu(x, var, weight, z)
+    _bf16_in(x, weight, z)
+    n = x.shape[-1]
+    rows = x.numel() // n
+    _require(z.shape == x.shape and weight.numel() == n, "z must match x and weight its last dim")
+    _require(var.dtype == torch.float32 and var.is_contiguous() and var.numel() == rows, "var must be [rows] fp32")
+    out = torch.empty_like(x)
+    check(lib().hsg_gated_finish(_ptr(x), _ptr(var), _ptr(weight), _ptr(z), float(eps), _ptr(out), rows, n,
+                                 _stream(x.device)), "hsg_gated_finish")
+    return out
+
+
+def square_rows(src, tokens, heads, row_stride, head_stride, dim):
+    """Replaces fused_kernels.py:245-249: fp32 squares [tokens, heads, dim] of the head rows read at
+    src + t*row_stride + h*head_stride (elements)."""
+    _gpu(src)
+    _bf16_in(src)
+    _require(tokens == 0 or (tokens - 1) * row_stride + (heads - 1) * head_stride + dim <= src.numel(),
+             "rows reach past src")
+    sq = torch.empty(tokens, heads, dim, dtype=torch.float32, device=src.device)
+    check(lib().hsg_square_rows(_ptr(src), _ptr(sq), tokens, heads, row_stride, head_stride, dim,
+                                _stream(src.device)), "hsg_square_rows")
+    return sq
+
+
+def norm_rope(src, var, w1, cos, sin, eps, n, lb, heads, groups, row_stride, head_stride, dim):
+    """Replaces fused_kernels.py:277-284: Qwen3_5RMSNorm per head (given var [n*lb*heads] fp32) then
+    apply_rotary_pos_emb with cos/sin [n, lb, rot] bf16, written as [n, heads // groups, groups * lb, dim]: the
+    grouped query layout of the ring kernel (groups = 1 gives the key layout [n, Hkv, lb, dim])."""
+    _gpu(src, var, w1, cos, sin)
+    _require(src.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16,
+             "src, cos and sin must be bf16")
+    _require(cos.is_contiguous() and sin.is_contiguous() and cos.shape == sin.shape
+             and cos.numel() == n * lb * cos.shape[-1], "cos and sin must be contiguous [n, lb, rot]")
+    _require(var.dtype == torch.float32 and var.is_contiguous() and var.numel() == n * lb * heads,
+             "var must be [n*lb*heads] fp32")
+    _require(w1.dtype == torch.float32 and w1.is_contiguous() and w1.numel() == dim, "w1 must be [dim] fp32")
+    _require(src.is_contiguous() and (n * lb == 0 or (n * lb - 1) * row_stride + (heads - 1) * head_stride + dim
+                                      <= src.numel()), "src must be contiguous and hold every head row")
+    _require(heads % groups == 0, "heads must be a multiple of groups")
+    rot = cos.shape[-1]
+    out = torch.empty(n, heads // groups, groups * lb, dim, dtype=torch.bfloat16, device=src.device)
+    check(lib().hsg_norm_rope_grouped(_ptr(src), _ptr(var), _ptr(w1), _ptr(cos), _ptr(sin), rot, float(eps), n, lb,
+                                      heads, groups, row_stride, head_stride, dim, _ptr(out), out.stride(0),
+                                      out.stride(1), out.stride(2), _stream(src.device)), "hsg_norm_rope_grouped")
+    return out
+
+
 def gdn_slot_v8(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log, dt_bias, state, slots, lens,
                 bv=32, num_warps=2):
     """Replaces fused_kernels.py:197-211. packed [N, L, 2*key_dim + value_dim] (conv_silu_update output);

@@ -276,6 +276,65 @@ int hsg_norm_rope(const void* q_src, int64_t q_row, int64_t q_head, int32_t q_he
                   int32_t tokens, int32_t head_dim, void* stream);
 
 /*
+ * Unfused entry points with the reference engine's own kernel contracts (the variance of each RMSNorm and the
+ * rotary cos/sin are inputs, as src/hs_guard/engine/slot_engine_v8.py:42-55,74-82 computes them), so that a caller
+ * composing the step as SlotStreamEngineV8 does can swap its imports (slot_engine_v8.py:6-7). Rows may have any
+ * width; contiguous row-major tensors, bf16 unless stated. The streaming engine of this library runs the fused
+ * forms above (hsg_add_rmsnorm, hsg_norm_rope, hsg_silu_mul, the slot step's gated epilogue) instead.
+ */
+
+/*
+ * Replaces add_square (src/hs_guard/engine/fused_kernels.py:44-52; kernel :30-41), over rows x width elements:
+ *   mixed non-NULL: out = bf16(residual + mixed) (one fp32 add), sq = out^2 (fp32);
+ *   mixed NULL:     sq = residual^2 (out is not written).
+ */
+int hsg_add_square(const void* residual, const void* mixed, void* out, float* sq, int64_t rows, int32_t width,
+                   void* stream);
+
+/*
+ * Replaces rms_finish (src/hs_guard/engine/fused_kernels.py:67-72; kernel :56-64):
+ *   out[r, c] = bf16((x[r, c] * rsqrt(var[r] + eps)) * w1[c]);  var [rows] fp32 (the mean of x^2 over the row),
+ *   w1 [width] fp32 (= 1 + weight).
+ */
+int hsg_rms_finish(const void* x, const float* var, const float* w1, float eps, void* out, int64_t rows,
+                   int32_t width, void* stream);
+
+/*
+ * Replaces silu_mul (src/hs_guard/engine/fused_kernels.py:86-90; kernel :76-83) on two separate tensors of n
+ * elements: out = bf16(bf16(silu(gate)) * up).
+ */
+int hsg_silu_mul_pair(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/*
+ * Replaces gated_finish (src/hs_guard/engine/fused_kernels.py:228-233; kernel :215-225):
+ *   out[r, c] = bf16(bf16(weight[c] * bf16(x[r, c] * rsqrt(var[r] + eps))) * silu(z[r, c]));
+ *   var [rows] fp32, weight [width] bf16.
+ */
+int hsg_gated_finish(const void* x, const float* var, const void* weight, const void* z, float eps, void* out,
+                     int64_t rows, int32_t width, void* stream);
+
+/*
+ * Replaces square_rows (src/hs_guard/engine/fused_kernels.py:245-249; kernel :237-242):
+ *   sq[t*heads + h, c] = src[t*row_stride + h*head_stride + c]^2 (fp32), sq [tokens*heads, dim].
+ */
+int hsg_square_rows(const void* src, float* sq, int64_t tokens, int32_t heads, int64_t row_stride,
+                    int64_t head_stride, int32_t dim, void* stream);
+
+/*
+ * Replaces norm_rope (src/hs_guard/engine/fused_kernels.py:277-284; kernel :252-274): per-head RMSNorm(1 + w) given
+ * var, then rotate-half RoPE on the first `rot` dims with the given cos/sin [n_rows*lb, rot] bf16:
+ *   x = bf16((src * rsqrt(var + eps)) * w1), out = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)) (d < rot),
+ *   bf16(x) beyond. Head j of token t = n*lb + l is read at src + t*row_stride + j*head_stride, its variance at
+ *   var[t*heads + j], and written at out + n*out_n + (j / groups)*out_h + ((j % groups)*lb + l)*out_row: the
+ *   grouped [N, heads/groups, groups*lb, dim] query layout of hsg_ring_attention (groups 1: [N, heads, lb, dim]).
+ *   w1 [dim] fp32. Supported: heads % groups == 0, rot even and <= dim.
+ */
+int hsg_norm_rope_grouped(const void* src, const float* var, const float* w1, const void* cos, const void* sin,
+                          int32_t rot, float eps, int32_t n_rows, int32_t lb, int32_t heads, int32_t groups,
+                          int64_t row_stride, int64_t head_stride, int32_t dim, void* out, int64_t out_n,
+                          int64_t out_h, int64_t out_row, void* stream);
+
+/*
  * SiLU-mul of the fused gate|up projection. Replaces silu_mul (src/hs_guard/engine/fused_kernels.py:86-90):
  *   out[t, c] = bf16(bf16(silu(gu[t, c])) * gu[t, width + c]), out [tokens, width] bf16.
  * Supported: width and row_stride multiples of 8, pointers 16-byte aligned.

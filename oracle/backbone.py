@@ -30,13 +30,19 @@ ROLES = ("user", "assistant")
 
 
 class StreamOracle:
-    def __init__(self, weights, cfg, max_slots, roles=ROLES, gdn="recurrent"):
+    def __init__(self, weights, cfg, max_slots, roles=ROLES, gdn="recurrent", state_dtype="float64"):
         """weights: name -> float32 numpy array of the bf16 weights (reference parameter names). gdn: "recurrent"
         (``gdn_slot_step``, token by token) or "chunk" (``gdn_slot_step_chunked`` for ticks of more than one
-        step: the same float64 recurrence in the chunk form, for full-geometry ticks of long rows)."""
+        step: the same float64 recurrence in the chunk form, for full-geometry ticks of long rows).
+        state_dtype "float16": the recurrent state is stored in fp16 between ticks, as the reference's
+        StreamingGuard keeps it (runtime.py:157, ``state_dtype='float16'``): each tick runs from the stored
+        fp16 values in float64 and rounds the pool to fp16 when it stores it back."""
         if gdn not in ("recurrent", "chunk"):
             raise ValueError("gdn must be 'recurrent' or 'chunk'")
+        if state_dtype not in ("float64", "float16"):
+            raise ValueError("state_dtype must be 'float64' or 'float16'")
         self.gdn = gdn
+        self.state_dtype = state_dtype
         self.w = weights
         self._fused = {}
         self.cfg = cfg
@@ -60,7 +66,7 @@ class StreamOracle:
     def reset(self, slots=None):
         """Zero every slot (the reference's reset, bucketed_engine.py:51-55) or only ``slots``."""
         if slots is None:
-            self.__init__(self.w, self.cfg, self.max_slots, self.roles, self.gdn)
+            self.__init__(self.w, self.cfg, self.max_slots, self.roles, self.gdn, self.state_dtype)
             return
         idx = np.asarray(list(slots), dtype=np.int64)
         self.rec[:, idx] = 0
@@ -112,6 +118,8 @@ class StreamOracle:
                 step = ogdn.gdn_slot_step_chunked if self.gdn == "chunk" and lb > 1 else ogdn.gdn_slot_step
                 o, _, self.rec[idx] = step(conv_out, cfg.key_dim, H, K, HV, V, aa, bb, w[a + "A_log"],
                                            w[a + "dt_bias"], self.rec[idx], slots, lens)
+                if self.state_dtype == "float16":
+                    self.rec[idx] = self.rec[idx].astype(np.float16).astype(np.float64)
                 gated = oglue.gated_rmsnorm(bf16(o), z.reshape(n, lb, HV, V), w[a + "norm.weight"], eps)
                 mix = gemm(gated.reshape(n, lb, HV * V), w[a + "out_proj.weight"], None, lens)
             else:

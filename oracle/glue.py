@@ -5,6 +5,9 @@ Rounding points follow the reference's fused kernels (bf16 where they store bf16
 * ``conv_silu_update``  -- fused_kernels.py:94-136: causal depthwise conv (4 taps) over [pool(3 rows); new
   tokens], fp32 accumulate, round to bf16, SiLU, round to bf16; pool row i <- ext[len + i] when len > 0.
   Pinned against transformers' ``causal_conv1d_update`` (qwen3_5/modeling_qwen3_5.py:200-216).
+* ``rms_finish``, ``gated_finish``, ``norm_rope_given`` -- the same formulas with the row variance as an
+  input, as the reference's kernels take it; ``rmsnorm``, ``gated_rmsnorm`` and ``norm_rope`` are these with
+  the variance computed, so the pins below hold for both forms.
 * ``add_rmsnorm``       -- add_square + rms_finish (fused_kernels.py:30-72, slot_engine_v8.py:42-55):
   h = bf16(res + mix); out = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w)). Pinned against transformers'
   ``Qwen3_5RMSNorm`` (modeling_qwen3_5.py:720-737 of that file's class).
@@ -60,11 +63,17 @@ def conv_silu_update(qkv, pool, weight, slots, lens):
     return out, pool2
 
 
+def rms_finish(x, var, w1, eps):
+    """rms_finish (fused_kernels.py:56-72): bf16((x * rsqrt(var + eps)) * w1) with the row variance given
+    (var [..., 1], the caller's mean of x^2), w1 = 1 + weight (fp32)."""
+    x = np.asarray(x, dtype=np.float64)
+    return bf16((x / np.sqrt(np.asarray(var, dtype=np.float64) + eps)) * np.asarray(w1, dtype=np.float64))
+
+
 def rmsnorm(h, w1, eps):
     """bf16((h * rsqrt(mean(h^2) + eps)) * w1) with h already bf16 values, w1 = 1 + weight (fp32)."""
     h = np.asarray(h, dtype=np.float64)
-    var = (h * h).mean(-1, keepdims=True)
-    return bf16((h / np.sqrt(var + eps)) * np.asarray(w1, dtype=np.float64))
+    return rms_finish(h, (h * h).mean(-1, keepdims=True), w1, eps)
 
 
 def add_rmsnorm(res, mix, w1, eps):
@@ -73,13 +82,19 @@ def add_rmsnorm(res, mix, w1, eps):
     return h, rmsnorm(h, w1, eps)
 
 
+def gated_finish(x, var, w, z, eps):
+    """gated_finish (fused_kernels.py:215-233) with the row variance given (var [..., 1]):
+    bf16(bf16(w * bf16(x * rsqrt(var + eps))) * silu(z))."""
+    x = np.asarray(x, dtype=np.float64)
+    hb = bf16(x / np.sqrt(np.asarray(var, dtype=np.float64) + eps))
+    t = bf16(np.asarray(w, dtype=np.float64) * hb)
+    return bf16(t * silu(z))
+
+
 def gated_rmsnorm(x, z, w, eps):
     """x, z [..., V] (x bf16 values), w [V] -> bf16 values."""
     x = np.asarray(x, dtype=np.float64)
-    var = (x * x).mean(-1, keepdims=True)
-    hb = bf16(x / np.sqrt(var + eps))
-    t = bf16(np.asarray(w, dtype=np.float64) * hb)
-    return bf16(t * silu(z))
+    return gated_finish(x, (x * x).mean(-1, keepdims=True), w, z, eps)
 
 
 def silu_mul(g, u):
@@ -101,8 +116,13 @@ def rope_cos_sin(pos, inv):
 def norm_rope(x, w1, eps, cos, sin):
     """x [..., heads, D] bf16 values; cos, sin [..., rot] (broadcast over heads) -> bf16 values."""
     x = np.asarray(x, dtype=np.float64)
-    var = (x * x).mean(-1, keepdims=True)
-    y = bf16((x / np.sqrt(var + eps)) * np.asarray(w1, dtype=np.float64)).astype(np.float64)
+    return norm_rope_given(x, (x * x).mean(-1, keepdims=True), w1, eps, cos, sin)
+
+
+def norm_rope_given(x, var, w1, eps, cos, sin):
+    """norm_rope (fused_kernels.py:252-284) with the per-head variance given (var [..., heads, 1])."""
+    x = np.asarray(x, dtype=np.float64)
+    y = bf16((x / np.sqrt(np.asarray(var, dtype=np.float64) + eps)) * np.asarray(w1, dtype=np.float64)).astype(np.float64)
     rot = cos.shape[-1]
     half = rot // 2
     c = np.asarray(cos, dtype=np.float64)[..., None, :]

@@ -11,6 +11,25 @@ import numpy as np
 import torch
 
 
+def bf16_ulp(x):
+    """The spacing of bf16 values at |x| (8 significant bits)."""
+    a = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+def close_bf16(got, ref, what, frac=5e-3, atol=1e-30, ulps=None):
+    """bf16 outputs against the oracle. Default bar: 2^-8 relative. With ``ulps``: that many bf16 ulps of the
+    reference value (one ulp is 2^-8 to 2^-7 relative, so a single rounding flip at the bottom of a binade passes
+    only this form). At most ``frac`` of the values may differ at all."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    diff = np.abs(got - ref)
+    tol = 2.0 ** -8 * np.abs(ref) if ulps is None else ulps * bf16_ulp(ref)
+    bad = diff > tol + atol
+    assert not bad.any(), f"{what}: {int(bad.sum())} values beyond the bar (max {diff.max():.3e})"
+    assert np.mean(diff > 0) <= frac, f"{what}: {np.mean(diff > 0):.3%} of values differ"
+
+
 def matched_gemm(eng):
     from hs_guard.engine.slot_engine import bucket, gdn_proj_width
     cache = {}

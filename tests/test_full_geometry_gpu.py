@@ -92,3 +92,51 @@ def test_baseline_geometry_matches_oracle(full):
     for k, (a, b) in stats.items():
         assert a <= FLOOR_FACTOR * b, f"{k}: engine {a:.2e} > {FLOOR_FACTOR} x floor {b:.2e}"
     assert max(rel) <= FLOOR_FACTOR * max(rel_twin)
+
+
+def test_benchmark_depth_at_north_star_bar():
+    """The 2e-3 bar itself at the benchmark depth: GuardConfig.baseline() (24 layers) with random-init weights
+    N(0, 0.0025), where the oracle's fp32-level noise floor is below 1e-3 (measured here on the same inputs, and on
+    the CPU by tests/test_oracle_backbone.py::test_noise_floor_scales_with_weights). Four slots receive contexts of
+    520-553 tokens in 64-token ticks (every ring wraps), then four single-token ticks and a mixed tick; every
+    per-token |d(1 - p(safe))| against the oracle with matched GEMMs must be within 2e-3. The recurrent state, whose
+    inputs carry the ~1% bf16 noise of the hidden state at this depth (the perturbed oracle's own state moves by
+    ~1e-2), is held to 1.5x the perturbed oracle's deviation."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    from oracle.backbone import StreamOracle
+    from oracle.bf16 import perturbed
+    print("[full] benchmark depth, N(0, 0.0025), 2e-3 bar", flush=True)
+    cfg = GuardConfig.baseline()
+    model_cpu = GuardModel.random(cfg, seed=0, device="cpu", std=0.0025)
+    weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
+    slots = 4
+    eng = SlotStreamEngine(model_cpu.to("cuda:0"), slots, use_graphs=False)
+    del model_cpu
+    orc = StreamOracle(weights, cfg, slots, gdn="chunk")
+    twin = StreamOracle(weights, cfg, slots, gdn="chunk")
+    gemm = matched_gemm(eng)
+    worst = floor = 0.0
+    for t, tick in enumerate(_ticks(np.random.default_rng(1), cfg.vocab_size, slots)):
+        got = eng.step(tick)
+        ref = orc.step(tick, gemm=gemm)
+        with perturbed(1):
+            alt = twin.step(tick, gemm=gemm)
+        d = _cut_diffs({r: [x.numpy() for x in v] for r, v in got.items()}, ref).max()
+        f = _cut_diffs(alt, ref).max()
+        worst, floor = max(worst, d), max(floor, f)
+        print(f"[full] tick {t}: {len(tick)} rows, {sum(len(i) for _, i in tick)} tokens, max |d cut| engine "
+              f"{d:.2e}, perturbed oracle {f:.2e}", flush=True)
+        assert d <= 2e-3, f"tick {t}: cut-score diff {d:.2e}"
+    W = cfg.window_tokens
+    np.testing.assert_array_equal(eng.length, orc.length)
+    np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
+    assert (orc.ring_pos[:slots, :W] >= 0).all() and (orc.length > W).all()
+    assert floor < 1e-3, f"noise floor {floor:.2e}: the bar would not be meaningful on these inputs"
+    rec = eng.rec.double().cpu().numpy()
+    rel = max(np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s]) for s in range(slots))
+    rel_twin = max(np.linalg.norm(twin.rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
+                   for s in range(slots))
+    print(f"[full] worst |d cut| {worst:.2e} (floor {floor:.2e}); state rel err {rel:.1e} (perturbed oracle "
+          f"{rel_twin:.1e})", flush=True)
+    assert rel <= FLOOR_FACTOR * rel_twin

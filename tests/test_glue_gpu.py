@@ -12,6 +12,7 @@ import torch
 from oracle import glue as oglue
 from oracle import pack as opack
 from oracle.bf16 import bf16
+from parity_helpers import close_bf16 as _close
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -23,24 +24,6 @@ def _np(t):
 
 def _bf(x):
     return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16)
-
-
-def _bf16_ulp(x):
-    """The spacing of bf16 values at |x| (8 significant bits)."""
-    a = np.maximum(np.abs(np.asarray(x, dtype=np.float64)), 2.0 ** -126)
-    return 2.0 ** (np.floor(np.log2(a)) - 7)
-
-
-def _close(got, ref, what, frac=5e-3, atol=1e-30, ulps=None):
-    """Default bar: 2^-8 relative. With ``ulps``: that many bf16 ulps of the reference value (one ulp is
-    2^-8 to 2^-7 relative, so a single rounding flip at the bottom of a binade passes only this form)."""
-    got = np.asarray(got, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
-    diff = np.abs(got - ref)
-    tol = 2.0 ** -8 * np.abs(ref) if ulps is None else ulps * _bf16_ulp(ref)
-    bad = diff > tol + atol
-    assert not bad.any(), f"{what}: {int(bad.sum())} values beyond one bf16 ulp (max {diff.max():.3e})"
-    assert np.mean(diff > 0) <= frac, f"{what}: {np.mean(diff > 0):.3%} of values differ"
 
 
 def _stream():
