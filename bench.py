@@ -334,11 +334,11 @@ def host_phases(torch, eng, load, steps=100):
             req = load.step_requests()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            n, total, max_len = _hostpack.scan(req, eng.max_slots)
+            n, total, max_len = _hostpack.scan(req, eng.max_slots, eng.cfg.vocab_size)
             nb, tb = bucket(n, eng.session_buckets), bucket(total, eng.token_buckets)
             graph, inp, probs, host_in, host_np, host_out, out_np = eng._static(nb, tb)
             lens, offs, slots = (np.empty(n, dtype=np.int64) for _ in range(3))
-            _hostpack.fill(req, eng.length, nb, tb, eng.max_slots, host_np, lens, offs, slots)
+            _hostpack.fill(req, eng.length, nb, tb, eng.max_slots, eng.cfg.vocab_size, host_np, lens, offs, slots)
             t1 = time.perf_counter()
             inp["all"].copy_(host_in, non_blocking=True)
             t2 = time.perf_counter()

@@ -125,7 +125,12 @@ int get_plan(DeviceCtx& c, int32_t M, int32_t N, int32_t K, int64_t lda, int64_t
     std::vector<hipblasLtMatmulHeuristicResult_t> res;
     const float alpha = 1.f, beta = 0.f;
     size_t ws = 0;
-    if (hipblaslt_ext::getAlgosFromIndex(c.handle, idx, res) != HIPBLAS_STATUS_SUCCESS || res.empty() ||
+    // The library's C++ extension calls are bound from the hipBLASLt the process loaded (torch's bundled one, which
+    // the plan table was generated with), not necessarily the release whose headers this file was compiled with;
+    // their mangled signatures are the same in both. The round trip index -> algo -> index checks that the result
+    // records were laid out as this build expects before one is used.
+    if (hipblaslt_ext::getAlgosFromIndex(c.handle, idx, res) != HIPBLAS_STATUS_SUCCESS || res.size() != 1 ||
+        hipblaslt_ext::getIndexFromAlgo(res[0].algo) != index ||
         hipblaslt_ext::matmulIsAlgoSupported(c.handle, p.desc, &alpha, p.lw, p.la, &beta, p.ld, p.ld, res[0].algo,
                                              ws) != HIPBLAS_STATUS_SUCCESS) {
       destroy_plan(p);

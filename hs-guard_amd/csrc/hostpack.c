@@ -7,10 +7,12 @@
  * as the numpy route in hs_guard/engine/slot_engine.py (pack_ticks, padded_rows), which stays the reference
  * for the tests:
  *
- *   scan(requests, max_slots) -> (n, total, max_len), or None when a request would fail the tick's checks
- *       (a slot outside [0, max_slots), a slot twice, an empty request); the caller then runs its own checks,
- *       which raise the reference's errors (src/hs_guard/runtime.py:148-174).
- *   fill(requests, length, nb, tb, max_slots, out, lens, offsets, slots) -> None
+ *   scan(requests, max_slots, vocab) -> (n, total, max_len), or None when a request would fail the tick's checks
+ *       (a slot outside [0, max_slots), a slot twice, an empty request, a token id that is not an integer in
+ *       [0, vocab)); the caller then runs its own checks, which raise the reference's errors
+ *       (src/hs_guard/runtime.py:148-174; docs/ENGINE.md:9 requires in-vocabulary ids).
+ *   fill(requests, length, nb, tb, max_slots, vocab, out, lens, offsets, slots) -> None (ValueError for an id
+ *       outside [0, vocab))
  *       out [2 tb + 4 nb] int64: ids | positions | offsets | lens | slots | starts of the packed tick with the
  *       rows longest first (stable), padding rows on the scratch slot max_slots (pack_ticks' layout);
  *       lens / offsets / slots [n] int64 in request order (offsets = where each request's tokens sit).
@@ -63,10 +65,37 @@ static int request_at(PyObject* seq, Py_ssize_t i, long long* slot, PyObject** i
   return 0;
 }
 
+/* every id of a request an integer in [0, vocab) (numpy integers included); 0 otherwise, with no error set */
+static int ids_in_vocab(PyObject* ids, long long vocab) {
+  PyObject* fast = PySequence_Fast(ids, "token ids must be a sequence");
+  if (!fast) {
+    PyErr_Clear();
+    return 0;
+  }
+  const Py_ssize_t len = PySequence_Fast_GET_SIZE(fast);
+  PyObject** items = PySequence_Fast_ITEMS(fast);
+  int ok = 1;
+  for (Py_ssize_t t = 0; t < len && ok; ++t) {
+    if (PyFloat_Check(items[t])) {   /* integers only (bool is an int, as the reference's isinstance check has it) */
+      ok = 0;
+      break;
+    }
+    const long long v = PyLong_AsLongLong(items[t]);
+    if (v == -1 && PyErr_Occurred()) {
+      PyErr_Clear();
+      ok = 0;
+    } else if (v < 0 || v >= vocab) {
+      ok = 0;
+    }
+  }
+  Py_DECREF(fast);
+  return ok;
+}
+
 static PyObject* scan(PyObject* self, PyObject* args) {
   PyObject *requests, *seq;
-  long long max_slots;
-  if (!PyArg_ParseTuple(args, "OL", &requests, &max_slots)) return NULL;
+  long long max_slots, vocab;
+  if (!PyArg_ParseTuple(args, "OLL", &requests, &max_slots, &vocab)) return NULL;
   seq = PySequence_Fast(requests, "requests must be a sequence");
   if (!seq) return NULL;
   const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
@@ -95,7 +124,8 @@ static PyObject* scan(PyObject* self, PyObject* args) {
       ok = 0;
       break;
     }
-    if (slot < 0 || slot >= max_slots || seen[slot] || len == 0) {
+    if (slot < 0 || slot >= max_slots || seen[slot] || len == 0 ||
+        !ids_in_vocab(PySequence_Fast_GET_ITEM(item, 1), vocab)) {
       ok = 0;
       break;
     }
@@ -111,9 +141,9 @@ static PyObject* scan(PyObject* self, PyObject* args) {
 
 static PyObject* fill(PyObject* self, PyObject* args) {
   PyObject *requests, *length_o, *out_o, *lens_o, *offs_o, *slots_o;
-  long long nb, tb, max_slots;
-  if (!PyArg_ParseTuple(args, "OOLLLOOOO", &requests, &length_o, &nb, &tb, &max_slots, &out_o, &lens_o, &offs_o,
-                        &slots_o))
+  long long nb, tb, max_slots, vocab;
+  if (!PyArg_ParseTuple(args, "OOLLLLOOOO", &requests, &length_o, &nb, &tb, &max_slots, &vocab, &out_o, &lens_o,
+                        &offs_o, &slots_o))
     return NULL;
   PyObject* seq = PySequence_Fast(requests, "requests must be a sequence");
   if (!seq) return NULL;
@@ -192,6 +222,10 @@ static PyObject* fill(PyObject* self, PyObject* args) {
       for (int64_t t = 0; t < lens[i]; ++t) {
         const long long v = PyLong_AsLongLong(items[t]);
         if (v == -1 && PyErr_Occurred()) goto done;
+        if (v < 0 || v >= vocab) {
+          PyErr_SetString(PyExc_ValueError, "Each request requires nonempty in-vocabulary integer token IDs");
+          goto done;
+        }
         id_out[off + t] = v;
         pos[off + t] = st + t;
       }

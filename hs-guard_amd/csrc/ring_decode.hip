@@ -401,15 +401,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecParams p) 
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Fused decode (groups <= 8): one workgroup of 8 waves per (row, kv head), wave w owning ring blocks w and w + 8,
-// so every score, block maximum and partial sum stays in LDS and the whole step is one launch. The numerics are
-// those of the three split-K kernels above (same block maxima, prefix maxima, bf16 probabilities and block
-// weights); only the fp32 summation order of the partial P.V sums differs (keys in order within a block, the
-// wave's two blocks in order, then a fixed tree over the waves). Memory: round trip 1 issues the blocks'
-// positions, the queries (into LDS) and the step's own key and value; then each visible block's keys, one block
-// at a time; the first block's values go out as soon as the scores are done and are in flight across the
-// block-maximum barrier, the second block's after the first block's P.V. At about 90 VGPRs two or more of these
-// workgroups share a CU, so one workgroup's loads cover the other's barriers and arithmetic.
+// Fused decode (groups <= 8): one workgroup of 4 waves per (row, kv head), wave w owning ring blocks w, w + 4,
+// w + 8 and w + 12 (32 keys each), so every score, block maximum and partial sum stays in LDS and the whole step is
+// one launch. The numerics are those of the three split-K kernels above (same block maxima, prefix maxima, bf16
+// probabilities and block weights); only the fp32 summation order of the partial P.V sums differs (keys in order
+// within a block, the wave's blocks in order, then a fixed tree over the waves). Memory: round trip 1 issues the
+// blocks' positions, the queries (into LDS) and the step's own key and value; then each visible block's keys, one
+// block at a time; the first block's values go out as soon as the scores are done and are in flight across the
+// block-maximum barrier, each later block's after the previous block's P.V. Several of these workgroups share a
+// CU, so one workgroup's loads cover another's barriers and arithmetic.
 template <int GT>
 __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
   constexpr int NWV = 4;                       // waves
@@ -740,11 +740,13 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   using namespace hsg;
   if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
+  // the workspace is the split-K path's (groups > 8); the fused kernel below that neither needs nor reads it
+  const bool split = groups > 8;
   if (!q || !ring_k || !ring_v || !new_k || !new_v || !ring_pos || !slots || !starts || !lens || !out ||
-      !workspace)
+      (split && !workspace))
     return HSG_ERR_ARG;
   if (head_dim != D || window <= 0 || window > W_MAX || window % KB != 0 || groups > G_MAX) return HSG_ERR_SHAPE;
-  if (workspace_bytes < hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window)) return HSG_ERR_SHAPE;
+  if (split && workspace_bytes < hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window)) return HSG_ERR_SHAPE;
   const int64_t s16[] = {q_sn, q_sl, q_sh, q_sg};
   for (int64_t s : s16)
     if (s % 8) return HSG_ERR_ALIGN;
@@ -752,7 +754,7 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   for (int64_t s : s4)
     if (s % 4) return HSG_ERR_ALIGN;
   if (!aligned(q, 16) || !aligned(ring_k, 16) || !aligned(ring_v, 16) || !aligned(new_k, 8) ||
-      !aligned(new_v, 8) || !aligned(out, 8) || (gate && !aligned(gate, 8)) || !aligned(workspace, 16))
+      !aligned(new_v, 8) || !aligned(out, 8) || (gate && !aligned(gate, 8)) || (split && !aligned(workspace, 16)))
     return HSG_ERR_ALIGN;
   DecParams p{};
   p.q = static_cast<const uint16_t*>(q); p.q_sn = q_sn; p.q_sl = q_sl; p.q_sh = q_sh; p.q_sg = q_sg;
@@ -770,7 +772,7 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   p.sc_stride = window + KB;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned units = (unsigned)(n_rows * hkv);
-  if (groups <= 8) {
+  if (!split) {
     if (groups <= 4) hipLaunchKernelGGL(decode_fused_kernel<4>, dim3(units), dim3(256), 0, st, p);
     else hipLaunchKernelGGL(decode_fused_kernel<8>, dim3(units), dim3(256), 0, st, p);
     return launch_status();
@@ -826,7 +828,9 @@ extern "C" int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl
                                        int64_t o_sg, void* stream) {
   if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
-  if (hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) > (size_t)HSG_RING_DECODE_SCRATCH_BYTES)
+  // only the split-K path (groups > 8) uses the workspace, so only it is bounded by the scratch
+  if (groups > 8 &&
+      hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) > (size_t)HSG_RING_DECODE_SCRATCH_BYTES)
     return HSG_ERR_SHAPE;
   void* ws = nullptr;
   const int rc = current_scratch(&ws);

@@ -8,7 +8,16 @@ from __future__ import annotations
 import ctypes
 import os
 
+# torch first: libhsg.so needs libamdhip64.so.7 and libhipblaslt.so.1, and torch's wheel bundles its own copies under
+# those sonames. Whichever copy a process loads first serves every later user of the soname, so loading libhsg.so
+# before torch would bind /opt/rocm's hipBLASLt and move torch.mm onto it as well. With torch loaded first the
+# process runs torch's bundled HIP runtime and hipBLASLt, the ones the committed GEMM plan table was made with.
+import torch  # noqa: F401,E402
+
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhsg.so")
+
+# return codes of include/hsg.h
+HSG_OK, HSG_ERR_ARG, HSG_ERR_ALIGN, HSG_ERR_SHAPE, HSG_ERR_BLAS = 0, -1, -2, -3, -4
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -50,6 +50,11 @@ class GemmPlans:
     def index(self, M, N, K):
         return self.table.get((int(M), int(N), int(K)), -1)
 
+    def drop(self, M, N, K):
+        """Forget the entry of (M, N, K): the running hipBLASLt rejected its solution (hsg_gemm_bf16 returned
+        HSG_ERR_SHAPE), so the product falls back to the heuristic's first candidate from now on."""
+        return self.table.pop((int(M), int(N), int(K)), None)
+
 
 def engine_shapes(cfg):
     """(N, K) of the engine's bias-free projections for a GuardConfig: GDN in (padded) and out, attention in and

@@ -249,7 +249,9 @@ def ring_attention_v8(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, st
     _gpu(q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens)
     out = torch.empty(n, lb, hkv * groups * d, dtype=torch.bfloat16, device=q.device)
     if lb == 1 and split_k:
-        ws_bytes = lib().hsg_ring_decode_workspace_bytes(n, hkv, groups, window)
+        # the split-K kernels (more than 8 query heads per kv head) keep their partial results in a workspace; the
+        # fused kernel below that needs none
+        ws_bytes = lib().hsg_ring_decode_workspace_bytes(n, hkv, groups, window) if groups > 8 else 0
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
         rc = lib().hsg_ring_decode(
             _ptr(q), hkv * m * d, d, m * d, d,

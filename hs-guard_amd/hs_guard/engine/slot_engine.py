@@ -19,12 +19,13 @@ Differences by design (the device program is the MI355X one, not a translation):
 from __future__ import annotations
 
 import itertools
+import warnings
 
 import numpy as np
 import torch
 
 from .. import _hostpack
-from .._lib import check, lib
+from .._lib import HSG_ERR_SHAPE, check, lib
 from ..model import ROLES, GuardModel
 from .gemm_plan import WORKSPACE_BYTES as GEMM_WORKSPACE_BYTES
 from .gemm_plan import GemmPlans
@@ -280,10 +281,18 @@ class SlotStreamEngine(PreparedWeights):
         N = w.shape[0]
         if w.shape[1] != K or out.shape != (M, N) or x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
             raise ValueError("mm: shapes or strides do not match D[M, N] = A[M, K] . W[N, K]^T")
-        check(lib().hsg_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
-                                  M, N, K, self.gemm_plans.index(M, N, K), self.gemm_ws.data_ptr(),
-                                  self.gemm_ws.numel(), torch.cuda.current_stream(self.device).cuda_stream),
-              "hsg_gemm_bf16")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        index = self.gemm_plans.index(M, N, K)
+        rc = lib().hsg_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+                                 M, N, K, index, self.gemm_ws.data_ptr(), self.gemm_ws.numel(), stream)
+        if rc == HSG_ERR_SHAPE and index >= 0:
+            # the running hipBLASLt rejected the table's solution before launching anything: use the heuristic's
+            # first candidate for this shape from now on
+            warnings.warn(f"hipBLASLt rejected solution {index} for ({M}, {N}, {K}); using its heuristic instead")
+            self.gemm_plans.drop(M, N, K)
+            rc = lib().hsg_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
+                                     out.stride(0), M, N, K, -1, self.gemm_ws.data_ptr(), self.gemm_ws.numel(), stream)
+        check(rc, "hsg_gemm_bf16")
         return out
 
     def _view(self, name, *shape):
@@ -530,6 +539,10 @@ class SlotStreamEngine(PreparedWeights):
                 raise ValueError("Slot is outside the allocated range")
             if len(ids) == 0:
                 raise ValueError("Each request requires nonempty token IDs")
+            a = np.asarray(ids)
+            if a.dtype.kind not in "iu" or a.ndim != 1 or int(a.min()) < 0 or int(a.max()) >= self.cfg.vocab_size:
+                # the reference's contract (docs/ENGINE.md:9): the embedding gather must never see an id it lacks
+                raise ValueError("Each request requires nonempty in-vocabulary integer token IDs")
 
     def _replay(self, nb, tb, graph, inp, probs, host_in, host_out):
         """Send the packed inputs, run the tick (graph replay, or eagerly without graphs) and bring the
@@ -554,7 +567,8 @@ class SlotStreamEngine(PreparedWeights):
         lens = np.empty(n, dtype=np.int64)
         offsets = np.empty(n, dtype=np.int64)
         slots = np.empty(n, dtype=np.int64)
-        _hostpack.fill(requests, self.length, nb, tb, self.max_slots, host_np, lens, offsets, slots)
+        _hostpack.fill(requests, self.length, nb, tb, self.max_slots, self.cfg.vocab_size, host_np, lens, offsets,
+                       slots)
         self._replay(nb, tb, graph, inp, probs, host_in, host_out)
         self.length[slots] += lens
         return out_np, tb, lens, offsets
@@ -567,7 +581,7 @@ class SlotStreamEngine(PreparedWeights):
 
         The host work runs in hs_guard._hostpack (checks, packing, the padded result): the same layout and
         values as pack_ticks / padded_rows, at a few microseconds instead of a few hundred per tick."""
-        scan = _hostpack.scan(requests, self.max_slots)
+        scan = _hostpack.scan(requests, self.max_slots, self.cfg.vocab_size)
         if scan is not None and scan[0] > 0:
             n, total, max_len = scan
             if n > self.max_rows or max_len > self.max_tick_tokens:
@@ -592,7 +606,7 @@ class SlotStreamEngine(PreparedWeights):
     def step(self, requests):
         """requests: list of (slot, token_ids), each slot at most once. Returns {role: [CPU tensor [L_i, 3]]}
         (src/hs_guard/engine/slot_engine_v7.py:147-167)."""
-        scan = _hostpack.scan(requests, self.max_slots)
+        scan = _hostpack.scan(requests, self.max_slots, self.cfg.vocab_size)
         if scan is not None and 0 < scan[0] <= self.max_rows and scan[2] <= self.max_tick_tokens:
             # one tick (the serving case), host work native: the request-ordered outputs split per role
             n, total, _ = scan

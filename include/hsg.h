@@ -180,9 +180,10 @@ int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, 
  * 9..16: three launches (scores and block maxima per quarter of the ring columns into the workspace; per-block
  * probabilities times values; combine, gate, ring write). Packed layout: rows with lens[n] != 1 are not
  * touched. Padded layout: rows with lens[n] == 0 (or a slot outside [0, ring_rows)) get zero outputs.
- * workspace: device memory of at least hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes,
- * 16-byte aligned; its contents need no initialisation and are garbage afterwards. Supported: head_dim == 256,
- * window <= 512 and a multiple of 32, groups <= 16.
+ * workspace (groups > 8 only; ignored, and may be NULL, up to 8): device memory of at least
+ * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes, 16-byte aligned; its contents need no
+ * initialisation and are garbage afterwards. Supported: head_dim == 256, window <= 512 and a multiple of 32,
+ * groups <= 16.
  */
 size_t hsg_ring_decode_workspace_bytes(int32_t n_rows, int32_t hkv, int32_t groups, int32_t window);
 int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,
@@ -201,10 +202,11 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
  * static device array of HSG_RING_DECODE_SCRATCH_BYTES, one copy per GPU, held until the process ends; its
  * device address is looked up on the first call made on each device (make that first call outside graph
  * capture). Arguments, outputs and
- * numerics are those of hsg_ring_decode, bit for bit. Returns HSG_ERR_SHAPE when
- * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 486 rows at 4 kv
- * heads, G = 4, W = 512; 122 rows at G = 16). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams,
- * or two threads) race and must be serialised by the caller; nothing left by an earlier call is read.
+ * numerics are those of hsg_ring_decode, bit for bit. Up to 8 query heads per kv head the call runs the fused kernel,
+ * which uses no workspace, and takes any number of rows; above that it returns HSG_ERR_SHAPE when
+ * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 122 rows at 4 kv heads,
+ * G = 16, W = 512). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams, or two
+ * threads) race and must be serialised by the caller; nothing left by an earlier call is read.
  */
 #define HSG_RING_DECODE_SCRATCH_BYTES (48u << 20)
 int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,

@@ -50,23 +50,31 @@ def test_argument_errors_are_rejected_before_launch():
     rc = L.hsg_ring_attention(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
                               8, 8, 8, 8, None, 2, 1, 4, 4, 128, 1.0, 0, 0, 16, 0, 0, 0, 0, None)
     assert rc == -3
-    # split-K decode: head_dim 128 and a too-small workspace are rejected, n_rows == 0 is a no-op
-    need = L.hsg_ring_decode_workspace_bytes(2, 4, 4, 512)
+    # decode: head_dim 128 is rejected; on the split-K path (G > 8) a missing or too-small workspace is rejected;
+    # n_rows == 0 is a no-op
+    need = L.hsg_ring_decode_workspace_bytes(2, 4, 16, 512)
     assert need > 0
     rc = L.hsg_ring_decode(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
                            8, 8, 8, 8, None, 2, 4, 4, 128, 1.0, 1, 16, 0, 0, 0, 0, 16, need, None)
     assert rc == -3
     rc = L.hsg_ring_decode(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
-                           8, 8, 8, 8, None, 2, 4, 4, 256, 1.0, 1, 16, 0, 0, 0, 0, 16, need - 1, None)
+                           8, 8, 8, 8, None, 2, 4, 16, 256, 1.0, 1, 16, 0, 0, 0, 0, 16, need - 1, None)
     assert rc == -3
+    rc = L.hsg_ring_decode(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
+                           8, 8, 8, 8, None, 2, 4, 16, 256, 1.0, 1, 16, 0, 0, 0, 0, None, need, None)
+    assert rc == -1
     assert L.hsg_ring_decode(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, 0,
                              0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0, None, 0,
                              None) == 0
-    # allocation-free decode: sizes beyond its 48 MiB scratch are rejected before any device call; 0 rows is a no-op
-    unit = L.hsg_ring_decode_workspace_bytes(1, 4, 4, 512)
-    rows = (48 << 20) // unit + 1
+    # allocation-free decode: split-K sizes (G > 8) beyond its scratch are rejected before any device call (the
+    # placeholder pointers are never read); 0 rows is a no-op
+    cap = re.search(r"#define HSG_RING_DECODE_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    cap = int(cap.group(1)) << int(cap.group(2))
+    unit = L.hsg_ring_decode_workspace_bytes(1, 4, 16, 512)
+    rows = cap // unit + 1
+    assert L.hsg_ring_decode_workspace_bytes(rows, 4, 16, 512) > cap
     assert L.hsg_ring_decode_noalloc(16, 0, 256, 0, 0, 16, 16, rows + 1, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0,
-                                     0, 0, 0, 0, 8, 8, 8, 8, None, rows, 4, 4, 256, 1.0, 1, 16, 0, 0, 0, 0,
+                                     0, 0, 0, 0, 8, 8, 8, 8, None, rows, 4, 16, 256, 1.0, 1, 16, 0, 0, 0, 0,
                                      None) == -3
     assert L.hsg_ring_decode_noalloc(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0,
                                      0, 0, 0, None, None, None, None, None, 0, 4, 4, 256, 1.0, 1, None, 0, 0, 0, 0,

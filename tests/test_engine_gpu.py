@@ -335,6 +335,16 @@ def test_streaming_guard_api(setup):
         guard.step([(3, [1])])
     with pytest.raises(ValueError):
         guard.step([(0, [cfg.vocab_size])])
+    # the engine's own entry points (step_packed is the serving backend's call) refuse out-of-vocabulary ids too,
+    # before anything runs: lengths, rings and state stay as they were
+    eng = guard.engine
+    before = (eng.length.copy(), eng.rec.clone(), eng.ring_pos.clone())
+    for bad in ([(0, [1, cfg.vocab_size])], [(2, [3]), (1, [-1])], [(0, [2.0])], [(0, list(range(70)) + [10 ** 9])]):
+        for call in (eng.step, eng.step_packed):
+            with pytest.raises(ValueError, match="in-vocabulary"):
+                call(bad)
+    assert np.array_equal(eng.length, before[0]) and torch.equal(eng.rec, before[1])
+    assert torch.equal(eng.ring_pos, before[2])
 
 
 def test_reset_slots_neighbours_untouched_and_fresh(setup2):

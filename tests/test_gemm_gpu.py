@@ -117,3 +117,37 @@ def test_engine_mm_uses_the_table():
     rc, ref = _run(x, w, eng.gemm_plans.index(M, w.shape[0], w.shape[1]), eng.gemm_ws)
     torch.cuda.synchronize()
     assert rc == 0 and torch.equal(got, ref)
+
+
+def test_engine_mm_falls_back_when_a_solution_is_rejected():
+    """A table entry the running hipBLASLt does not have (an index out of its solution map: HSG_ERR_SHAPE, nothing
+    launched) is dropped with a warning and the product runs on the heuristic's first candidate."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    eng = SlotStreamEngine(GuardModel.random(cfg, seed=0, device="cuda"), 4, use_graphs=False)
+    w = eng.layers[0]["w_in"]
+    M, N, K = 24, w.shape[0], w.shape[1]
+    eng.gemm_plans.table[(M, N, K)] = 1 << 30
+    x = torch.randn(M, K, device="cuda").bfloat16()
+    with pytest.warns(UserWarning, match="rejected solution"):
+        got = eng.mm(x, w, torch.empty(M, N, dtype=torch.bfloat16, device="cuda"))
+    assert (M, N, K) not in eng.gemm_plans.table
+    rc, ref = _run(x, w, -1, eng.gemm_ws)
+    torch.cuda.synchronize()
+    assert rc == 0 and torch.equal(got, ref)
+
+
+def test_process_runs_torchs_hipblaslt():
+    """Loading the library binds the hipBLASLt torch bundles (the one the plan table was made with), whatever the
+    import order of the caller."""
+    import os
+    import torch as _torch
+    from hs_guard._lib import lib
+    lib().hsg_gemm_blas_version()
+    maps = open("/proc/self/maps").read()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libhipblaslt.so" in line}
+    torch_lib = os.path.realpath(os.path.join(os.path.dirname(_torch.__file__), "lib"))
+    assert paths and all(os.path.realpath(p).startswith(torch_lib) for p in paths), paths

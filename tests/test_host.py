@@ -212,14 +212,14 @@ def test_native_host_packing_matches_numpy_route():
             reqs.append((int(s) if i % 2 else np.int64(s), ids))
         length = rng.integers(0, 9000, max_slots).astype(np.int64)
         total = int(lens.sum())
-        assert _hostpack.scan(reqs, max_slots) == (n, total, int(lens.max()))
+        assert _hostpack.scan(reqs, max_slots, 151936) == (n, total, int(lens.max()))
         nb, tb = n + int(rng.integers(0, 5)), total + int(rng.integers(0, 40))
         ref = np.full(2 * tb + 4 * nb, -7, dtype=np.int64)
         order = np.argsort(-lens, kind="stable")
         lens_p, offs_p = pack_ticks([chunks[r] for r in order], slots[order], length, nb, tb, max_slots, ref)
         got = np.full(2 * tb + 4 * nb, -7, dtype=np.int64)
         g_lens, g_offs, g_slots = (np.empty(n, dtype=np.int64) for _ in range(3))
-        _hostpack.fill(reqs, length, nb, tb, max_slots, got, g_lens, g_offs, g_slots)
+        _hostpack.fill(reqs, length, nb, tb, max_slots, 151936, got, g_lens, g_offs, g_slots)
         np.testing.assert_array_equal(got, ref)
         np.testing.assert_array_equal(g_lens, lens)
         np.testing.assert_array_equal(g_slots, slots)
@@ -237,10 +237,16 @@ def test_native_host_packing_matches_numpy_route():
         _hostpack.gather_rows(flat, 2, tb, g_lens, g_offs, got_o)
         np.testing.assert_array_equal(got_o, want)
     # requests the engine's checks reject (or that the native route leaves to the numpy route): scan says None
-    ok = [(0, [1, 2]), (3, [4])]
-    assert _hostpack.scan(ok, 4) == (2, 3, 2)
-    for bad in ([(0, [1]), (0, [2])], [(4, [1])], [(-1, [1])], [(1, [])], [(1.0, [2])], [(1, (x for x in [2]))]):
-        assert _hostpack.scan(bad, 4) is None, bad
+    ok = [(0, [1, 2]), (3, [np.int32(9)])]
+    assert _hostpack.scan(ok, 4, 10) == (2, 3, 2)
+    for bad in ([(0, [1]), (0, [2])], [(4, [1])], [(-1, [1])], [(1, [])], [(1.0, [2])], [(1, (x for x in [2]))],
+                [(0, [1, 10])], [(0, [-1])], [(0, [np.int64(10)])], [(0, [2.0])], [(0, [np.float32(2)])],
+                [(2, [3]), (0, [1 << 40])]):
+        assert _hostpack.scan(bad, 4, 10) is None, bad
+    # fill refuses an out-of-vocabulary id itself (the docs/ENGINE.md:9 contract), before the tick could run
+    out, l3 = np.zeros(2 * 8 + 4 * 2, np.int64), np.zeros(2, np.int64)
+    with pytest.raises(ValueError, match="in-vocabulary"):
+        _hostpack.fill([(0, [1, 2]), (1, [10])], np.zeros(4, np.int64), 2, 8, 4, 10, out, l3, l3.copy(), l3.copy())
     with pytest.raises(ValueError):
         _hostpack.scatter_padded(np.zeros((2, 4, 3), np.float32), 2, 4, np.array([3], np.int64),
                                  np.array([2], np.int64), 4, np.zeros((2, 1, 4, 3), np.float32))
