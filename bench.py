@@ -364,24 +364,36 @@ def host_phases(torch, eng, load, steps=100):
     return out
 
 
-def v10_leg(torch, slots=352, steps=60, warmup=10, seed=0, state_dtype="float32"):
-    """The config-5 mixed load on the released v10 geometry (8 q / 2 kv attention heads, vocab 248,320; 754.5M
-    parameters, docs/evaluation.json:623) instead of the BASELINE geometry: random-init weights, contexts
-    U{512, 2048, 8000} prefilled untimed, ``steps`` timed mixed steps through step_packed (no resets). Reported
-    apart from the headline, which is quoted on the BASELINE geometry."""
+def config5_leg(torch, cfg_name="v10", slots=352, steps=60, warmup=10, seed=0, state_dtype="float32", reset_p=0.0,
+                model=None):
+    """The config-5 mixed load on a second engine, reported apart from the headline: ``cfg_name`` "v10" is the
+    released geometry (8 q / 2 kv attention heads, vocab 248,320; 754.5M parameters, docs/evaluation.json:623) with
+    its own random-init weights; "baseline" is the headline's geometry (pass its ``model`` to share the weights), for
+    another state storage (``state_dtype`` "float16": the reference StreamingGuard's, src/hs_guard/runtime.py:157).
+    Contexts U{512, 2048, 8000} prefilled untimed, ``steps`` timed mixed steps through step_packed, resets with
+    probability ``reset_p`` re-prefilled untimed."""
     from hs_guard.engine.slot_engine import SlotStreamEngine
     from hs_guard.model import GuardConfig, GuardModel
     from hs_guard.synthetic import MixedServingLoad
     dev = torch.device("cuda:0")
-    cfg = GuardConfig.v10()
-    model = GuardModel.random(cfg, seed=seed, device=dev, gen_device=dev)
+    cfg = getattr(GuardConfig, cfg_name)()
+    own = model is None
+    if own:
+        model = GuardModel.random(cfg, seed=seed, device=dev, gen_device=dev)
     eng = SlotStreamEngine(model, slots, state_dtype=state_dtype)
-    load = MixedServingLoad(slots=slots, vocab=cfg.vocab_size, seed=seed + 11, reset_p=0.0)
+    load = MixedServingLoad(slots=slots, vocab=cfg.vocab_size, seed=seed + 11, reset_p=reset_p)
     eng.step([(s, load.context()) for s in range(slots)])
     mean, sd = 4.175 * slots, 9.48 * slots ** 0.5
     eng.prepare(slots, range(slots, int(mean + 8 * sd) + 1, 16))
+
+    def reprefill():
+        gone = load.resets()
+        if gone:
+            eng.reset(gone)
+            eng.step([(s, load.context()) for s in gone])
     for _ in range(warmup):
         eng.step(load.step_requests())
+        reprefill()
     times, tokens = [], 0
     for _ in range(steps):
         req = load.step_requests()
@@ -391,11 +403,16 @@ def v10_leg(torch, slots=352, steps=60, warmup=10, seed=0, state_dtype="float32"
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
         tokens += sum(len(ids) for _, ids in req)
-    out = {"geometry": "v10: hidden 1024, 24 layers 3 GDN:1 attn, GDN 16x128, attn 8q/2kv/256 window 512, MLP 3584, "
-                       "vocab 248320", "params": model.num_parameters(), "slots": slots, "steps": steps,
-           "tokens_per_s": round(tokens / (sum(times) / 1e3), 1), "p50": round(percentile(times, 50), 3),
-           "p95": round(percentile(times, 95), 3)}
-    del eng, model
+        reprefill()
+    geometry = {"v10": "v10: hidden 1024, 24 layers 3 GDN:1 attn, GDN 16x128, attn 8q/2kv/256 window 512, MLP 3584, "
+                       "vocab 248320",
+                "baseline": "baseline (the headline's): attn 16q/4kv/256, vocab 151936"}[cfg_name]
+    out = {"geometry": geometry, "params": model.num_parameters(), "slots": slots, "state_dtype": state_dtype,
+           "reset_p": reset_p, "steps": steps, "tokens_per_s": round(tokens / (sum(times) / 1e3), 1),
+           "p50": round(percentile(times, 50), 3), "p95": round(percentile(times, 95), 3)}
+    del eng
+    if own:
+        del model
     torch.cuda.empty_cache()
     return out
 
@@ -552,8 +569,8 @@ def main():
     import numpy as np
     import torch
     from hs_guard._lib import lib
-    from hs_guard.engine.slot_engine import SlotStreamEngine
     from hs_guard.model import GuardConfig, GuardModel
+    from hs_guard.runtime import StreamingGuard, random_metadata
     from hs_guard.synthetic import MixedServingLoad
 
     dev = torch.device("cuda:0")
@@ -596,8 +613,12 @@ def main():
     t0 = time.time()
     model = GuardModel.random(cfg, seed=args.seed, device=dev, gen_device=dev)
     log(f"model {model.num_parameters() / 1e6:.1f}M params in {time.time() - t0:.1f}s")
-    extra = {} if args.chunk_min_tokens is None else {"chunk_min_tokens": args.chunk_min_tokens}
-    eng = SlotStreamEngine(model, args.slots, state_dtype=args.state_dtype, **extra)
+    # the public API object (src/hs_guard/runtime.py:148-174); the headline times its engine's step_packed, the
+    # serving backend's call, and the guard_step leg times guard.step() itself
+    guard = StreamingGuard(model, random_metadata(), max_slots=args.slots, state_dtype=args.state_dtype)
+    eng = guard.engine
+    if args.chunk_min_tokens is not None:
+        eng.chunk_min_tokens = args.chunk_min_tokens   # before the first tick: every graph is captured with it
     load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
                             contexts=tuple(int(x) for x in args.contexts.split(",")), reset_p=args.reset_p)
 
@@ -687,6 +708,21 @@ def main():
                 "p50": round(percentile([t * 1e3 for t in api_t], 50), 3),
                 "p95": round(percentile([t * 1e3 for t in api_t], 95), 3)}
     log(f"step() leg {api_step}")
+    # the same load through StreamingGuard.step() (the API the north star names): the reference's per-id checks,
+    # the engine's step(), then one record per request with its cut scores 1 - p(safe) as a Python list
+    g_t, g_tok = [], 0
+    for i in range(60):
+        req = load.step_requests()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        guard.step(req, role="assistant")
+        g_t.append(time.perf_counter() - t0)
+        g_tok += sum(len(ids) for _, ids in req)
+        reprefill(load.resets())
+    guard_step = {"steps": len(g_t), "tokens_per_s": round(g_tok / sum(g_t), 1),
+                  "p50": round(percentile([t * 1e3 for t in g_t], 50), 3),
+                  "p95": round(percentile([t * 1e3 for t in g_t], 95), 3)}
+    log(f"StreamingGuard.step() leg {guard_step}")
     phases = host_phases(torch, eng, MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed + 3,
                                                       reset_p=0.0))
     log(f"host phases of a tick (us) {phases}")
@@ -696,7 +732,7 @@ def main():
                           "tokens": tokens, "ms_per_step": round(total / args.steps * 1e3, 4),
                           "latency_ms": {"p50": round(percentile(step_ms, 50), 3),
                                          "p95": round(percentile(step_ms, 95), 3)}, "api_step": api_step,
-                          "host_phases_us": phases}),
+                          "guard_step": guard_step, "host_phases_us": phases}),
               flush=True)
         return
 
@@ -761,7 +797,13 @@ def main():
     log(f"complete-message scorer, 8000 tokens: {whole_ms:.1f} ms")
 
     del scorer
-    v10 = v10_leg(torch, slots=args.slots, seed=args.seed, state_dtype=args.state_dtype)
+    # the headline load with the reference StreamingGuard's fp16 state storage, on the same weights (a second
+    # engine; the headline's is left as it is)
+    other = "float16" if args.state_dtype == "float32" else "float32"
+    state_leg = config5_leg(torch, "baseline", slots=args.slots, steps=100, seed=args.seed, state_dtype=other,
+                            reset_p=args.reset_p, model=model)
+    log(f"config 5 at {other} state {state_leg}")
+    v10 = config5_leg(torch, "v10", slots=args.slots, seed=args.seed, state_dtype=args.state_dtype)
     log(f"v10 geometry {v10}")
 
     cpu = None
@@ -792,6 +834,7 @@ def main():
                        "max": round(max(step_ms), 3)},
         "latency_by_context_ms": by_context,
         "api_step": api_step,
+        "guard_step": guard_step,
         "host_phases_us": phases,
         "decode_352x1_ms": {"p50": round(percentile(dec, 50), 3), "p95": round(percentile(dec, 95), 3),
                             "tokens_per_s": round(args.slots / (np.mean(dec) / 1e3), 1)},
@@ -808,6 +851,7 @@ def main():
         "gdn_lone_row_64": lone,
         "prefill_352_contexts": prefill,
         "complete_message_8000": {"ms": round(whole_ms, 2), "tokens_per_s": round(8000 / whole_ms * 1e3, 1)},
+        f"config5_{other}_state": state_leg,
         "v10_geometry": v10,
         "cpu_baseline": cpu,
     }
