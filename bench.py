@@ -51,17 +51,24 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     on the stream the kernel is launched on. Algorithmic bytes per launch: per (row, head) the state read +
     write 2*K*V*4 B and the 3-row conv history of its 3*128 channels read + written 2 x 3 x 384 x 2 B, per (row,
     head, token) the raw q, k, v, z in and out = 5 x 256 B and a, b = 4 B, and once per launch the conv
-    weights 16 x 384 x 4 x 2 B."""
+    weights 16 x 384 x 4 x 2 B.
+
+    Launch i works on state buffer and conv pool i mod 3, so no launch reads what the previous one wrote: in a step
+    each GDN layer's state was last touched a whole step earlier, and one buffer reused back to back would be
+    read partly from the 256 MB Infinity Cache (352 x 1, fp32 state, on MI355X: 119 us with one buffer, 155 us
+    rotating three)."""
+    from hs_guard._lib import HSG_GDN_BURST_MIN_DEFAULT
     dev = torch.device("cuda:0")
     H = HV = 16
     K = V = 128
     C = 3 * H * K
     stride = C + HV * V + 2 * HV
     gen = torch.Generator(device=dev).manual_seed(1)
-    state = (torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02)
-    if state_dtype == 1:
-        state = state.half()
-    pool = torch.randn(rows + 1, 3, C, generator=gen, device=dev).bfloat16()
+    states, pools = [], []
+    for _ in range(3):
+        state = (torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02)
+        states.append(state.half() if state_dtype == 1 else state)
+        pools.append(torch.randn(rows + 1, 3, C, generator=gen, device=dev).bfloat16())
     conv_w = (torch.randn(C, 4, generator=gen, device=dev) * 0.3).bfloat16()
     proj = torch.randn(rows, stride, generator=gen, device=dev).bfloat16()
     out = torch.empty(rows, HV * V, dtype=torch.bfloat16, device=dev)
@@ -73,21 +80,22 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
     stream = torch.cuda.current_stream(dev)
     base = proj.data_ptr()
 
-    def launch():
-        rc = lib.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, conv_w.data_ptr(), pool.data_ptr(),
-                                              C, base + 2 * (C + HV * V + HV), base + 2 * (C + HV * V), stride,
-                                              A.data_ptr(), A.data_ptr(), state.data_ptr(), state_dtype, rows + 1,
-                                              slots.data_ptr(), lens.data_ptr(), offs.data_ptr(), rows, H, HV, K, V,
-                                              K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(),
-                                              stream.cuda_stream)
+    def launch(i):
+        rc = lib.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, conv_w.data_ptr(),
+                                              pools[i % 3].data_ptr(), C, base + 2 * (C + HV * V + HV),
+                                              base + 2 * (C + HV * V), stride, A.data_ptr(), A.data_ptr(),
+                                              states[i % 3].data_ptr(), state_dtype, rows + 1, slots.data_ptr(),
+                                              lens.data_ptr(), offs.data_ptr(), rows, H, HV, K, V, K ** -0.5,
+                                              base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(),
+                                              HSG_GDN_BURST_MIN_DEFAULT, stream.cuda_stream)
         assert rc == 0, rc
-    for _ in range(10):
-        launch()
+    for i in range(9):
+        launch(i)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for _ in range(iters):
-        launch()
+    for i in range(iters):
+        launch(i)
     t1.record(stream)
     torch.cuda.synchronize()
     us = t0.elapsed_time(t1) * 1e3 / iters
@@ -101,10 +109,11 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
             "achieved_gbs": round(gbs, 1)}
 
 
-def lone_row_rate(torch, lib, tokens=64, iters=20):
+def lone_row_rate(torch, lib, tokens=64, iters=20, burst_min=8):
     """The conv + gated GDN slot step (hsg_gdn_conv_slot_step_gated) on one row of ``tokens`` tokens, 16 heads x
     128, fp32 state, every other row of an 8-row grid empty: a mixed tick's critical path when its longest row
-    runs on the slot step (the chip otherwise idle). HIP events on the launch stream around ``iters`` launches."""
+    runs on the slot step (the chip otherwise idle). HIP events on the launch stream around ``iters`` launches.
+    ``burst_min`` as the entry point's (0: token by token; 8: the row in bursts of 8 tokens on MFMA)."""
     dev = torch.device("cuda:0")
     N, H, K = 8, 16, 128
     C = 3 * H * K
@@ -130,7 +139,7 @@ def lone_row_rate(torch, lib, tokens=64, iters=20):
                                               A.data_ptr(), A.data_ptr(), state.data_ptr(), 0, N + 1,
                                               slots.data_ptr(), lens.data_ptr(), offs.data_ptr(), N, H, H, K, K,
                                               K ** -0.5, base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(),
-                                              stream.cuda_stream)
+                                              burst_min, stream.cuda_stream)
         assert rc == 0, rc
     launch()
     torch.cuda.synchronize()
@@ -141,7 +150,66 @@ def lone_row_rate(torch, lib, tokens=64, iters=20):
     t1.record(stream)
     torch.cuda.synchronize()
     us = t0.elapsed_time(t1) * 1e3 / iters
-    return {"tokens": tokens, "avg_us": round(us, 2), "us_per_token": round(us / tokens, 3)}
+    return {"tokens": tokens, "burst_min": burst_min, "avg_us": round(us, 2), "us_per_token": round(us / tokens, 3)}
+
+
+def gdn_tick_rate(torch, lib, rows=352, iters=30, seed=5, burst_mins=(0, 8)):
+    """The conv + gated GDN slot step (hsg_gdn_conv_slot_step_gated, as the engine runs every GDN layer of a mixed
+    tick) on a config-5 tick: 352 rows, chunk lengths 1 (p 0.8), 2-16 (p 0.15), 17-64 (p 0.05), packed longest
+    first, 16 heads x 128, fp32 state, for each burst threshold in ``burst_mins``. HIP events on the launch stream
+    around ``iters`` launches. Algorithmic bytes: per (row, head) the state and the conv history read and written,
+    per (token, head) q, k, v, z in, the output out and a, b, as the roofline leg counts them. Slots are a random
+    permutation (as the engine's schedule assigns them) and launch i works on state buffer and conv pool i mod 3,
+    as in the roofline leg."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    H = HV = 16
+    K = V = 128
+    C = 3 * H * K
+    stride = C + HV * V + 2 * HV
+    rng = np.random.default_rng(seed)
+    u = rng.random(rows)
+    lens_h = np.where(u < 0.8, 1, np.where(u < 0.95, rng.integers(2, 17, rows), rng.integers(17, 65, rows)))
+    lens_h = np.sort(lens_h)[::-1].copy()
+    T = int(lens_h.sum())
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    states = [torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02 for _ in range(3)]
+    pools = [torch.randn(rows + 1, 3, C, generator=gen, device=dev).bfloat16() for _ in range(3)]
+    conv_w = (torch.randn(C, 4, generator=gen, device=dev) * 0.3).bfloat16()
+    proj = torch.randn(T, stride, generator=gen, device=dev).bfloat16()
+    out = torch.empty(T, HV * V, dtype=torch.bfloat16, device=dev)
+    A = torch.zeros(HV, dtype=torch.bfloat16, device=dev)
+    w = torch.ones(V, dtype=torch.bfloat16, device=dev)
+    slots = torch.from_numpy(rng.permutation(rows)).to(dev)
+    lens = torch.from_numpy(lens_h).to(dev)
+    offs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens_h)[:-1]])).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    base = proj.data_ptr()
+    res = {"rows": rows, "tokens": T, "multi_token_rows": int((lens_h > 1).sum()), "state_buffers": 3}
+    alg = rows * HV * (2 * K * V * 4 + 2 * 3 * 3 * K * 2) + T * HV * (5 * 256 + 4) + HV * 3 * K * 4 * 2
+    for bm in burst_mins:
+        def launch(i):
+            rc = lib.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, conv_w.data_ptr(),
+                                                  pools[i % 3].data_ptr(), C, base + 2 * (C + HV * V + HV),
+                                                  base + 2 * (C + HV * V), stride, A.data_ptr(), A.data_ptr(),
+                                                  states[i % 3].data_ptr(), 0, rows + 1, slots.data_ptr(),
+                                                  lens.data_ptr(), offs.data_ptr(), rows, H, HV, K, V, K ** -0.5,
+                                                  base + 2 * C, stride, w.data_ptr(), 1e-6, out.data_ptr(), bm,
+                                                  stream.cuda_stream)
+            assert rc == 0, rc
+        for i in range(6):
+            launch(i)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(iters):
+            launch(i)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / iters
+        res[f"burst_min_{bm}"] = {"avg_us": round(us, 2), "hbm_frac": round(alg / (us * 1e-6) / 8e12, 3)}
+    res["alg_bytes_per_launch"] = alg
+    return res
 
 
 def calibration_copy(torch, dev):
@@ -543,6 +611,8 @@ def main():
                     help="only the dominant-kernel measurement (the command profiled under rocprofv3)")
     ap.add_argument("--chunk-only", action="store_true",
                     help="only the config-4 chunked-prefill measurement (profiled under rocprofv3)")
+    ap.add_argument("--gdn-tick-only", action="store_true",
+                    help="only the GDN slot step on a config-5 tick at several burst thresholds, and a lone 64-token row")
     ap.add_argument("--ring-tick-only", action="store_true",
                     help="only the tiled ring attention on a config-5 mixed tick's multi-token rows")
     ap.add_argument("--ring-only", action="store_true",
@@ -556,6 +626,9 @@ def main():
     ap.add_argument("--chunk-min-tokens", type=int, default=None,
                     help="SlotStreamEngine's chunk_min_tokens (default: the engine's; 0 puts every GDN row on the "
                          "slot step)")
+    ap.add_argument("--gdn-burst-min", type=int, default=None,
+                    help="SlotStreamEngine's gdn_burst_min (default: the engine's): slot-step rows of at least this "
+                         "many tokens run in 8-token bursts on MFMA (0: every row token by token)")
     ap.add_argument("--sweep-steps", type=int, default=60,
                     help="timed mixed steps per initial-context length in the per-context latency sweep (0: skip)")
     args = ap.parse_args()
@@ -568,7 +641,7 @@ def main():
 
     import numpy as np
     import torch
-    from hs_guard._lib import lib
+    from hs_guard._lib import HSG_GDN_BURST_MIN_DEFAULT, lib
     from hs_guard.model import GuardConfig, GuardModel
     from hs_guard.runtime import StreamingGuard, random_metadata
     from hs_guard.synthetic import MixedServingLoad
@@ -577,7 +650,13 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}")
     state_code = 0 if args.state_dtype == "float32" else 1
     if args.lone_row_only:
-        print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib())}), flush=True)
+        print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib()),
+                          "gdn_lone_row_64_token_path": lone_row_rate(torch, lib(), burst_min=0)}), flush=True)
+        return
+    if args.gdn_tick_only:
+        print(json.dumps({"gdn_tick": gdn_tick_rate(torch, lib(), rows=args.slots, burst_mins=(0, 8, 16, 32)),
+                          "gdn_lone_row_64": lone_row_rate(torch, lib()),
+                          "gdn_lone_row_64_token_path": lone_row_rate(torch, lib(), burst_min=0)}), flush=True)
         return
     if args.ring_tick_only:
         print(json.dumps({"ring_attn_tick": ring_tick_rate(torch, rows=args.slots)}), flush=True)
@@ -606,7 +685,8 @@ def main():
         log(f"tiled ring attention, mixed tick {tick}")
         chunk = chunk_prefill_rate(torch)
         log(f"chunk prefill config 4 {chunk}")
-        lone = lone_row_rate(torch, lib())
+        lone = lone_row_rate(torch, lib(), burst_min=(HSG_GDN_BURST_MIN_DEFAULT if args.gdn_burst_min is None
+                                                      else args.gdn_burst_min))
         log(f"GDN slot step, one 64-token row {lone}")
 
     cfg = GuardConfig.baseline()
@@ -619,6 +699,8 @@ def main():
     eng = guard.engine
     if args.chunk_min_tokens is not None:
         eng.chunk_min_tokens = args.chunk_min_tokens   # before the first tick: every graph is captured with it
+    if args.gdn_burst_min is not None:
+        eng.gdn_burst_min = args.gdn_burst_min   # before the first tick, as chunk_min_tokens
     load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
                             contexts=tuple(int(x) for x in args.contexts.split(",")), reset_p=args.reset_p)
 

@@ -58,6 +58,7 @@ struct GdnParams {
   float eps;
   uint16_t* out;
   int skip_rows, skip_min_len;   // packed layout: rows n < skip_rows with lens >= skip_min_len are left alone
+  int mfma_min;                  // rows of at least this many tokens take the MFMA burst path (0: none)
   // fused causal conv (CONV): qkv holds the raw projection; weights [conv_C, 4], history pool [state_rows, 3, conv_C]
   const uint16_t* conv_w;
   uint16_t* conv_pool;
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   __shared__ __align__(16) float fk_[CT][KD / ROWS][ROWS + 4];
   __shared__ __align__(16) uint16_t sv_[CT][VD];
   __shared__ __align__(16) uint16_t sz_[GATED ? CT : 1][VD];
-  __shared__ __align__(16) float so_[GATED ? CT : 1][VD];   // bf16-rounded o of the burst, for the gated norm
+  __shared__ __align__(16) float so_[CT][VD];   // bf16-rounded o of the burst (gated norm; the burst path's outputs)
   __shared__ float sdec_[CT], sbe_[CT];
   constexpr int SEGS = GATED ? 64 : 48;   // 16-byte segments per token: q, k, v (, z)
   // CONV: the burst's raw q, k, v rows (48 segments each), then its z rows; the first burst also fetches the 3
@@ -416,6 +417,322 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       sbe_[tid] = sigmoidf_(bf2f(pb));
     }
   };
+  // gated RMSNorm of the burst's outputs (so_, bf16-rounded o), stored to `out`: 32 threads per token, 4 value
+  // columns each
+  auto gated_epilogue = [&](int t0, int nt) __attribute__((always_inline)) {
+    __syncthreads();
+    const int u = threadIdx.x >> 5;
+    const int cc = (threadIdx.x & 31) * 4;
+    const f32x4_t ob = *reinterpret_cast<const f32x4_t*>(&so_[u][cc]);
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part += ob[i] * ob[i];
+    part = sum32_dpp(part);
+    const float r = rsqrtf(part * (1.0f / VD) + p.eps);
+    if (u < nt) {
+      float y[4], z4[4], w4[4];
+      load4_bf16(&sz_[GATED ? u : 0][cc], z4);
+      load4_bf16(&sw_[GATED ? cc : 0], w4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float hb = rbf(ob[i] * r);
+        const float tw = rbf(w4[i] * hb);
+        y[i] = tw * siluf_(z4[i]);
+      }
+      store4_bf16(p.out + (tok0 + t0 + u) * (int64_t)(p.HV * VD) + hv * VD + cc, y);
+    }
+  };
+  // the next burst into LDS once every read of this one is done
+  auto next_burst = [&](int t0) __attribute__((always_inline)) {
+    // the next burst's conv history: this (full) burst's last 3 raw rows
+    if (CONV && threadIdx.x < (CKS - 1) * 48)
+      hist = *reinterpret_cast<const u32x4*>(&rw_[CONV ? CT + threadIdx.x / 48 : 0][(threadIdx.x % 48) * 8]);
+    __syncthreads();
+    stage(min(CT, ntok - t0 - CT), false);
+  };
+  auto store_conv_history = [&]() __attribute__((always_inline)) {
+    if (CONV && threadIdx.x < (CKS - 1) * 48) {
+      // new conv history = ext[ntok .. ntok + 2] of ext = [pool; tokens]: raw rows nt .. nt + 2 of the last burst
+      // (the row's last three tokens, or old pool rows when it has fewer); every read of the old rows came first
+      const int nt_last = ntok - (ntok - 1) / CT * CT;
+      const int i = threadIdx.x / 48, sg = threadIdx.x % 48;
+      *reinterpret_cast<u32x4*>(p.conv_pool + (slot * (CKS - 1) + i) * (int64_t)p.conv_C + conv_ch(8 * sg)) =
+          *reinterpret_cast<const u32x4*>(&rw_[CONV ? nt_last + i : 0][8 * sg]);
+    }
+  };
+
+  // ---------------------------------------------------------------------------------------------------------
+  // Burst path, for rows of at least p.mfma_min tokens: each burst of CT tokens in the WY/UT chunk form on fp32
+  // MFMA (v_mfma_f32_16x16x4f32) instead of CT dependent token updates on the VALU. With Gamma_t the decay from
+  // the burst's start through token t, X = K S0, Y = Q S0 (one product: K and Q stacked as the 16 rows of one
+  // operand), A[t][s] = beta_t Gamma_t / Gamma_s (k_t . k_s) for s < t, T = (I + A)^-1:
+  //   V' = T diag(beta) (V - diag(Gamma) X),  O = diag(Gamma) Y + (Gamma_t / Gamma_s (q_t . k_s))_{s<=t} V',
+  //   S_C = Gamma_C S0 + K^T diag(Gamma_C / Gamma) V'
+  // (the token recurrence unrolled; equal in exact arithmetic). The state stays in registers in the MFMA
+  // accumulator layout, as St with S = D St (D folded back as in the token path): wave w owns value columns
+  // [32w, 32w + 32) as 16 tiles of 16 keys x 16 columns; lane (j4 = lane / 16, n16 = lane % 16) holds
+  // Sm[2 kt + ct][i] = St[16 kt + 4 j4 + i][32 w + 16 ct + n16]. In X = K St that is the B operand as it stands
+  // (the contraction index of step (kt, i), slot j4, is key 16 kt + 4 j4 + i), and the update K^T W accumulates
+  // onto it. Staging, the conv, the gated norm and the conv history are the token path's.
+  // ---------------------------------------------------------------------------------------------------------
+  if (p.mfma_min > 0 && ntok >= p.mfma_min) {   // uniform over the workgroup
+    __shared__ __align__(16) float gp_[4][CT][2 * CT];   // per-wave partial Gram rows: K k^T (t < CT), Q k^T
+    __shared__ __align__(16) float am_[CT][CT], tm_[CT][CT], bm_[CT][CT], fac_[2][CT];
+    // the (slot, head) state block as a buffer resource: every state load and store is one VGPR lane offset,
+    // the key tile's offset as a scalar and the rest as an immediate (no per-access 64-bit addresses, which the
+    // compiler would otherwise compute up front and keep live across the bursts)
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<ST*>(p.state) + (slot * p.HV + hv) * (int64_t)(KD * VD), (short)0,
+        (int)(KD * VD * sizeof(ST)), 0x00020000);
+    // token index of contraction slot k at step s of an 8-token contraction: lanes 0-31 take their own rows
+    // 4 k + 2 s, lanes 32-63 rows 4 (k - 2) + 2 s + 1 through permlane32_swap (see bop)
+    auto tau = [](int s, int k) { return 4 * (k & 1) + 2 * s + (k >> 1); };
+    // B operand of an 8-token contraction from a D-layout value (rows 4 j4 + i): lanes 0-31 keep register 2 s,
+    // lanes 32-63 receive register 2 s + 1 of lane - 32
+    auto bop = [](const f32x4_t& x, int s) {
+      return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x[2 * s]), __float_as_uint(x[2 * s + 1]),
+                                                              false, false)[0]);
+    };
+    // zero the K and Q rows of a partial burst's missing tokens (products with them must be exactly zero)
+    auto zero_pad = [&](int nt) __attribute__((always_inline)) {
+      for (int e = threadIdx.x; e < (CT - nt) * KD; e += 256) {
+        const int u = nt + e / KD, cc = e % KD;
+        fq_[u][cc / ROWS][cc % ROWS] = 0.f;
+        fk_[u][cc / ROWS][cc % ROWS] = 0.f;
+      }
+    };
+    if constexpr (CONV) fetch_first_conv();
+    else fetch(0);
+    u32x4 cwr[4], swr;
+    if constexpr (CONV) {
+      const uint16_t* wsrc = p.conv_w + (int64_t)conv_ch(8 * min((int)threadIdx.x, CH3 / 8 - 1)) * CKS;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cwr[j] = *reinterpret_cast<const u32x4*>(wsrc + 8 * j);
+    }
+    if constexpr (GATED) swr = *reinterpret_cast<const u32x4*>(p.norm_w + 8 * min((int)threadIdx.x, VD / 8 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const int soff = (4 * (lane >> 4) * VD + wave * TILE_V + (lane & 15)) * (int)sizeof(ST);   // lane's byte offset
+    constexpr int KT_BYTES = 16 * VD * (int)sizeof(ST);
+    f32x4_t Sm[16];
+#pragma unroll
+    for (int kt = 0; kt < KD / 16; ++kt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int off = soff + (i * VD + 16 * ct) * (int)sizeof(ST);
+          if constexpr (sizeof(ST) == 4)
+            Sm[2 * kt + ct][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, kt * KT_BYTES, 0));
+          else
+            Sm[2 * kt + ct][i] = h2f(__builtin_amdgcn_raw_buffer_load_b16(srs, off, kt * KT_BYTES, 0));
+        }
+    if (CONV && threadIdx.x < CH3 / 8) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(&cw_[CONV ? 8 * threadIdx.x : 0][0] + 8 * j) = cwr[j];
+    }
+    if (GATED && threadIdx.x < VD / 8) *reinterpret_cast<u32x4*>(&sw_[GATED ? 8 * threadIdx.x : 0]) = swr;
+    float D = 1.0f;
+    stage(min(CT, ntok), true);
+    zero_pad(min(CT, ntok));
+    for (int t0 = 0; t0 < ntok; t0 += CT) {
+      const int nt = min(CT, ntok - t0);
+      if (t0 + CT < ntok) fetch(t0 + CT);
+      __syncthreads();
+      // lane indices of this burst's products, recomputed here (not hoisted out of the loop: every address
+      // derived from them would otherwise stay live across the next burst's staging)
+      const int bt = tid_per_site();
+      const int j4 = (bt & 63) >> 4, n16 = bt & 15;
+      const int cbase = (bt >> 6) * TILE_V + n16;
+      // X = K St (rows 0-7) and Y = Q St (rows 8-15); this wave's share of the Gram products [K; Q] K^T
+      f32x4_t xy[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      f32x4_t gr = {0.f, 0.f, 0.f, 0.f};
+      const float* arow = n16 < CT ? &fk_[n16 & (CT - 1)][0][4 * j4] : &fq_[n16 & (CT - 1)][0][4 * j4];
+#pragma unroll
+      for (int kt = 0; kt < KD / 16; ++kt) {
+        const f32x4_t a4 = *reinterpret_cast<const f32x4_t*>(arow + kt * (ROWS + 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xy[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i], Sm[2 * kt][i], xy[0], 0, 0, 0);
+          xy[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i], Sm[2 * kt + 1][i], xy[1], 0, 0, 0);
+        }
+      }
+      // this wave's two key tiles of the Gram products (B = the same operand: [K; Q] row n16 against keys)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const f32x4_t a4 = *reinterpret_cast<const f32x4_t*>(arow + (2 * wave + kk) * (ROWS + 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gr = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i], a4[i], gr, 0, 0, 0);
+      }
+      // partial Gram rows 0-15 (k_t or q_t against k_s, s < CT): lanes n16 < CT of every row group
+      if (n16 < CT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gp_[wave][(4 * j4 + i) & (CT - 1)][(j4 >> 1) * CT + n16] = gr[i];
+      }
+      lds_barrier();
+      // the burst's small matrices, by wave 0 (the others wait at the barrier below). gamma = 1, beta = 0 past nt.
+      //   lane 8 t + s: A[t][s] = beta_t Gamma_t / Gamma_s (k_t . k_s) for s < t and Bm[t][s] = Gamma_t / Gamma_s
+      //   (q_t . k_s) for s <= t, from the four waves' partial Gram sums; lanes 0-7: the factors Gamma_t D and c_t,
+      //   then column t of T = (I + A)^-1 by forward substitution over A read back from LDS. Every operand is
+      //   loaded before the arithmetic that uses it (no LDS round trip per term).
+      if (wave == 0) {
+        const int ln = lane;
+        float g8[CT];
+#pragma unroll
+        for (int r = 0; r < CT; ++r) g8[r] = r < nt ? sdec_[r] : 1.0f;
+        {
+          const int t = ln >> 3, sc = ln & 7;
+          float kk = 0.f, qk = 0.f;
+#pragma unroll
+          for (int w4 = 0; w4 < 4; ++w4) {
+            kk += gp_[w4][t][sc];
+            qk += gp_[w4][t][CT + sc];
+          }
+          float ratio = 1.0f;   // Gamma_t / Gamma_sc = product of gamma over (sc, t]
+#pragma unroll
+          for (int r = 1; r < CT; ++r) ratio *= (r > sc && r <= t) ? g8[r] : 1.0f;
+          am_[t][sc] = sc < t && t < nt ? sbe_[t] * ratio * kk : 0.0f;
+          bm_[t][sc] = sc <= t ? ratio * qk : 0.0f;
+        }
+        if (ln < CT) {
+          float g_to_t = 1.0f, g_after = 1.0f, gcw = 1.0f;   // Gamma_t, Gamma_C / Gamma_t, Gamma_C
+#pragma unroll
+          for (int r = 0; r < CT; ++r) {
+            g_to_t *= r <= ln ? g8[r] : 1.0f;
+            g_after *= r > ln ? g8[r] : 1.0f;
+            gcw *= g8[r];
+          }
+          fac_[0][ln] = g_to_t * D;
+          fac_[1][ln] = D * gcw < 0x1p-40f ? g_after : 1.0f / (g_to_t * D);
+        }
+        // the lanes' A entries are read by other lanes of this wave: a wave-scope fence orders them
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (ln < CT) {
+          const int sc = ln;   // column of T: T[t][sc] = -sum_{sc <= r < t} A[t][r] T[r][sc], T[sc][sc] = 1
+          float a[CT][CT];
+#pragma unroll
+          for (int t = 1; t < CT; ++t)
+#pragma unroll
+            for (int r = 0; r < t; ++r) a[t][r] = am_[t][r];
+          float tc[CT];
+#pragma unroll
+          for (int t = 0; t < CT; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int r = 0; r < t; ++r) acc = fmaf(r >= sc ? a[t][r] : 0.0f, tc[r], acc);
+            tc[t] = t < sc ? 0.0f : t == sc ? 1.0f : -acc;
+          }
+#pragma unroll
+          for (int t = 0; t < CT; ++t) tm_[t][sc] = tc[t];
+        }
+      }
+      lds_barrier();
+      float gc = 1.0f;   // Gamma_C, the same product in every thread
+      for (int r = 0; r < CT; ++r) gc *= r < nt ? sdec_[r] : 1.0f;
+      f32x4_t w[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        // Every LDS operand below is read unconditionally from a clamped index and pinned there, and the lane
+        // conditions select after: a read inside a conditional compiles to a branch with its own wait.
+        // R = beta (V - Gamma D X) on rows 0-7 (lanes j4 < 2); zero elsewhere
+        f32x4_t rr, oc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = (4 * j4 + i) & (CT - 1);
+          const int cc = cbase + 16 * ct;
+          const float v = loaded_here(CONV ? bf2f(co_[CONV ? t : 0][CONV ? 2 * KD + cc : 0]) : bf2f(sv_[t][cc]));
+          const float be = loaded_here(sbe_[t]), f0 = loaded_here(fac_[0][t]);
+          const float r = be * (v - f0 * xy[ct][i]);
+          rr[i] = (j4 < 2 && t < nt) ? r : 0.0f;
+          oc[i] = j4 >= 2 ? f0 * xy[ct][i] : 0.0f;   // O's C input: Gamma D Y (rows 8-15)
+        }
+        float ta[2], ba[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const float tv = loaded_here(tm_[n16 & (CT - 1)][tau(s2, j4)]);
+          const float bv = loaded_here(bm_[n16 & (CT - 1)][tau(s2, j4)]);
+          ta[s2] = n16 < CT ? tv : 0.0f;
+          ba[s2] = n16 >= CT ? bv : 0.0f;
+        }
+        // V' = T R (rows 0-7)
+        f32x4_t vp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) vp = __builtin_amdgcn_mfma_f32_16x16x4f32(ta[s2], bop(rr, s2), vp, 0, 0, 0);
+        // O = Gamma D Y + Bm V' (rows 8-15: the lanes holding Y)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) oc = __builtin_amdgcn_mfma_f32_16x16x4f32(ba[s2], bop(vp, s2), oc, 0, 0, 0);
+        // the burst's outputs (rows 8-15) -> so_, rounded to bf16 as the token path stores them. Rows at and past
+        // nt hold padding tokens' outputs, which the epilogue reads but never stores.
+        if (j4 >= 2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) so_[4 * (j4 - 2) + i][cbase + 16 * ct] = rbf(oc[i]);
+        }
+        // W = c V' (rows 0-7) for the state update
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float f1 = loaded_here(fac_[1][(4 * j4 + i) & (CT - 1)]);
+          w[ct][i] = j4 < 2 ? f1 * vp[i] : 0.0f;
+        }
+      }
+      if (D * gc < 0x1p-40f) {   // uniform: fold D and the burst's decay into St before the update
+        const float f = D * gc;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Sm[e] *= f;
+        D = 1.0f;
+      } else {
+        D *= gc;
+      }
+      // S += K^T W: A = K^T (key 16 kt + n16, token tau), B = W
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float b0 = bop(w[0], s2), b1 = bop(w[1], s2);
+        const float* krow = &fk_[tau(s2, j4)][0][n16];
+#pragma unroll
+        for (int kt = 0; kt < KD / 16; ++kt) {
+          const float a = krow[kt * (ROWS + 4)];
+          Sm[2 * kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b0, Sm[2 * kt], 0, 0, 0);
+          Sm[2 * kt + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b1, Sm[2 * kt + 1], 0, 0, 0);
+        }
+      }
+      if constexpr (GATED) {
+        gated_epilogue(t0, nt);
+      } else {
+        __syncthreads();
+        const int u = threadIdx.x >> 5, cc = (threadIdx.x & 31) * 4;
+        if (u < nt) {
+          const f32x4_t ob = *reinterpret_cast<const f32x4_t*>(&so_[u][cc]);
+          const int64_t base = ((tok0 + t0 + u) * p.HV + hv) * VD + cc;
+          const float o4[4] = {ob[0], ob[1], ob[2], ob[3]};
+          store4_bf16(p.o + base, o4);
+          if (p.sq != nullptr)
+            *reinterpret_cast<float4*>(p.sq + base) = make_float4(ob[0] * ob[0], ob[1] * ob[1], ob[2] * ob[2],
+                                                                  ob[3] * ob[3]);
+        }
+      }
+      if (t0 + CT < ntok) {
+        next_burst(t0);
+        zero_pad(min(CT, ntok - t0 - CT));
+      }
+    }
+    store_conv_history();
+    zero_tail();
+    const int st = tid_per_site();
+    const int soff_st = (4 * ((st & 63) >> 4) * VD + (st >> 6) * TILE_V + (st & 15)) * (int)sizeof(ST);
+#pragma unroll
+    for (int kt = 0; kt < KD / 16; ++kt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int off = soff_st + (i * VD + 16 * ct) * (int)sizeof(ST);
+          const float x = Sm[2 * kt + ct][i] * D;
+          if constexpr (sizeof(ST) == 4)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), srs, off, kt * KT_BYTES, 2);   // nt
+          else
+            __builtin_amdgcn_raw_buffer_store_b16(f2h(x), srs, off, kt * KT_BYTES, 2);
+        }
+    return;
+  }
+
   // Issue order: the first burst, the weights, then the state. Load counters retire in order, so staging the
   // burst (and the weights' copy to LDS) waits only for the loads issued before the state's and overlaps the
   // state's latency. Every load here is unconditional (the weight loads of surplus threads repeat the last
@@ -512,53 +829,16 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       } else {
         if (rg == 0) {
           const f32x4_t ob = {rbf(o[0]), rbf(o[1]), rbf(o[2]), rbf(o[3])};
-          *reinterpret_cast<f32x4_t*>(&so_[GATED ? tt : 0][col]) = ob;
+          *reinterpret_cast<f32x4_t*>(&so_[tt][col]) = ob;
         }
       }
     }
 
-    if constexpr (GATED) {
-      // gated RMSNorm of the burst: 32 threads per token, 4 value columns each
-      __syncthreads();
-      const int u = threadIdx.x >> 5;
-      const int cc = (threadIdx.x & 31) * 4;
-      const f32x4_t ob = *reinterpret_cast<const f32x4_t*>(&so_[GATED ? u : 0][cc]);
-      float part = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) part += ob[i] * ob[i];
-      part = sum32_dpp(part);
-      const float r = rsqrtf(part * (1.0f / VD) + p.eps);
-      if (u < nt) {
-        float y[4], z4[4], w4[4];
-        load4_bf16(&sz_[GATED ? u : 0][cc], z4);
-        load4_bf16(&sw_[GATED ? cc : 0], w4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float hb = rbf(ob[i] * r);
-          const float tw = rbf(w4[i] * hb);
-          y[i] = tw * siluf_(z4[i]);
-        }
-        store4_bf16(p.out + (tok0 + t0 + u) * (int64_t)(p.HV * VD) + hv * VD + cc, y);
-      }
-    }
-    if (t0 + CT < ntok) {
-      // the next burst's conv history: this (full) burst's last 3 raw rows
-      if (CONV && threadIdx.x < (CKS - 1) * 48)
-        hist = *reinterpret_cast<const u32x4*>(&rw_[CONV ? CT + threadIdx.x / 48 : 0][(threadIdx.x % 48) * 8]);
-      __syncthreads();   // every read of this burst's LDS is done
-      stage(min(CT, ntok - t0 - CT), false);
-    }
+    if constexpr (GATED) gated_epilogue(t0, nt);
+    if (t0 + CT < ntok) next_burst(t0);
   }
 
-  if (CONV && threadIdx.x < (CKS - 1) * 48) {
-    // new conv history = ext[ntok .. ntok + 2] of ext = [pool; tokens]: raw rows nt .. nt + 2 of the last burst
-    // (the row's last three tokens, or old pool rows when it has fewer); every read of the old rows came first
-    const int nt_last = ntok - (ntok - 1) / CT * CT;
-    const int i = threadIdx.x / 48, sg = threadIdx.x % 48;
-    *reinterpret_cast<u32x4*>(p.conv_pool + (slot * (CKS - 1) + i) * (int64_t)p.conv_C + conv_ch(8 * sg)) =
-        *reinterpret_cast<const u32x4*>(&rw_[CONV ? nt_last + i : 0][8 * sg]);
-  }
-
+  store_conv_history();
   zero_tail();
 
 #pragma unroll
@@ -570,7 +850,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
 }
 
 int check_common(const GdnParams& p, int state_dtype, int n_rows, int K, int V) {
-  if (n_rows < 0 || p.H <= 0 || p.HV <= 0 || p.L < 0 || p.state_rows <= 0) return HSG_ERR_ARG;
+  if (n_rows < 0 || p.H <= 0 || p.HV <= 0 || p.L < 0 || p.state_rows <= 0 || p.mfma_min < 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
   if (!p.qkv || !p.a || !p.b || !p.A_log || !p.dt_bias || !p.state || !p.slots || !p.lens) return HSG_ERR_ARG;
   if (p.offsets == nullptr && p.L <= 0) return HSG_ERR_ARG;
@@ -602,7 +882,8 @@ extern "C" int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_
                                  const void* A_log, const void* dt_bias, void* state, int32_t state_dtype,
                                  int64_t state_rows, const int64_t* slots, const int64_t* lens,
                                  const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
-                                 int32_t K, int32_t V, float scale, void* o, float* sq, void* stream) {
+                                 int32_t K, int32_t V, float scale, void* o, float* sq, int32_t burst_min,
+                                 void* stream) {
   GdnParams p{};
   p.qkv = static_cast<const uint16_t*>(qkv);
   p.qkv_stride = qkv_stride;
@@ -618,6 +899,7 @@ extern "C" int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_
   p.L = L; p.H = H; p.HV = HV; p.scale = scale;
   p.o = static_cast<uint16_t*>(o);
   p.sq = sq;
+  p.mfma_min = burst_min;
   const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
   if (rc <= 0) return rc;
   if (!o) return HSG_ERR_ARG;
@@ -632,7 +914,8 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
                                        const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t L,
                                        int32_t H, int32_t HV, int32_t K, int32_t V, float scale,
                                        const void* z, int64_t z_stride, const void* norm_w, float eps,
-                                       void* out, int32_t skip_rows, int32_t skip_min_len, void* stream) {
+                                       void* out, int32_t skip_rows, int32_t skip_min_len, int32_t burst_min,
+                                       void* stream) {
   GdnParams p{};
   p.qkv = static_cast<const uint16_t*>(qkv);
   p.qkv_stride = qkv_stride;
@@ -653,6 +936,7 @@ extern "C" int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int3
   p.out = static_cast<uint16_t*>(out);
   p.skip_rows = skip_rows;
   p.skip_min_len = skip_min_len;
+  p.mfma_min = burst_min;
   const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
   if (rc <= 0) return rc;
   if (!z || !norm_w || !out || skip_rows < 0 || (skip_rows > 0 && skip_min_len < 1)) return HSG_ERR_ARG;
@@ -667,7 +951,8 @@ extern "C" int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_strid
                                             int64_t state_rows, const int64_t* slots, const int64_t* lens,
                                             const int64_t* offsets, int32_t n_rows, int32_t H, int32_t HV,
                                             int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
-                                            const void* norm_w, float eps, void* out, void* stream) {
+                                            const void* norm_w, float eps, void* out, int32_t burst_min,
+                                            void* stream) {
   GdnParams p{};
   p.qkv = static_cast<const uint16_t*>(proj);
   p.qkv_stride = proj_stride;
@@ -690,6 +975,7 @@ extern "C" int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_strid
   p.conv_pool = static_cast<uint16_t*>(conv_pool);
   p.conv_C = channels;
   if (!offsets) return HSG_ERR_ARG;   // packed rows only
+  p.mfma_min = burst_min;
   const int rc = hsg::check_common(p, state_dtype, n_rows, K, V);
   if (rc <= 0) return rc;
   if (!z || !norm_w || !out || !conv_w || !conv_pool) return HSG_ERR_ARG;

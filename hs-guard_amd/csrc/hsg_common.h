@@ -132,6 +132,13 @@ __device__ __forceinline__ int tid_per_site() {
   return t;
 }
 
+// A loaded value through an empty asm: the load then runs where it stands. Without it the compiler sinks a load
+// whose value only one side of a select uses into a branch, with its own wait, at every such select.
+__device__ __forceinline__ float loaded_here(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp_<0xB1>(x));
   x = fmaxf(x, dpp_<0x4E>(x));

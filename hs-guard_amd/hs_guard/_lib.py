@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhsg.so")
 
 # return codes of include/hsg.h
 HSG_OK, HSG_ERR_ARG, HSG_ERR_ALIGN, HSG_ERR_SHAPE, HSG_ERR_BLAS = 0, -1, -2, -3, -4
+HSG_GDN_BURST_MIN_DEFAULT = 16   # include/hsg.h
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -34,7 +35,7 @@ SIGNATURES = {
         _P, _I32, _I64,                      # state, state_dtype, state_rows
         _P, _P, _P, _I32, _I32,              # slots, lens, offsets, n_rows, L
         _I32, _I32, _I32, _I32, _F,          # H, HV, K, V, scale
-        _P, _P, _P]),                        # o, sq, stream
+        _P, _P, _I32, _P]),                  # o, sq, burst_min, stream
     "hsg_gdn_chunk_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32]),
     "hsg_gdn_chunk_prefill": (ctypes.c_int, [
         _P, _I64, _I32, _I32, _I32,
@@ -57,7 +58,8 @@ SIGNATURES = {
         _P, _I32, _I64,
         _P, _P, _P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F,
-        _P, _I64, _P, _F, _P, _I32, _I32, _P]),   # z, z_stride, norm_w, eps, out, skip_rows, skip_min_len, stream
+        _P, _I64, _P, _F, _P, _I32, _I32, _I32, _P]),   # z, z_stride, norm_w, eps, out, skip_rows, skip_min_len,
+                                                        # burst_min, stream
     "hsg_gdn_conv_slot_step_gated": (ctypes.c_int, [
         _P, _I64, _I32, _I32, _I32,          # proj, proj_stride, q_off, k_off, v_off
         _P, _P, _I32,                        # conv_w, conv_pool, channels
@@ -65,7 +67,7 @@ SIGNATURES = {
         _P, _I32, _I64,                      # state, state_dtype, state_rows
         _P, _P, _P, _I32,                    # slots, lens, offsets, n_rows
         _I32, _I32, _I32, _I32, _F,          # H, HV, K, V, scale
-        _P, _I64, _P, _F, _P, _P]),          # z, z_stride, norm_w, eps, out, stream
+        _P, _I64, _P, _F, _P, _I32, _P]),    # z, z_stride, norm_w, eps, out, burst_min, stream
     "hsg_ring_attention": (ctypes.c_int, [
         _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
         _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from .._lib import check, lib
+from .._lib import HSG_GDN_BURST_MIN_DEFAULT, check, lib
 
 HSG_STATE_F32 = 0
 HSG_STATE_F16 = 1
@@ -149,11 +149,12 @@ def norm_rope(src, var, w1, cos, sin, eps, n, lb, heads, groups, row_stride, hea
 
 
 def gdn_slot_v8(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log, dt_bias, state, slots, lens,
-                bv=32, num_warps=2):
+                bv=32, num_warps=2, burst_min=HSG_GDN_BURST_MIN_DEFAULT):
     """Replaces fused_kernels.py:197-211. packed [N, L, 2*key_dim + value_dim] (conv_silu_update output);
     a, b [N, L, HV]; state [S, HV, K, V] pool (fp32 or fp16) updated in place at rows slots[n] with
     lens[n] > 0. Returns (o [N, L, HV, V] bf16, zeros at padded positions; sq = o.float()**2 fp32).
-    ``bv`` and ``num_warps`` are accepted for signature parity; the HIP kernel has one fixed tiling."""
+    ``bv`` and ``num_warps`` are accepted for signature parity; the HIP kernel has one fixed tiling.
+    ``burst_min``: rows of at least that many tokens run 8 at a time in the chunk form on MFMA (0: none)."""
     n, length, c = packed.shape
     for tensor in (packed, a, b, state):
         _require(tensor.is_contiguous(), "tensors must be contiguous")
@@ -166,12 +167,13 @@ def gdn_slot_v8(packed, key_dim, heads, head_k, value_heads, head_v, a, b, A_log
     rc = lib().hsg_gdn_slot_step(
         _ptr(packed), c, 0, key_dim, 2 * key_dim, _ptr(a), _ptr(b), value_heads, _ptr(A_log), _ptr(dt_bias),
         _ptr(state), _STATE_CODES[state.dtype], state.shape[0], _ptr(slots), _ptr(lens), None, n, length,
-        heads, value_heads, head_k, head_v, head_k ** -0.5, _ptr(o), _ptr(sq), _stream(packed.device))
+        heads, value_heads, head_k, head_v, head_k ** -0.5, _ptr(o), _ptr(sq), int(burst_min), _stream(packed.device))
     check(rc, "hsg_gdn_slot_step")
     return o, sq
 
 
-def gdn_slot_recurrent(q, k, v, a, b, A_log, dt_bias, state, slots, lens, scale=None, bv=8, num_warps=1):
+def gdn_slot_recurrent(q, k, v, a, b, A_log, dt_bias, state, slots, lens, scale=None, bv=8, num_warps=1,
+                       burst_min=HSG_GDN_BURST_MIN_DEFAULT):
     """Replaces gdn_slot_kernel.py:57-73: q, k [N, L, H, K]; v [N, L, HV, V]; returns o [N, L, HV, V]."""
     n, length, h, kd = k.shape
     hv, vd = v.shape[2], v.shape[3]
@@ -185,7 +187,7 @@ def gdn_slot_recurrent(q, k, v, a, b, A_log, dt_bias, state, slots, lens, scale=
     rc = lib().hsg_gdn_slot_step(
         _ptr(qkv), qkv.shape[-1], 0, h * kd, 2 * h * kd, _ptr(a), _ptr(b), hv, _ptr(A_log), _ptr(dt_bias),
         _ptr(state), _STATE_CODES[state.dtype], state.shape[0], _ptr(slots), _ptr(lens), None, n, length,
-        h, hv, kd, vd, scale, _ptr(o), None, _stream(v.device))
+        h, hv, kd, vd, scale, _ptr(o), None, int(burst_min), _stream(v.device))
     check(rc, "hsg_gdn_slot_step")
     return o
 

@@ -25,7 +25,7 @@ import numpy as np
 import torch
 
 from .. import _hostpack
-from .._lib import HSG_ERR_SHAPE, check, lib
+from .._lib import HSG_ERR_SHAPE, HSG_GDN_BURST_MIN_DEFAULT, check, lib
 from ..model import ROLES, GuardModel
 from .gemm_plan import WORKSPACE_BYTES as GEMM_WORKSPACE_BYTES
 from .gemm_plan import GemmPlans
@@ -183,7 +183,8 @@ class SlotStreamEngine(PreparedWeights):
     slot of padding rows)."""
 
     def __init__(self, model: GuardModel, max_slots, state_dtype="float32", use_graphs=True, roles=ROLES,
-                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=16, fuse_conv=True):
+                 session_buckets=None, max_tick_tokens=64, chunk_min_tokens=16, fuse_conv=True,
+                 gdn_burst_min=HSG_GDN_BURST_MIN_DEFAULT):
         if not isinstance(max_slots, int) or max_slots < 1:
             raise ValueError("max_slots must be a positive integer")
         if state_dtype not in STATE_DTYPES:
@@ -198,6 +199,11 @@ class SlotStreamEngine(PreparedWeights):
         # 0 keeps every row on the slot step. In a mixed tick the few long rows do not repay the chunk path's
         # extra launches (conv, prep, order, state, gate per layer), so those stay with the slot step.
         self.chunk_min_tokens = chunk_min_tokens
+        # slot-step rows of at least gdn_burst_min tokens run 8 tokens at a time in the chunk form on MFMA inside
+        # the slot-step kernel (no extra launch); 0 runs every row token by token
+        if gdn_burst_min < 0:
+            raise ValueError("gdn_burst_min must be >= 0")
+        self.gdn_burst_min = int(gdn_burst_min)
         lib()  # fail loudly here if the HIP library is missing
         cfg = model.config
         # the GDN layers' causal conv runs inside the slot step (hsg_gdn_conv_slot_step_gated) when every value
@@ -384,7 +390,8 @@ class SlotStreamEngine(PreparedWeights):
                         base + 2 * (C + cfg.value_dim), self.gdn_in, Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(),
                         self.rec[idx].data_ptr(), _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(),
                         offsets.data_ptr(), nb, nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in,
-                        Lw["norm_w"].data_ptr(), eps, out.data_ptr(), st), "hsg_gdn_conv_slot_step_gated")
+                        Lw["norm_w"].data_ptr(), eps, out.data_ptr(), self.gdn_burst_min, st),
+                          "hsg_gdn_conv_slot_step_gated")
                 else:
                     conv = self._view("conv", tb, C)
                     check(L.hsg_conv_silu_update(proj.data_ptr(), self.gdn_in, self.conv[idx].data_ptr(), S,
@@ -397,7 +404,8 @@ class SlotStreamEngine(PreparedWeights):
                         Lw["A_log"].data_ptr(), Lw["dt_bias"].data_ptr(), self.rec[idx].data_ptr(),
                         _STATE_CODE[self.state_dtype], S, slots.data_ptr(), lens.data_ptr(), offsets.data_ptr(), nb,
                         0, nh, hv, kd, vd, kd ** -0.5, base + 2 * C, self.gdn_in, Lw["norm_w"].data_ptr(), eps,
-                        out.data_ptr(), R, max(self.chunk_min_tokens, 1), st), "hsg_gdn_slot_step_gated")
+                        out.data_ptr(), R, max(self.chunk_min_tokens, 1), self.gdn_burst_min, st),
+                          "hsg_gdn_slot_step_gated")
                     if R:
                         check(L.hsg_gdn_chunk_prefill_gated(
                             conv.data_ptr(), C, 0, cfg.key_dim, 2 * cfg.key_dim,

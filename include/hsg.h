@@ -52,14 +52,21 @@ const char* hsg_error_string(int code);
  *   A_log, dt_bias [HV] bf16.
  *   state    [state_rows, HV, K, V] fp32 (state_dtype HSG_STATE_F32) or fp16; V contiguous.
  *   o        [tokens, HV, V] bf16;  sq [tokens, HV, V] fp32 = bf16(o)^2 (sq may be NULL).
+ *   burst_min: rows of at least this many tokens (>= 1) run their tokens 8 at a time in the WY/UT chunk form on
+ *            fp32 MFMA (the token recurrence unrolled over the burst; equal in exact arithmetic, within fp32
+ *            rounding of it); shorter rows, and every row when burst_min is 0, run token by token.
  * Supported: K == V == 128, HV % H == 0.
  */
+/* The engine's burst_min: a row of 8-15 tokens would take two bursts (the second partial) for no gain in a mixed
+ * tick, whose time the state reads set; from 16 tokens on the bursts shorten the row (a lone 64-token row 70.4 ->
+ * 58.0 us on MI355X). */
+#define HSG_GDN_BURST_MIN_DEFAULT 16
 int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off, int32_t v_off,
                       const void* a, const void* b, int64_t ab_stride, const void* A_log,
                       const void* dt_bias, void* state, int32_t state_dtype, int64_t state_rows,
                       const int64_t* slots, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
                       int32_t L, int32_t H, int32_t HV, int32_t K, int32_t V, float scale, void* o,
-                      float* sq, void* stream);
+                      float* sq, int32_t burst_min, void* stream);
 
 /*
  * The same step with Qwen3.5's gated RMSNorm fused into the epilogue.
@@ -68,7 +75,8 @@ int hsg_gdn_slot_step(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_
  *   out[tok, hv*V + c] = bf16( bf16(w[c] * bf16(o*rsqrt(mean(bf16(o)^2)+eps))) * silu(z[tok, hv*V + c]) )
  *   z [tokens, z_stride] bf16, norm_w [V] bf16, out [tokens, HV*V] bf16.
  * Packed layout: rows n < skip_rows with lens[n] >= skip_min_len (>= 1) are left alone (no output, state
- * untouched), for hsg_gdn_chunk_prefill_gated to take; skip_rows 0 processes every row.
+ * untouched), for hsg_gdn_chunk_prefill_gated to take; skip_rows 0 processes every row. burst_min as
+ * hsg_gdn_slot_step.
  */
 int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, int32_t k_off,
                             int32_t v_off, const void* a, const void* b, int64_t ab_stride,
@@ -77,7 +85,7 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
                             const int64_t* offsets, int32_t n_rows, int32_t L, int32_t H, int32_t HV,
                             int32_t K, int32_t V, float scale, const void* z, int64_t z_stride,
                             const void* norm_w, float eps, void* out, int32_t skip_rows, int32_t skip_min_len,
-                            void* stream);
+                            int32_t burst_min, void* stream);
 
 /*
  * hsg_gdn_slot_step_gated with the causal conv + SiLU of its inputs fused in (conv_silu_update,
@@ -87,9 +95,9 @@ int hsg_gdn_slot_step_gated(const void* qkv, int64_t qkv_stride, int32_t q_off, 
  * q_off, k_off, v_off; conv_w [channels, 4] bf16; conv_pool [state_rows, 3, channels] bf16, the per-slot conv
  * history, updated in place at slots[n] for rows with lens[n] > 0. Each (row, head) workgroup convolves its own
  * q, k, v channels from the pool and the raw rows, with the conv kernel's arithmetic, so outputs, state and pool
- * equal hsg_conv_silu_update followed by hsg_gdn_slot_step_gated bit for bit. Packed rows only (offsets
- * required), HV == H (every q / k channel belongs to one workgroup), no chunk-routing filter. out must not
- * alias proj, z or conv_pool; rows must name distinct slots.
+ * equal hsg_conv_silu_update followed by hsg_gdn_slot_step_gated bit for bit (with the same burst_min). Packed
+ * rows only (offsets required), HV == H (every q / k channel belongs to one workgroup), no chunk-routing filter.
+ * out must not alias proj, z or conv_pool; rows must name distinct slots. burst_min as hsg_gdn_slot_step.
  */
 int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_stride, int32_t q_off, int32_t k_off, int32_t v_off,
                                  const void* conv_w, void* conv_pool, int32_t channels, const void* a, const void* b,
@@ -97,7 +105,7 @@ int hsg_gdn_conv_slot_step_gated(const void* proj, int64_t proj_stride, int32_t 
                                  int32_t state_dtype, int64_t state_rows, const int64_t* slots, const int64_t* lens,
                                  const int64_t* offsets, int32_t n_rows, int32_t H, int32_t HV, int32_t K, int32_t V,
                                  float scale, const void* z, int64_t z_stride, const void* norm_w, float eps,
-                                 void* out, void* stream);
+                                 void* out, int32_t burst_min, void* stream);
 
 /*
  * Chunked gated-delta-rule prefill: the same recurrence and contract as hsg_gdn_slot_step, evaluated

@@ -30,6 +30,16 @@ def test_library_exports_every_declared_symbol():
     assert set(SIGNATURES) == set(_declared()), "ctypes signatures out of sync with include/hsg.h"
 
 
+def test_constants_match_the_header():
+    """The Python mirror of the header's constants (return codes, the engine's GDN burst threshold)."""
+    from hs_guard import _lib
+    text = open(HEADER).read()
+    assert int(re.search(r"#define HSG_GDN_BURST_MIN_DEFAULT (\d+)", text).group(1)) == _lib.HSG_GDN_BURST_MIN_DEFAULT
+    for name in ("HSG_OK", "HSG_ERR_ARG", "HSG_ERR_ALIGN", "HSG_ERR_SHAPE", "HSG_ERR_BLAS"):
+        m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
+        assert m is not None and int(m.group(1)) == getattr(_lib, name), name
+
+
 def test_version_and_error_strings():
     from hs_guard._lib import lib
     assert lib().hsg_version() >= 100
@@ -42,11 +52,14 @@ def test_argument_errors_are_rejected_before_launch():
     L = lib()
     # n_rows > 0 with null pointers -> HSG_ERR_ARG; unsupported head size -> HSG_ERR_SHAPE
     rc = L.hsg_gdn_slot_step(None, 6144, 0, 2048, 4096, None, None, 16, None, None, None, 0, 17, None, None, None,
-                             4, 1, 16, 16, 128, 128, 1.0, None, None, None)
+                             4, 1, 16, 16, 128, 128, 1.0, None, None, 8, None)
     assert rc == -1
     rc = L.hsg_gdn_slot_step(8, 6144, 0, 2048, 4096, 8, 8, 16, 8, 8, 16, 0, 17, 8, 8, None, 4, 1, 16, 16, 64, 128,
-                             1.0, 8, None, None)
+                             1.0, 8, None, 8, None)
     assert rc == -3
+    rc = L.hsg_gdn_slot_step(8, 6144, 0, 2048, 4096, 8, 8, 16, 8, 8, 16, 0, 17, 8, 8, None, 4, 1, 16, 16, 128, 128,
+                             1.0, 8, None, -1, None)
+    assert rc == -1          # a negative burst threshold
     rc = L.hsg_ring_attention(16, 0, 256, 0, 0, 16, 16, 5, 512, 16, 0, 256, 0, 16, 0, 256, 0, None, 0, 0, 0, 0, 0,
                               8, 8, 8, 8, None, 2, 1, 4, 4, 128, 1.0, 0, 0, 16, 0, 0, 0, 0, None)
     assert rc == -3

@@ -227,7 +227,7 @@ def test_tick_split_between_slot_step_and_chunk():
         assert lib().hsg_gdn_slot_step_gated(base, stride, 0, H * K, 2 * H * K, a_ptr, b_ptr, stride, A_d.data_ptr(),
                                              dt_d.data_ptr(), state.data_ptr(), 0, 8, sl.data_ptr(), ln.data_ptr(),
                                              of.data_ptr(), 7, 0, H, HV, K, K, K ** -0.5, z_ptr, stride,
-                                             w_d.data_ptr(), 1e-6, out.data_ptr(), skip_rows, THR, st) == 0
+                                             w_d.data_ptr(), 1e-6, out.data_ptr(), skip_rows, THR, 8, st) == 0
 
     s_ref, o_ref = state0.to(dev), torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
     slot_step(s_ref, o_ref, 0)

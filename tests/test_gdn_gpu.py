@@ -69,8 +69,10 @@ def test_config1_64_steps(state_dtype):
     assert torch.count_nonzero(state[16]).item() == 0  # scratch slot untouched
 
 
-def test_multi_token_and_padding():
-    """L=7 tick with lens [7, 3, 0, 1, 5]; slots permuted; a row with lens 0 leaves its slot bit-exact."""
+@pytest.mark.parametrize("burst_min", [8, 1])
+def test_multi_token_and_padding(burst_min):
+    """L=7 tick with lens [7, 3, 0, 1, 5]; slots permuted; a row with lens 0 leaves its slot bit-exact. burst_min 1:
+    every row through the 8-token MFMA burst path (padded layout, zeros past lens, two value heads per key head)."""
     from hs_guard.engine.kernels import gdn_slot_v8
     print("[gdn] multi-token padded tick", flush=True)
     gen = torch.Generator().manual_seed(1)
@@ -88,9 +90,11 @@ def test_multi_token_and_padding():
     dev = torch.device("cuda:0")
     state = state0.to(dev)
     o, sq = gdn_slot_v8(packed.to(dev), H * K, H, K, HV, K, a.to(dev), b.to(dev), A_log.to(dev), dt.to(dev),
-                        state, slots.to(dev), lens.to(dev))
+                        state, slots.to(dev), lens.to(dev), burst_min=burst_min)
     o_ref, _, st_ref = ogdn.gdn_slot_step(_np(packed), H * K, H, K, HV, K, _np(a), _np(b), _np(A_log), _np(dt),
                                           _np(state0), slots.numpy(), lens.numpy())
+    ob = _np(o).astype(np.float64)
+    np.testing.assert_array_equal(_np(sq), (ob * ob).astype(np.float32))
     bad, worst = _out_close(_np(o), o_ref)
     assert bad == 0, f"{bad} outputs off (max diff {worst})"
     for n in range(N):
@@ -104,7 +108,7 @@ def test_multi_token_and_padding():
             np.testing.assert_array_equal(got[s], _np(state0[s]))
 
 
-def _check_packed_gated(lens_list, A_log_vals, dt_scale, seed, state_scale=0.02):
+def _check_packed_gated(lens_list, A_log_vals, dt_scale, seed, state_scale=0.02, burst_min=8):
     """Packed rows (offsets) with the fused gated RMSNorm epilogue, z read from a strided projection; gated
     outputs and states against the oracle, rows of zero length bit-exact."""
     from hs_guard._lib import lib
@@ -135,7 +139,7 @@ def _check_packed_gated(lens_list, A_log_vals, dt_scale, seed, state_scale=0.02)
         proj_d.data_ptr(), stride, 0, H * K, 2 * H * K, ab_d[:, HV:].data_ptr(), ab_d.data_ptr(), 2 * HV,
         A_d.data_ptr(), dt_d.data_ptr(), state.data_ptr(), 0, S, slots_d.data_ptr(), lens_d.data_ptr(),
         off_d.data_ptr(), N, 0, H, HV, K, K, K ** -0.5, proj_d[:, C:].data_ptr(), stride, w_d.data_ptr(), 1e-6,
-        out.data_ptr(), 0, 0, torch.cuda.current_stream().cuda_stream)
+        out.data_ptr(), 0, 0, burst_min, torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     # oracle in padded form
     L = int(lens.max())
@@ -180,22 +184,27 @@ def test_packed_gated_matches_oracle():
     _check_packed_gated([3, 1, 0, 4], [0.0], 0.5, seed=2)
 
 
+@pytest.mark.parametrize("burst_min", [0, 8, 1], ids=["tokens", "bursts8", "bursts_all"])
 @pytest.mark.parametrize("case", ["bursts", "fast_decay", "zero_decay"])
-def test_packed_gated_long_rows_and_decay(case):
+def test_packed_gated_long_rows_and_decay(case, burst_min):
     """Rows spanning several 8-token bursts (full and partial), and heads whose decay is fast enough that the
     kernel's deferred decay factor is folded back into the state mid-row (exp(A_log) = 20: exp(g) ~ 1e-6 per
-    token, below 2^-40 after two tokens) or underflows to exactly zero in fp32 (exp(A_log) = 403)."""
-    print(f"[gdn] packed + gated, {case}", flush=True)
+    token, below 2^-40 after two tokens) or underflows to exactly zero in fp32 (exp(A_log) = 403). burst_min: the
+    token path for every row (0), the MFMA burst path for the rows of 8 or more tokens (8), or for every row with
+    partial bursts padded (1)."""
+    print(f"[gdn] packed + gated, {case}, burst_min {burst_min}", flush=True)
     lens = [64, 17, 1, 9, 0, 33, 8, 2]
     A_log = {"bursts": [0.0, -1.0], "fast_decay": [0.0, 3.0, -2.0, 3.0], "zero_decay": [6.0, 0.0, 3.0, 6.0]}[case]
-    _check_packed_gated(lens, A_log, 1.0, seed=11, state_scale=0.05)
+    _check_packed_gated(lens, A_log, 1.0, seed=11, state_scale=0.05, burst_min=burst_min)
 
 
+@pytest.mark.parametrize("burst_min", [0, 8])
 @pytest.mark.parametrize("state_code", [0, 1])
-def test_conv_fused_step_equals_conv_then_step(state_code):
+def test_conv_fused_step_equals_conv_then_step(state_code, burst_min):
     """hsg_gdn_conv_slot_step_gated (conv + SiLU inside the slot step) == hsg_conv_silu_update followed by
     hsg_gdn_slot_step_gated, bit for bit on the gated outputs, the state and the conv history pool: rows of 0 to 64
-    tokens (one to eight 8-token bursts, rows shorter than the 3-token history), HV == H."""
+    tokens (one to eight 8-token bursts, rows shorter than the 3-token history), HV == H; on the token path and with
+    the rows of 8 or more tokens on the MFMA burst path."""
     from hs_guard._lib import lib
     L = lib()
     print(f"[gdn] conv fused, state code {state_code}", flush=True)
@@ -235,14 +244,15 @@ def test_conv_fused_step_equals_conv_then_step(state_code):
     assert L.hsg_gdn_slot_step_gated(conv.data_ptr(), C, 0, H * K, 2 * H * K, a_ptr, b_ptr, stride, Ad.data_ptr(),
                                      dtd.data_ptr(), state_a.data_ptr(), state_code, S, sl.data_ptr(), ln.data_ptr(),
                                      of.data_ptr(), N, 0, H, HV, K, K, K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6,
-                                     out_a.data_ptr(), 0, 0, st) == 0
+                                     out_a.data_ptr(), 0, 0, burst_min, st) == 0
     # fused
     pool_b, state_b = pool0.to(dev), state0.to(dev)
     out_b = torch.zeros(T, HV * K, dtype=torch.bfloat16, device=dev)
     assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
                                           a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
                                           state_code, S, sl.data_ptr(), ln.data_ptr(), of.data_ptr(), N, H, HV, K, K,
-                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == 0
+                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), burst_min,
+                                          st) == 0
     torch.cuda.synchronize()
     assert torch.equal(out_a, out_b)
     assert torch.equal(state_a, state_b)
@@ -252,8 +262,10 @@ def test_conv_fused_step_equals_conv_then_step(state_code):
     assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
                                           a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
                                           state_code, S, sl.data_ptr(), ln.data_ptr(), None, N, H, HV, K, K,
-                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == -1
+                                          K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), burst_min,
+                                          st) == -1
     assert L.hsg_gdn_conv_slot_step_gated(base, stride, 0, H * K, 2 * H * K, wd.data_ptr(), pool_b.data_ptr(), C,
                                           a_ptr, b_ptr, stride, Ad.data_ptr(), dtd.data_ptr(), state_b.data_ptr(),
                                           state_code, S, sl.data_ptr(), ln.data_ptr(), of.data_ptr(), N, H // 2, HV, K,
-                                          K, K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), st) == -3
+                                          K, K ** -0.5, z_ptr, stride, nwd.data_ptr(), 1e-6, out_b.data_ptr(), burst_min,
+                                          st) == -3
