@@ -55,8 +55,7 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
 
     Launch i works on state buffer and conv pool i mod 3, so no launch reads what the previous one wrote: in a step
     each GDN layer's state was last touched a whole step earlier, and one buffer reused back to back would be
-    read partly from the 256 MB Infinity Cache (352 x 1, fp32 state, on MI355X: 119 us with one buffer, 155 us
-    rotating three)."""
+    read partly from the 256 MB Infinity Cache, faster than any step sees it."""
     from hs_guard._lib import HSG_GDN_BURST_MIN_DEFAULT
     dev = torch.device("cuda:0")
     H = HV = 16
@@ -109,11 +108,12 @@ def gdn_roofline(torch, lib, rows=352, iters=100, state_dtype=0):
             "achieved_gbs": round(gbs, 1)}
 
 
-def lone_row_rate(torch, lib, tokens=64, iters=20, burst_min=8):
+def lone_row_rate(torch, lib, tokens=64, iters=20, burst_min=16):
     """The conv + gated GDN slot step (hsg_gdn_conv_slot_step_gated) on one row of ``tokens`` tokens, 16 heads x
     128, fp32 state, every other row of an 8-row grid empty: a mixed tick's critical path when its longest row
     runs on the slot step (the chip otherwise idle). HIP events on the launch stream around ``iters`` launches.
-    ``burst_min`` as the entry point's (0: token by token; 8: the row in bursts of 8 tokens on MFMA)."""
+    ``burst_min`` as the entry point's (0: token by token; 16, the engine's: this row in bursts of 8 tokens on
+    MFMA)."""
     dev = torch.device("cuda:0")
     N, H, K = 8, 16, 128
     C = 3 * H * K

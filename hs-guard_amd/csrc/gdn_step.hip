@@ -12,9 +12,10 @@
 // 128-byte row segment, so every load instruction reads 8 full 128-byte lines. The k.S and q.S
 // reductions over the 128 key rows are in-lane (16 rows) plus a 3-step butterfly over rg (lane xor 8,
 // 16, 32) done with a DPP row rotate and gfx950's permlane16/32 swaps, not the LDS crossbar. The state is
-// read with ordinary loads and written back with nontemporal stores (it is touched once per tick, so the
-// write should not displace cached weights and activations); measured on MI355X this pairing streams
-// faster than nontemporal loads (6.0 vs 5.4 TB/s at 352 x 16).
+// read with nontemporal loads and written back with nontemporal stores (it is touched once per tick). In a
+// step each layer's state was last touched a whole step earlier, so its reads miss the 256 MB Infinity Cache;
+// measured on MI355X with three state buffers in rotation, 352 x 1: nontemporal loads 142.9 us, ordinary loads
+// 159.1 us (ordinary loads win only when one buffer is reused back to back, 129 vs 142 us, which no step does).
 // Per-token work is cut to the three 16 x 4 products a token needs (S^T k, the rank-1 update, S^T q):
 //   * the registers hold St with S = D St, so exp(g) scales the scalar D, not 64 registers (D is folded
 //     back before 1 / D could overflow and when the state is stored);
@@ -74,7 +75,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 template <>
 struct StateIO<float> {
   static __device__ __forceinline__ void load(const float* p, float* v) {
-    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(p);
+    const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
     v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
   }
   static __device__ __forceinline__ void store(float* p, const float* v) {
@@ -86,7 +87,7 @@ struct StateIO<float> {
 template <>
 struct StateIO<uint16_t> {  // fp16 storage, fp32 arithmetic
   static __device__ __forceinline__ void load(const uint16_t* p, float* v) {
-    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(p);
+    const u32x2_t w = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
     v[0] = h2f((uint16_t)(w[0] & 0xffffu)); v[1] = h2f((uint16_t)(w[0] >> 16));
     v[2] = h2f((uint16_t)(w[1] & 0xffffu)); v[3] = h2f((uint16_t)(w[1] >> 16));
   }
@@ -522,9 +523,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
         for (int i = 0; i < 4; ++i) {
           const int off = soff + (i * VD + 16 * ct) * (int)sizeof(ST);
           if constexpr (sizeof(ST) == 4)
-            Sm[2 * kt + ct][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, kt * KT_BYTES, 0));
+            Sm[2 * kt + ct][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, kt * KT_BYTES, 2));
           else
-            Sm[2 * kt + ct][i] = h2f(__builtin_amdgcn_raw_buffer_load_b16(srs, off, kt * KT_BYTES, 0));
+            Sm[2 * kt + ct][i] = h2f(__builtin_amdgcn_raw_buffer_load_b16(srs, off, kt * KT_BYTES, 2));
         }
     if (CONV && threadIdx.x < CH3 / 8) {
 #pragma unroll
