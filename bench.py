@@ -158,9 +158,9 @@ def gdn_tick_rate(torch, lib, rows=352, iters=30, seed=5, burst_mins=(0, 8)):
     tick) on a config-5 tick: 352 rows, chunk lengths 1 (p 0.8), 2-16 (p 0.15), 17-64 (p 0.05), packed longest
     first, 16 heads x 128, fp32 state, for each burst threshold in ``burst_mins``. HIP events on the launch stream
     around ``iters`` launches. Algorithmic bytes: per (row, head) the state and the conv history read and written,
-    per (token, head) q, k, v, z in, the output out and a, b, as the roofline leg counts them. Slots are a random
-    permutation (as the engine's schedule assigns them) and launch i works on state buffer and conv pool i mod 3,
-    as in the roofline leg."""
+    per (token, head) q, k, v, z in, the output out and a, b, as the roofline leg counts them. Row r is slot r's
+    request, the rows packed as the engine packs a step's requests in slot order (longest first, ties in slot
+    order), and launch i works on state buffer and conv pool i mod 3, as in the roofline leg."""
     import numpy as np
     dev = torch.device("cuda:0")
     H = HV = 16
@@ -169,8 +169,9 @@ def gdn_tick_rate(torch, lib, rows=352, iters=30, seed=5, burst_mins=(0, 8)):
     stride = C + HV * V + 2 * HV
     rng = np.random.default_rng(seed)
     u = rng.random(rows)
-    lens_h = np.where(u < 0.8, 1, np.where(u < 0.95, rng.integers(2, 17, rows), rng.integers(17, 65, rows)))
-    lens_h = np.sort(lens_h)[::-1].copy()
+    lens_slot = np.where(u < 0.8, 1, np.where(u < 0.95, rng.integers(2, 17, rows), rng.integers(17, 65, rows)))
+    order = np.argsort(-lens_slot, kind="stable")   # the engine's packing: longest first, ties in slot order
+    lens_h = lens_slot[order].copy()
     T = int(lens_h.sum())
     gen = torch.Generator(device=dev).manual_seed(seed)
     states = [torch.randn(rows + 1, HV, K, V, generator=gen, device=dev) * 0.02 for _ in range(3)]
@@ -180,7 +181,7 @@ def gdn_tick_rate(torch, lib, rows=352, iters=30, seed=5, burst_mins=(0, 8)):
     out = torch.empty(T, HV * V, dtype=torch.bfloat16, device=dev)
     A = torch.zeros(HV, dtype=torch.bfloat16, device=dev)
     w = torch.ones(V, dtype=torch.bfloat16, device=dev)
-    slots = torch.from_numpy(rng.permutation(rows)).to(dev)
+    slots = torch.from_numpy(order).to(dev)
     lens = torch.from_numpy(lens_h).to(dev)
     offs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens_h)[:-1]])).to(dev)
     stream = torch.cuda.current_stream(dev)
@@ -618,7 +619,8 @@ def main():
     ap.add_argument("--ring-only", action="store_true",
                     help="only the 352 x 1-token split-K ring decode measurement (profiled under rocprofv3)")
     ap.add_argument("--lone-row-only", action="store_true",
-                    help="only the GDN slot step on one 64-token row (profiled under rocprofv3 --pmc)")
+                    help="only the GDN slot step on one 64-token row at --gdn-burst-min (profiled under rocprofv3 "
+                         "--pmc)")
     ap.add_argument("--mixed-only", action="store_true",
                     help="only the prefill and the mixed steps (no kernel legs, decode legs, context sweep or CPU "
                          "baseline): the command whose kernel statistics give the per-step kernel breakdown")
@@ -649,9 +651,9 @@ def main():
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(0)}")
     state_code = 0 if args.state_dtype == "float32" else 1
-    if args.lone_row_only:
-        print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib()),
-                          "gdn_lone_row_64_token_path": lone_row_rate(torch, lib(), burst_min=0)}), flush=True)
+    if args.lone_row_only:   # one threshold per run, so counters of one run describe one path
+        bm = HSG_GDN_BURST_MIN_DEFAULT if args.gdn_burst_min is None else args.gdn_burst_min
+        print(json.dumps({"gdn_lone_row_64": lone_row_rate(torch, lib(), burst_min=bm)}), flush=True)
         return
     if args.gdn_tick_only:
         print(json.dumps({"gdn_tick": gdn_tick_rate(torch, lib(), rows=args.slots, burst_mins=(0, 8, 16, 32)),
