@@ -99,7 +99,11 @@ int heuristic(DeviceCtx& c, Plan& p, size_t limit, int count, std::vector<hipbla
   return HSG_OK;
 }
 
-// the plan of a problem with the given solution (-1: first heuristic candidate), cached per device
+// heuristic candidates examined for solution -1
+constexpr int kHeuristicCandidates = 16;
+
+// the plan of a problem with the given solution (-1: the first heuristic candidate whose workspace fits `limit`),
+// cached per device
 int get_plan(DeviceCtx& c, int32_t M, int32_t N, int32_t K, int64_t lda, int64_t ldw, int64_t ldd, int32_t index,
              size_t limit, Plan** out) {
   const PlanKey key{M, N, K, lda, ldw, ldd, index};
@@ -112,14 +116,23 @@ int get_plan(DeviceCtx& c, int32_t M, int32_t N, int32_t K, int64_t lda, int64_t
   int rc = describe(M, N, K, lda, ldw, ldd, p);
   if (rc != HSG_OK) return rc;
   if (index < 0) {
+    // the first candidate, in the heuristic's order, whose workspace fits: the hipBLASLt PyTorch ships returns
+    // candidates beyond the preference's workspace limit (61 MiB against 32 at M = 11264, N = 7168, K = 1024)
     std::vector<hipblasLtMatmulHeuristicResult_t> res;
-    rc = heuristic(c, p, limit, 1, res);
+    rc = heuristic(c, p, limit, kHeuristicCandidates, res);
     if (rc != HSG_OK) {
       destroy_plan(p);
       return rc;
     }
-    p.algo = res[0].algo;
-    p.workspace = res[0].workspaceSize;
+    size_t pick = res.size();
+    for (size_t i = 0; i < res.size() && pick == res.size(); ++i)
+      if (res[i].workspaceSize <= limit) pick = i;
+    if (pick == res.size()) {
+      destroy_plan(p);
+      return HSG_ERR_SHAPE;   // no candidate fits the caller's workspace
+    }
+    p.algo = res[pick].algo;
+    p.workspace = res[pick].workspaceSize;
   } else {
     std::vector<int> idx{index};
     std::vector<hipblasLtMatmulHeuristicResult_t> res;
@@ -185,7 +198,7 @@ extern "C" int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* ind
   int n = 0;
   for (auto& r : res) {
     const int idx = hipblaslt_ext::getIndexFromAlgo(r.algo);
-    if (idx < 0) continue;
+    if (idx < 0 || r.workspaceSize > workspace_limit) continue;   // the library does not always apply the limit
     indices[n] = idx;
     if (workspace) workspace[n] = r.workspaceSize;
     ++n;

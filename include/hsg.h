@@ -386,8 +386,9 @@ int hsg_ring_pos_update(int64_t* ring_pos, int64_t ring_rows, int32_t window, co
  * Projection GEMM on hipBLASLt with a fixed solution: D[M, N] = A[M, K] . W[N, K]^T, bf16 row-major with row
  * strides lda, ldw, ldd (elements), fp32 accumulation. Replaces the backbone's nn.Linear products
  * (src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89). algo_index: a hipBLASLt solution index (from a
- * committed plan table, so every process runs the same accumulation order), or -1 for hipBLASLt's first
- * heuristic candidate (torch.mm's choice). workspace: device memory for solutions that need it. Returns
+ * committed plan table, so every process runs the same accumulation order), or -1 for the first of hipBLASLt's
+ * heuristic candidates (16 examined, in its order) whose workspace fits workspace_bytes (torch.mm's choice when
+ * that is the first). workspace: device memory for solutions that need it. Returns
  * HSG_ERR_SHAPE when the solution does not exist in this hipBLASLt, does not support the problem or needs more
  * than workspace_bytes, HSG_ERR_BLAS when hipBLASLt fails. The first call on a device creates its hipBLASLt
  * handle (make it outside graph capture); later calls are capturable.
@@ -397,8 +398,8 @@ int hsg_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
 
 /*
  * Up to max_count hipBLASLt heuristic candidates for the dense problem (M, N, K) of hsg_gemm_bf16, in hipBLASLt's
- * order, as solution indices (and each one's workspace bytes, when `workspace` is non-NULL), limited to
- * workspace_limit bytes of workspace. Returns the count, or -1. For generating a plan table.
+ * order, as solution indices (and each one's workspace bytes, when `workspace` is non-NULL), those needing more
+ * than workspace_limit bytes of workspace left out. Returns the count, or -1. For generating a plan table.
  */
 int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_t* workspace, int32_t max_count,
                         size_t workspace_limit);

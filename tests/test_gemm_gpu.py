@@ -53,6 +53,29 @@ def test_heuristic_solution_matches_fp32_and_repeats(M):
         assert _rel(out, A, W) <= 2.0 ** -7, (M, N, K)
 
 
+@pytest.mark.parametrize("ws_bytes", [32 << 20, 0], ids=["32MiB", "none"])
+def test_heuristic_solution_fits_the_workspace(ws_bytes):
+    """Solution -1 at a shape whose first heuristic candidate needs more workspace than the caller has (the running
+    hipBLASLt returns a 61 MiB candidate first at M = 11264, N = 7168, K = 1024 whatever the preference's limit):
+    the first candidate that fits runs, as a 176-slot engine's 64-token prefill tick needs. The candidates the
+    plan table is built from respect the limit too."""
+    from hs_guard._lib import lib
+    print(f"[gemm] heuristic within {ws_bytes} bytes of workspace at M=11264", flush=True)
+    M, N, K = 11264, 7168, 1024
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device="cuda")
+    A, W = _inputs(M, N, K)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    rc = lib().hsg_gemm_bf16(A.data_ptr(), K, W.data_ptr(), K, out.data_ptr(), N, M, N, K, -1, ws.data_ptr(), ws_bytes,
+                             torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, rc
+    assert _rel(out, A, W) <= 2.0 ** -7
+    idx = (ctypes.c_int32 * 16)()
+    wsz = (ctypes.c_size_t * 16)()
+    n = lib().hsg_gemm_candidates(M, N, K, idx, wsz, 16, ws_bytes)
+    assert n > 0 and all(wsz[i] <= ws_bytes for i in range(n))
+
+
 def test_candidates_and_rejections():
     from hs_guard._lib import lib
     from hs_guard.engine.gemm_plan import WORKSPACE_BYTES
