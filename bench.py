@@ -243,7 +243,9 @@ def ring_decode_rate(torch, rows=352, iters=50):
     decode shape, HIP events on the launch stream: config 2's ring fills (uniform in [1, 512]) scaled to 352 rows,
     and full rings (the steady state of a live session). Algorithmic bytes: the visible keys and values (n 256 dims x 2 B x 2),
     their positions (8 B each), q, gate and out (3 x 16 heads x 512 B), the new key and value read and
-    written to the ring (4 kv heads x 512 B x 4)."""
+    written to the ring (4 kv heads x 512 B x 4). Launch i reads ring set i mod 3 (the rings of every row, 740 MB a
+    set), so no launch reads rings the previous one just read from the 256 MB Infinity Cache: in a step each
+    attention layer's rings were last read a whole step earlier."""
     from hs_guard.engine.kernels import ring_attention_v8
     from hs_guard.synthetic import ring_decode_inputs
     out = {}
@@ -259,18 +261,20 @@ def ring_decode_rate(torch, rows=352, iters=50):
                 rp[i, cols % W] = cols
             r["ring_pos"] = rp
         d = {k: v.to("cuda:0") for k, v in r.items() if torch.is_tensor(v)}
+        rings = [(d["ring_k"], d["ring_v"])] + [(d["ring_k"].clone(), d["ring_v"].clone()) for _ in range(2)]
         stream = torch.cuda.current_stream()
 
-        def run():
-            ring_attention_v8(d["q"], d["ring_k"], d["ring_v"], d["new_k"], d["value"], d["gate"], d["ring_pos"],
+        def run(i):
+            rk, rv = rings[i % 3]
+            ring_attention_v8(d["q"], rk, rv, d["new_k"], d["value"], d["gate"], d["ring_pos"],
                               d["slots"], d["starts"], d["lens"], 1 / 16, 512, False)
-        for _ in range(5):
-            run()
+        for i in range(6):
+            run(i)
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record(stream)
-        for _ in range(iters):
-            run()
+        for i in range(iters):
+            run(i)
         t1.record(stream)
         torch.cuda.synchronize()
         us = t0.elapsed_time(t1) * 1e3 / iters
@@ -285,7 +289,8 @@ def ring_tick_rate(torch, rows=352, iters=50, seed=5):
     """The tiled ring attention (hsg_ring_attention with min_len 2: the multi-token rows of a tick; the engine gives
     the single-token rows to hsg_ring_decode) on a config-5 mixed tick: 352 rows, chunk lengths 1 (p 0.8), 2-16
     (p 0.15), 17-64 (p 0.05), packed layout, 16 q / 4 kv heads of 256, full 512-column rings, ring write off (the
-    engine's separate ring_write_kernel). HIP events on the launch stream around ``iters`` launches. Algorithmic
+    engine's separate ring_write_kernel). HIP events on the launch stream around ``iters`` launches, launch i on
+    ring set i mod 3 (the multi-token rows' rings, 147 MB, would otherwise stay in the Infinity Cache). Algorithmic
     bytes per multi-token row and kv head: its ring keys and values (512 x 256 x 2 B x 2) and positions (512 x 8 B),
     and per token its new key and value (2 x 512 B), 4 queries and gates in and 4 outputs out (12 x 512 B)."""
     import numpy as np
@@ -321,20 +326,23 @@ def ring_tick_rate(torch, rows=352, iters=50, seed=5):
     base = proj.data_ptr()
     stream = torch.cuda.current_stream(dev)
 
-    def run():
-        rc = L.hsg_ring_attention(q.data_ptr(), 0, hq * D, G * D, D, ring_k.data_ptr(), ring_v.data_ptr(), rows + 1,
+    rings = [(ring_k, ring_v)] + [(ring_k.clone(), ring_v.clone()) for _ in range(2)]
+
+    def run(i):
+        rk, rv = rings[i % 3]
+        rc = L.hsg_ring_attention(q.data_ptr(), 0, hq * D, G * D, D, rk.data_ptr(), rv.data_ptr(), rows + 1,
                                   W, k.data_ptr(), 0, hkv * D, D, base + 2 * (hq * 2 * D + hkv * D), 0, att_in, D,
                                   base, 0, att_in, G * 2 * D, 2 * D, D, ring_pos.data_ptr(), slots.data_ptr(),
                                   starts.data_ptr(), lens.data_ptr(), offs.data_ptr(), rows, 64, hkv, G, D, D ** -0.5,
                                   0, 2, out.data_ptr(), 0, hq * D, G * D, D, stream.cuda_stream)
         assert rc == 0, rc
-    for _ in range(5):
-        run()
+    for i in range(6):
+        run(i)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for _ in range(iters):
-        run()
+    for i in range(iters):
+        run(i)
     t1.record(stream)
     torch.cuda.synchronize()
     us = t0.elapsed_time(t1) * 1e3 / iters
