@@ -117,8 +117,10 @@ def test_benchmark_depth_at_north_star_bar():
     twin = StreamOracle(weights, cfg, slots, gdn="chunk")
     gemm = matched_gemm(eng)
     worst = floor = 0.0
+    cuts = []
     for t, tick in enumerate(_ticks(np.random.default_rng(1), cfg.vocab_size, slots)):
         got = eng.step(tick)
+        cuts.extend(x.numpy()[:, 0] for v in got.values() for x in v)
         ref = orc.step(tick, gemm=gemm)
         with perturbed(1):
             alt = twin.step(tick, gemm=gemm)
@@ -133,6 +135,11 @@ def test_benchmark_depth_at_north_star_bar():
     np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
     assert (orc.ring_pos[:slots, :W] >= 0).all() and (orc.length > W).all()
     assert floor < 1e-3, f"noise floor {floor:.2e}: the bar would not be meaningful on these inputs"
+    # and the bar discriminates: at this weight scale the cut scores still move with the input far beyond 2e-3
+    cuts = np.concatenate(cuts)
+    spread = float(np.percentile(cuts, 95) - np.percentile(cuts, 5))
+    print(f"[full] cut scores: 5-95 percentile spread {spread:.2e} over {cuts.size} tokens", flush=True)
+    assert spread > 10 * 2e-3
     rec = eng.rec.double().cpu().numpy()
     rel = max(np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s]) for s in range(slots))
     rel_twin = max(np.linalg.norm(twin.rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])

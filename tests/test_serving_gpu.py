@@ -106,3 +106,59 @@ def test_config5_mixed_ticks_with_resets():
         print(f"[serve] mixed tick {t}: {int(sizes.sum())} tokens, alone diff {worst:.2e}", flush=True)
         assert worst <= ALONE_TOL
     assert eng.stats["graph_replays"] > 0
+
+
+def test_config5_sampled_slots_match_oracle():
+    """The north-star bar at config 5's scale: a 352-slot engine of the benchmark geometry (graphs on, as served),
+    with random-init weights N(0, 0.0025), where the oracle's own fp32-level noise floor at 24 layers is below
+    1e-3 (tests/test_full_geometry_gpu.py::test_benchmark_depth_at_north_star_bar measures it on the same
+    geometry and scale). Contexts of 8-599 tokens (the sampled slots' rings wrap), then three mixed ticks of
+    config 5's chunk sizes, the sampled slots given 1-, 9- and 40-token chunks in one of them (token path and
+    MFMA bursts). Every per-token 1 - p(safe) of three sampled slots must be within 2e-3 of the oracle run on
+    those slots alone, with the oracle's own GEMMs (the engine's products at 352 rows are not reproducible at 3)."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    from oracle.backbone import StreamOracle
+    print("[serve] 352-slot baseline engine vs oracle on sampled slots, N(0, 0.0025)", flush=True)
+    cfg = GuardConfig.baseline()
+    model_cpu = GuardModel.random(cfg, seed=1, device="cpu", std=0.0025)
+    weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
+    eng = SlotStreamEngine(model_cpu.to("cuda:0"), SLOTS)
+    del model_cpu
+    sample = [3, 180, 351]
+    orc = StreamOracle(weights, cfg, len(sample), gdn="chunk")
+    to_orc = {s: i for i, s in enumerate(sample)}
+    V = cfg.vocab_size
+    rng = np.random.default_rng(5)
+
+    seen = []
+
+    def run(requests, what):
+        got = eng.step(requests)
+        mine = [(to_orc[s], ids) for s, ids in requests if s in to_orc]
+        ref = orc.step(mine)
+        where = [i for i, (s, _) in enumerate(requests) if s in to_orc]
+        worst = 0.0
+        for role in ("user", "assistant"):
+            for j, i in enumerate(where):
+                cut = got[role][i].numpy()[:, 0]
+                seen.append(cut)
+                worst = max(worst, float(np.abs(cut - np.asarray(ref[role][j])[:, 0]).max()))
+        print(f"[serve] {what}: {sum(len(ids) for _, ids in requests)} tokens, sampled slots' worst |d cut| "
+              f"{worst:.2e}", flush=True)
+        assert worst <= 2e-3, f"{what}: {worst:.2e}"
+
+    ctx = rng.integers(8, 600, SLOTS)
+    ctx[sample] = (530, 545, 560)
+    run([(s, rng.integers(0, V, int(n)).tolist()) for s, n in enumerate(ctx)], "contexts")
+    for t in range(3):
+        sizes = _chunk_sizes(rng, SLOTS)
+        if t == 1:
+            sizes[sample] = (1, 9, 40)
+        run([(s, rng.integers(0, V, int(n)).tolist()) for s, n in enumerate(sizes)], f"mixed tick {t}")
+    np.testing.assert_array_equal(eng.length[sample], orc.length[:len(sample)])
+    # the bar discriminates: at this weight scale the cut scores still move with the input far beyond 2e-3
+    cuts = np.concatenate(seen)
+    spread = float(np.percentile(cuts, 95) - np.percentile(cuts, 5))
+    print(f"[serve] sampled cut scores: 5-95 percentile spread {spread:.2e} over {cuts.size} tokens", flush=True)
+    assert spread > 10 * 2e-3
