@@ -205,6 +205,23 @@ __device__ __forceinline__ int swz_at(int r, int c) { return r * KD + 4 * (c ^ s
 // the same for the 64-column planes M' and P (16 pieces per row; the XOR permutes all of them)
 __device__ __forceinline__ int pw_at(int r, int c) { return r * PW + 4 * (c ^ swz(r)); }
 
+// The lower-triangle blocks of a plane pair (hi then lo plane) are the only part of M' and P the state kernel
+// reads: 320 16-byte slots per plane, row block I holding 2 (I + 1) slots per row. Slot q of the pair holds 16-byte
+// piece k of its row's lower triangle, i.e. logical pieces 4 (k / 2) .. +3, whose physical 16-byte slot is
+// 2 ((k / 2) ^ (swz(row) >> 2)) + k % 2 (the XOR keeps aligned groups of four). Returns its offset (bf16) in
+// the pair.
+constexpr int TRI_SLOTS = 320;
+__device__ __forceinline__ int tri_slot_offset(int q) {
+  const int e = q >= TRI_SLOTS;
+  const int qq = q - TRI_SLOTS * e;
+  const int I = qq >= 192 ? 3 : qq >= 96 ? 2 : qq >= 32 ? 1 : 0;
+  const int n2 = 2 * (I + 1);
+  const int q2 = qq - (I == 3 ? 192 : I == 2 ? 96 : I == 1 ? 32 : 0);
+  const int row = 16 * I + q2 / n2;
+  const int k = q2 - (q2 / n2) * n2;
+  return e * PL + row * PW + 8 * (2 * ((k >> 1) ^ (swz(row) >> 2)) + (k & 1));
+}
+
 // acc += sum_{J < NJ} M[row block I][col block J] . B_J for a matrix M kept in LDS as scaled fp16 hi / lo planes
 // (swizzled rows): hrow / lrow = row 16 I + m of the hi / lo planes, po[J] = offset of the lane's logical piece
 // 4 J + g in that row (rows 16 I + m share swz(m)); B_J are scaled fp16 hi / lo pairs in B layout. Three passes per
@@ -535,12 +552,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const ChunkParams p
     }
   }
   lds_barrier();
-  // the two planes are contiguous in LDS and in the workspace with the same swizzled rows: a linear copy
+  // the two planes have the same swizzled rows in LDS and in the workspace: a copy of the lower-triangle slots,
+  // all that the state kernel reads (640 of the pair's 1,024 16-byte pieces)
 #pragma unroll
-  for (int i = 0; i < (2 * PL * 2 / 16 + 255) / 256; ++i) {
-    const int x = threadIdx.x + 256 * i;
-    if (x < 2 * PL * 2 / 16)
-      reinterpret_cast<u32x4*>(Mh_g)[x] = reinterpret_cast<const u32x4*>(Mh_s)[x];
+  for (int i = 0; i < (2 * TRI_SLOTS + 255) / 256; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    if (q < 2 * TRI_SLOTS) {
+      const int off = tri_slot_offset(q);
+      *reinterpret_cast<u32x4*>(Mh_g + off) = *reinterpret_cast<const u32x4*>(Mh_s + off);
+    }
   }
 }
 
@@ -584,7 +604,6 @@ __global__ __launch_bounds__(1024) void gdn_chunk_order_kernel(const ChunkParams
 //   output: fetch Q V P                        | B1 | Sx -> Q S (64 x 16) | B2 | Vx -> O, stage, store O | B0
 // ---------------------------------------------------------------------------------------------------------
 constexpr int XP = 64 * 4;         // one handed-over fragment: 64 lanes x 4 bf16
-constexpr int TRI_SLOTS = 320;     // 16-byte slots of a plane's lower-triangle blocks: 16 rows x 2 (I + 1), I < 4
 
 template <typename ST>
 __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams p) {
@@ -671,22 +690,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(const ChunkParams 
   const int rx = threadIdx.x & 255;
   const int st_t = rx >> 2;
   const int sp = rx & 3;
-  // slot q of a plane pair (hi then lo plane, 320 slots each; row block I has 2 (I + 1) slots per row): the
-  // slot holds 16-byte piece k of the row's lower triangle, i.e. logical pieces 4 (k / 2) .. +3, whose
-  // physical 16-byte slot is 2 ((k / 2) ^ (swz(row) >> 2)) + k % 2 (the XOR keeps aligned groups of four)
+  // the lower-triangle slots of a plane pair this thread stages (tri_slot_offset)
   int qoff[3];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int q = min(rx + 256 * i, 2 * TRI_SLOTS - 1);
-    const int e = q >= TRI_SLOTS;
-    const int qq = q - TRI_SLOTS * e;
-    const int I = qq >= 192 ? 3 : qq >= 96 ? 2 : qq >= 32 ? 1 : 0;
-    const int n2 = 2 * (I + 1);
-    const int q2 = qq - (I == 3 ? 192 : I == 2 ? 96 : I == 1 ? 32 : 0);
-    const int row = 16 * I + q2 / n2;
-    const int k = q2 - (q2 / n2) * n2;
-    qoff[i] = e * PL + row * PW + 8 * (2 * ((k >> 1) ^ (swz(row) >> 2)) + (k & 1));
-  }
+  for (int i = 0; i < 3; ++i) qoff[i] = tri_slot_offset(min(rx + 256 * i, 2 * TRI_SLOTS - 1));
   const bool third = rx + 512 < 2 * TRI_SLOTS;
   auto row_of = [&](int c0) { return p.qkv + (tok0 + (c0 + st_t < ntok ? c0 + st_t : 0)) * p.qkv_stride; };
   // 16-byte piece j of a K / Q row holds logical 8-byte pieces 2j, 2j + 1: it lands in 16-byte slot
