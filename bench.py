@@ -241,9 +241,9 @@ def measured_traffic(rows, state_dtype):
 def ring_decode_rate(torch, rows=352, iters=50):
     """Decode ring attention (hsg_ring_decode: one fused launch at 4 query heads per kv head) at the 352 x 1-token
     decode shape, HIP events on the launch stream: config 2's ring fills (uniform in [1, 512]) scaled to 352 rows,
-    and full rings (the steady state of a live session). Algorithmic bytes: the visible keys and values (n 256 dims x 2 B x 2),
-    their positions (8 B each), q, gate and out (3 x 16 heads x 512 B), the new key and value read and
-    written to the ring (4 kv heads x 512 B x 4). Launch i reads ring set i mod 3 (the rings of every row, 740 MB a
+    and full rings (the steady state of a live session). Algorithmic bytes: the visible keys and values (n 256
+    dims x 2 B x 2), their positions (8 B each), q, gate and out (3 x 16 heads x 512 B), the new key and value read
+    and written to the ring (4 kv heads x 512 B x 4). Launch i reads ring set i mod 3 (the rings of every row, 740 MB a
     set), so no launch reads rings the previous one just read from the 256 MB Infinity Cache: in a step each
     attention layer's rings were last read a whole step earlier."""
     from hs_guard.engine.kernels import ring_attention_v8
@@ -621,7 +621,8 @@ def main():
     ap.add_argument("--chunk-only", action="store_true",
                     help="only the config-4 chunked-prefill measurement (profiled under rocprofv3)")
     ap.add_argument("--gdn-tick-only", action="store_true",
-                    help="only the GDN slot step on a config-5 tick at several burst thresholds, and a lone 64-token row")
+                    help="only the GDN slot step on a config-5 tick at several burst thresholds, and a lone 64-token "
+                         "row")
     ap.add_argument("--ring-tick-only", action="store_true",
                     help="only the tiled ring attention on a config-5 mixed tick's multi-token rows")
     ap.add_argument("--ring-only", action="store_true",
