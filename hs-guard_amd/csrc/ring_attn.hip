@@ -306,6 +306,14 @@ __global__ __launch_bounds__(NW * 64, 2) void ring_attn_mfma_kernel(const RingPa
     if (row_ok) {
       uint16_t* dst = p.out + o_row + l_tok * p.o_sl + h * p.o_sh + gq * p.o_sg;
       const uint16_t* gsrc = p.gate ? p.gate + g_row + l_tok * p.g_sl + h * p.g_sh + gq * p.g_sg + p.g_off : nullptr;
+      // every gate piece is loaded before the first store: out may alias gate as far as the compiler knows, so a
+      // load after a store waits for it, and the 16 pieces were 16 serial memory round trips at the end of each
+      // workgroup
+      uint2 gw[D / 16];
+      if (gsrc) {
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) gw[t] = *reinterpret_cast<const uint2*>(gsrc + 16 * t + 4 * q4);
+      }
 #pragma unroll
       for (int t = 0; t < D / 16; ++t) {
         const int d = 16 * t + 4 * q4;
@@ -314,7 +322,8 @@ __global__ __launch_bounds__(NW * 64, 2) void ring_attn_mfma_kernel(const RingPa
         for (int i = 0; i < 4; ++i) y[i] = l_run > 0.f ? rbf(O[t][i] / l_run) : 0.f;
         if (gsrc) {
           float gt[4];
-          load4_bf16(gsrc + d, gt);
+          unpack2(gw[t].x, gt[0], gt[1]);
+          unpack2(gw[t].y, gt[2], gt[3]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) y[i] = y[i] * rbf(1.0f / (1.0f + expf(-gt[i])));
         }
