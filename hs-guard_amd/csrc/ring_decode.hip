@@ -693,6 +693,14 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
     uint16_t* orow = p.out + row_base(p, p.o_sn, p.o_sl, n, ri.tok) + h * p.o_sh;
     const uint16_t* grow = p.gate ? p.gate + row_base(p, p.g_sn, p.g_sl, n, ri.tok) + h * p.g_sh + p.g_off
                                   : nullptr;
+    // every head's gate piece is loaded before the first output store (out may alias gate as far as the compiler
+    // knows, so a load after a store waits for it: one memory round trip per head otherwise)
+    uint2 gw[GT];
+    if (grow) {
+#pragma unroll
+      for (int g = 0; g < GT; ++g)
+        gw[g] = *reinterpret_cast<const uint2*>(grow + min(g, G - 1) * p.g_sg + 4 * lane);
+    }
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
       if (g < G) {
@@ -703,7 +711,8 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
         for (int e = 0; e < 4; ++e) y[e] = l > 0.f ? rbf(acc[g][e] / l) : 0.f;
         if (grow) {
           float gt[4];
-          load4_bf16(grow + g * p.g_sg + 4 * lane, gt);
+          unpack2(gw[g].x, gt[0], gt[1]);
+          unpack2(gw[g].y, gt[2], gt[3]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = y[e] * rbf(1.0f / (1.0f + expf(-gt[e])));
         }
