@@ -94,8 +94,10 @@ def test_baseline_geometry_matches_oracle(full):
     assert max(rel) <= FLOOR_FACTOR * max(rel_twin)
 
 
-def test_benchmark_depth_at_north_star_bar():
-    """The 2e-3 bar itself at the benchmark depth: GuardConfig.baseline() (24 layers) with random-init weights
+@pytest.mark.parametrize("geometry", ["baseline", "v10"])
+def test_benchmark_depth_at_north_star_bar(geometry):
+    """The 2e-3 bar itself at the benchmark depth: GuardConfig.baseline() (24 layers; and the released v10
+    geometry, 8 q / 2 kv heads, vocab 248,320) with random-init weights
     N(0, 0.0025), where the oracle's fp32-level noise floor is below 1e-3 (measured here on the same inputs, and on
     the CPU by tests/test_oracle_backbone.py::test_noise_floor_scales_with_weights). Four slots receive contexts of
     520-553 tokens in 64-token ticks (every ring wraps), then four single-token ticks and a mixed tick; every
@@ -106,8 +108,8 @@ def test_benchmark_depth_at_north_star_bar():
     from hs_guard.model import GuardConfig, GuardModel
     from oracle.backbone import StreamOracle
     from oracle.bf16 import perturbed
-    print("[full] benchmark depth, N(0, 0.0025), 2e-3 bar", flush=True)
-    cfg = GuardConfig.baseline()
+    print(f"[full] benchmark depth, {geometry} geometry, N(0, 0.0025), 2e-3 bar", flush=True)
+    cfg = getattr(GuardConfig, geometry)()
     model_cpu = GuardModel.random(cfg, seed=0, device="cpu", std=0.0025)
     weights = {k: v.float().numpy() for k, v in model_cpu.weights.items()}
     slots = 4
