@@ -206,6 +206,137 @@ extern "C" int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* ind
   return n;
 }
 
+namespace {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// Skinny products (M <= MM rows, the decode ticks): D[m, n] = sum_k A[m, k] W[n, k], bandwidth-bound on W. Each
+// wave takes NC output columns (4 waves per workgroup); lane l takes the 8 elements 512 c + 8 l .. +7 of each
+// 512-wide chunk c of K, so every load instruction of a wave reads 1 KB of one contiguous W row. K runs in panels
+// of CH chunks: the workgroup loads A's panel (MM rows x 512 CH) once into LDS while the waves' NC x CH W loads are
+// in flight, then each wave takes A's pieces from LDS (conflict-free 16-byte reads, each used for NC columns),
+// accumulates in fp32 on v_dot2_f32_bf16 (two products per instruction), reduces over the 64 lanes with the fixed
+// DPP / permlane tree (so a result does not depend on timing), and rounds to bf16. Lane l's sum runs over its
+// pieces in k order whatever MM, CH and NC are, so a row's result depends on its own inputs and K only.
+template <int MM, int CH, int NC>
+__global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int64_t lda, const uint16_t* W,
+                                                          int64_t ldw, uint16_t* D, int64_t ldd, int M, int N,
+                                                          int K) {
+  constexpr int PIECES = 64 * CH;                    // 8-element pieces per A row per panel
+  constexpr int STAGE = (MM * PIECES + 255) / 256;   // A pieces each thread stages per panel
+  __shared__ hsg::u32x4 a_lds[MM * PIECES];          // [MM][PIECES], MM * CH KiB
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int n0 = (blockIdx.x * 4 + (tid >> 6)) * NC;
+  // a column past N is computed as column N - 1 and not stored, so every wave reaches the barriers
+  const uint16_t* wrow[NC];
+#pragma unroll
+  for (int t = 0; t < NC; ++t) wrow[t] = W + (int64_t)min(n0 + t, N - 1) * ldw;
+  float acc[NC][MM];
+#pragma unroll
+  for (int t = 0; t < NC; ++t)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[t][m] = 0.f;
+  for (int kb = 0; kb < K; kb += 512 * CH) {
+    hsg::u32x4 ap[STAGE];
+#pragma unroll
+    for (int i = 0; i < STAGE; ++i) {
+      const int q = min(tid + 256 * i, MM * PIECES - 1);
+      const int m = q / PIECES, p = q % PIECES;
+      ap[i] = *reinterpret_cast<const hsg::u32x4*>(A + (int64_t)min(m, M - 1) * lda + min(kb + 8 * p, K - 8));
+    }
+    hsg::u32x4 wv[NC][CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k0 = min(kb + 512 * c + 8 * lane, K - 8);   // clamped in bounds; pieces past K count as zero
+#pragma unroll
+      for (int t = 0; t < NC; ++t) wv[t][c] = *reinterpret_cast<const hsg::u32x4*>(wrow[t] + k0);
+    }
+    __syncthreads();   // the previous panel's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < STAGE; ++i)
+      if (tid + 256 * i < MM * PIECES) a_lds[tid + 256 * i] = ap[i];
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int k = kb + 512 * c + 8 * lane;
+      const bool live = k < K;
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        const hsg::u32x4 av = a_lds[m * PIECES + 64 * c + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // both operands through plain uint32_t values: a bit_cast of a vector element lvalue (wv[t][c][j])
+          // reads element 0 whatever j is
+          const uint32_t a2 = live ? av[j] : 0u;
+#pragma unroll
+          for (int t = 0; t < NC; ++t) {
+            const uint32_t w2 = live ? wv[t][c][j] : 0u;
+            acc[t][m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a2),
+                                                        __builtin_bit_cast(bf16x2_t, w2), acc[t][m], false);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NC; ++t) {
+    float out = 0.f;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const float s = hsg::wave_sum(acc[t][m]);
+      if (lane == m) out = s;
+    }
+    if (n0 + t < N && lane < M) D[(int64_t)lane * ldd + n0 + t] = hsg::f2bf(out);
+  }
+}
+
+// columns per wave: two where K is short (K <= 1024, the products of width 7168 and more), so each wave has 4 KB of
+// W in flight and the grid fits the chip in one round; measured on MI355X against one and four per wave
+template <int MM, int CH>
+void launch_skinny_nc(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* d, int64_t ldd,
+                      int M, int N, int K, hipStream_t st) {
+  if (K <= 1024)
+    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 2>), dim3((N + 7) / 8), dim3(256), 0, st, a, lda, w, ldw, d, ldd,
+                       M, N, K);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 1>), dim3((N + 3) / 4), dim3(256), 0, st, a, lda, w, ldw, d, ldd,
+                       M, N, K);
+}
+
+template <int MM>
+void launch_skinny(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* d, int64_t ldd, int M,
+                   int N, int K, hipStream_t st) {
+  if (K <= 1024)
+    launch_skinny_nc<MM, 2>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  else if (K <= 2048)
+    launch_skinny_nc<MM, 4>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  else
+    launch_skinny_nc<MM, 8>(a, lda, w, ldw, d, ldd, M, N, K, st);
+}
+
+}  // namespace
+
+extern "C" int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd,
+                                    int32_t M, int32_t N, int32_t K, void* stream) {
+  using namespace hsg;
+  if (!A || !W || !D || M <= 0 || N <= 0 || K <= 0 || lda < K || ldw < K || ldd < N) return HSG_ERR_ARG;
+  if (M > HSG_GEMM_SKINNY_M_MAX) return HSG_ERR_SHAPE;
+  if (K % 8 || lda % 8 || ldw % 8 || !aligned(A, 16) || !aligned(W, 16) || !aligned(D, 2)) return HSG_ERR_ALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t* a = static_cast<const uint16_t*>(A);
+  const uint16_t* w = static_cast<const uint16_t*>(W);
+  uint16_t* d = static_cast<uint16_t*>(D);
+  if (M == 1)
+    launch_skinny<1>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  else if (M == 2)
+    launch_skinny<2>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  else if (M <= 4)
+    launch_skinny<4>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  else
+    launch_skinny<8>(a, lda, w, ldw, d, ldd, M, N, K, st);
+  return launch_status();
+}
+
 extern "C" int hsg_gemm_blas_version(void) {
   std::lock_guard<std::mutex> lock(ctx_mu);
   DeviceCtx* c = nullptr;

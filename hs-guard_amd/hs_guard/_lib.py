@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libhsg.so")
 # return codes of include/hsg.h
 HSG_OK, HSG_ERR_ARG, HSG_ERR_ALIGN, HSG_ERR_SHAPE, HSG_ERR_BLAS = 0, -1, -2, -3, -4
 HSG_GDN_BURST_MIN_DEFAULT = 16   # include/hsg.h
+HSG_GEMM_SKINNY_M_MAX = 8        # include/hsg.h
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -119,6 +120,7 @@ SIGNATURES = {
     "hsg_ring_pos_update": (ctypes.c_int, [_P, _I64, _I32, _P, _P, _P, _I32, _I32, _P]),
     "hsg_gemm_bf16": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _I32, _P, ctypes.c_size_t,
                                      _P]),                  # A, lda, W, ldw, D, ldd, M, N, K, algo, ws, ws_bytes, stream
+    "hsg_gemm_bf16_skinny": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32, _P]),
     "hsg_gemm_candidates": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, ctypes.c_size_t]),
     "hsg_gemm_blas_version": (ctypes.c_int, []),
 }

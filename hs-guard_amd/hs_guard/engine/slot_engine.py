@@ -25,7 +25,7 @@ import numpy as np
 import torch
 
 from .. import _hostpack
-from .._lib import HSG_ERR_SHAPE, HSG_GDN_BURST_MIN_DEFAULT, check, lib
+from .._lib import HSG_ERR_SHAPE, HSG_GDN_BURST_MIN_DEFAULT, HSG_GEMM_SKINNY_M_MAX, check, lib
 from ..model import ROLES, GuardModel
 from .gemm_plan import WORKSPACE_BYTES as GEMM_WORKSPACE_BYTES
 from .gemm_plan import GemmPlans
@@ -184,7 +184,7 @@ class SlotStreamEngine(PreparedWeights):
 
     def __init__(self, model: GuardModel, max_slots, state_dtype="float32", use_graphs=True, roles=ROLES,
                  session_buckets=None, max_tick_tokens=64, chunk_min_tokens=16, fuse_conv=True,
-                 gdn_burst_min=HSG_GDN_BURST_MIN_DEFAULT):
+                 gdn_burst_min=HSG_GDN_BURST_MIN_DEFAULT, gemm_skinny_rows=HSG_GEMM_SKINNY_M_MAX):
         if not isinstance(max_slots, int) or max_slots < 1:
             raise ValueError("max_slots must be a positive integer")
         if state_dtype not in STATE_DTYPES:
@@ -204,6 +204,11 @@ class SlotStreamEngine(PreparedWeights):
         if gdn_burst_min < 0:
             raise ValueError("gdn_burst_min must be >= 0")
         self.gdn_burst_min = int(gdn_burst_min)
+        # projections of at most gemm_skinny_rows tokens (the small decode ticks) run on hsg_gemm_bf16_skinny, which
+        # streams the weights at HBM rate where hipBLASLt's smallest tiles do not; 0 sends every product to hipBLASLt
+        if not 0 <= gemm_skinny_rows <= HSG_GEMM_SKINNY_M_MAX:
+            raise ValueError(f"gemm_skinny_rows must be in [0, {HSG_GEMM_SKINNY_M_MAX}]")
+        self.gemm_skinny_rows = int(gemm_skinny_rows)
         lib()  # fail loudly here if the HIP library is missing
         cfg = model.config
         # the GDN layers' causal conv runs inside the slot step (hsg_gdn_conv_slot_step_gated) when every value
@@ -279,15 +284,21 @@ class SlotStreamEngine(PreparedWeights):
             self.buf["gdn_o"] = torch.zeros(T * cfg.value_dim, dtype=bf16, device=dev)
 
     def mm(self, x, w, out):
-        """out[M, N] = x[M, K] . w[N, K]^T (bf16, row-major, unit column stride) on the current stream, through
-        hsg_gemm_bf16 with the committed solution for (M, N, K) (hipBLASLt's first heuristic candidate for shapes the
-        table lacks). Every projection of the tick goes through here, so a test that wants the engine's exact
-        products calls this too."""
+        """out[M, N] = x[M, K] . w[N, K]^T (bf16, row-major, unit column stride) on the current stream: through
+        hsg_gemm_bf16_skinny for M <= gemm_skinny_rows (when K, the row strides and the operands are aligned as it
+        needs), else through hsg_gemm_bf16 with the committed solution for (M, N, K) (hipBLASLt's first heuristic
+        candidate for shapes the table lacks). Every projection of the tick goes through here, so a test that wants
+        the engine's exact products calls this too."""
         M, K = x.shape
         N = w.shape[0]
         if w.shape[1] != K or out.shape != (M, N) or x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
             raise ValueError("mm: shapes or strides do not match D[M, N] = A[M, K] . W[N, K]^T")
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        if (M <= self.gemm_skinny_rows and K % 8 == 0 and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0
+                and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0):
+            check(lib().hsg_gemm_bf16_skinny(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
+                                             out.stride(0), M, N, K, stream), "hsg_gemm_bf16_skinny")
+            return out
         index = self.gemm_plans.index(M, N, K)
         rc = lib().hsg_gemm_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
                                  M, N, K, index, self.gemm_ws.data_ptr(), self.gemm_ws.numel(), stream)

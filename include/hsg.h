@@ -404,6 +404,21 @@ int hsg_gemm_bf16(const void* A, int64_t lda, const void* W, int64_t ldw, void* 
 int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_t* workspace, int32_t max_count,
                         size_t workspace_limit);
 
+/* Rows of A that hsg_gemm_bf16_skinny accepts. */
+#define HSG_GEMM_SKINNY_M_MAX 8
+
+/*
+ * Skinny projection product for decode ticks, bandwidth-bound on W: D[M, N] = A[M, K] . W[N, K]^T for
+ * M <= HSG_GEMM_SKINNY_M_MAX, bf16 row-major (row strides lda, ldw, ldd in elements), fp32 accumulation, one
+ * rounding to bf16. Replaces the same nn.Linear products as hsg_gemm_bf16
+ * (src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89) when a tick has at most 8 tokens. Each output is a
+ * fixed reduction over k (per lane in k order, then a fixed tree over 64 lanes): the result depends on the inputs
+ * and K only, not on M, N or timing. Requires K, lda and ldw multiples of 8 and A, W 16-byte aligned
+ * (HSG_ERR_ALIGN), M <= HSG_GEMM_SKINNY_M_MAX (HSG_ERR_SHAPE). Allocates nothing; capturable.
+ */
+int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd, int32_t M,
+                         int32_t N, int32_t K, void* stream);
+
 /* hipBLASLt's version on the current device (solution indices are valid only for the version they came from). */
 int hsg_gemm_blas_version(void);
 

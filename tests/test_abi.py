@@ -35,6 +35,7 @@ def test_constants_match_the_header():
     from hs_guard import _lib
     text = open(HEADER).read()
     assert int(re.search(r"#define HSG_GDN_BURST_MIN_DEFAULT (\d+)", text).group(1)) == _lib.HSG_GDN_BURST_MIN_DEFAULT
+    assert int(re.search(r"#define HSG_GEMM_SKINNY_M_MAX (\d+)", text).group(1)) == _lib.HSG_GEMM_SKINNY_M_MAX
     for name in ("HSG_OK", "HSG_ERR_ARG", "HSG_ERR_ALIGN", "HSG_ERR_SHAPE", "HSG_ERR_BLAS"):
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m is not None and int(m.group(1)) == getattr(_lib, name), name
@@ -110,3 +111,9 @@ def test_argument_errors_are_rejected_before_launch():
     assert L.hsg_ring_attention(None, 0, 0, 0, 0, None, None, 5, 512, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
                                 0, 0, None, None, None, None, None, 0, 1, 4, 4, 256, 1.0, 0, 0, None, 0, 0, 0, 0,
                                 None) == 0
+    # skinny GEMM: null operands, more than 8 rows, K not a multiple of 8, unaligned A (placeholders, never read)
+    assert L.hsg_gemm_bf16_skinny(None, 1024, 256, 1024, 256, 64, 1, 64, 1024, None) == -1
+    assert L.hsg_gemm_bf16_skinny(256, 1024, 256, 1024, 256, 64, 9, 64, 1024, None) == -3
+    assert L.hsg_gemm_bf16_skinny(256, 1020, 256, 1020, 256, 64, 1, 64, 1020, None) == -2
+    assert L.hsg_gemm_bf16_skinny(258, 1024, 256, 1024, 256, 64, 1, 64, 1024, None) == -2
+    assert L.hsg_gemm_bf16_skinny(256, 1000, 256, 1024, 256, 64, 1, 64, 1024, None) == -1   # lda < K

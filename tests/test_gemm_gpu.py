@@ -174,3 +174,88 @@ def test_process_runs_torchs_hipblaslt():
     paths = {line.split()[-1] for line in maps.splitlines() if "libhipblaslt.so" in line}
     torch_lib = os.path.realpath(os.path.join(os.path.dirname(_torch.__file__), "lib"))
     assert paths and all(os.path.realpath(p).startswith(torch_lib) for p in paths), paths
+
+
+def _skinny(A, W, out=None):
+    from hs_guard._lib import lib
+    M, K = A.shape
+    N = W.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=A.device)
+    rc = lib().hsg_gemm_bf16_skinny(A.data_ptr(), A.stride(0), W.data_ptr(), W.stride(0), out.data_ptr(),
+                                    out.stride(0), M, N, K, torch.cuda.current_stream().cuda_stream)
+    return rc, out
+
+
+def _within_rounding(out, A, W):
+    """Every element within bf16 output rounding (2^-8 relative, twice the half-ulp) of the float64 product, plus
+    2^-16 of sum_k |a_k w_k| for fp32 accumulation: a dropped, doubled or misplaced 8-element piece fails it."""
+    a, w = A.double().cpu(), W.double().cpu()
+    ref = a @ w.t()
+    mag = a.abs() @ w.abs().t()
+    err = (out.double().cpu() - ref).abs()
+    bad = err > 2.0 ** -8 * ref.abs() + 2.0 ** -16 * mag
+    return int(bad.sum())
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+def test_skinny_matches_float64_per_element(M):
+    """hsg_gemm_bf16_skinny at the engine's projection shapes and at ragged ones (N not a multiple of 4, K not a
+    multiple of 512, K = 8), every element against the float64 product; repeated calls equal bit for bit."""
+    print(f"[gemm] skinny M={M}", flush=True)
+    for N, K in SHAPES + [(1027, 1016), (5, 8), (13, 4104), (3, 520)]:
+        A, W = _inputs(M, N, K, seed=M)
+        rc, out = _skinny(A, W)
+        rc2, out2 = _skinny(A, W)
+        torch.cuda.synchronize()
+        assert rc == 0 and rc2 == 0, (M, N, K, rc, rc2)
+        assert torch.equal(out, out2), (M, N, K)
+        assert _within_rounding(out, A, W) == 0, (M, N, K)
+
+
+def test_skinny_reads_only_k_columns_and_rows_are_independent():
+    """Row strides beyond K with NaN in the padding columns (never read), and each row's result the same bit for
+    bit whether it is computed alone or with 7 others (the per-row reduction order depends on K only)."""
+    M, N, K, ld = 8, 1030, 1016, 1032
+    A, W = _inputs(M, N, ld, seed=3)
+    A[:, K:] = float("nan")
+    W[:, K:] = float("nan")
+    A, W = A[:, :K], W[:, :K]
+    out_full = torch.full((M, N + 6), float("nan"), dtype=torch.bfloat16, device="cuda")
+    rc, _ = _skinny(A, W, out_full[:, :N])
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.isnan(out_full[:, N:]).all()          # columns past N untouched
+    out = out_full[:, :N]
+    assert not torch.isnan(out).any()
+    assert _within_rounding(out, A, W) == 0
+    for m in range(M):
+        rc, one = _skinny(A[m:m + 1], W)
+        torch.cuda.synchronize()
+        assert rc == 0 and torch.equal(one[0], out[m]), m
+
+
+def test_engine_mm_routes_small_products_to_the_skinny_kernel():
+    """The engine's mm at M <= 8 is hsg_gemm_bf16_skinny's product; with gemm_skinny_rows=0 it is hipBLASLt's."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    model = GuardModel.random(cfg, seed=0, device="cuda")
+    eng = SlotStreamEngine(model, 4, use_graphs=False)
+    eng0 = SlotStreamEngine(model, 4, use_graphs=False, gemm_skinny_rows=0)
+    w = eng.layers[0]["w_in"]
+    for M in (1, 4, 8, 9):
+        x = torch.randn(M, w.shape[1], device="cuda").bfloat16()
+        got = eng.mm(x, w, torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda"))
+        got0 = eng0.mm(x, w, torch.empty(M, w.shape[0], dtype=torch.bfloat16, device="cuda"))
+        rc, ref = _skinny(x, w) if M <= 8 else _run(x, w, eng.gemm_plans.index(M, w.shape[0], w.shape[1]),
+                                                    eng.gemm_ws)
+        rc0, ref0 = _run(x, w, eng0.gemm_plans.index(M, w.shape[0], w.shape[1]), eng0.gemm_ws)
+        torch.cuda.synchronize()
+        assert rc == 0 and rc0 == 0
+        assert torch.equal(got, ref), M
+        assert torch.equal(got0, ref0), M
+    with pytest.raises(ValueError):
+        SlotStreamEngine(model, 4, use_graphs=False, gemm_skinny_rows=9)
