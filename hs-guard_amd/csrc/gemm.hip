@@ -218,15 +218,53 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 // accumulates in fp32 on v_dot2_f32_bf16 (two products per instruction), reduces over the 64 lanes with the fixed
 // DPP / permlane tree (so a result does not depend on timing), and rounds to bf16. Lane l's sum runs over its
 // pieces in k order whatever MM, CH and NC are, so a row's result depends on its own inputs and K only.
-template <int MM, int CH, int NC>
+// The operand A is staged in one of three modes:
+//   PLAIN:   A as given;
+//   SILU:    A is the MLP's gate|up projection (row m: gate in columns [0, K), up in [K, 2K)) and the operand is
+//            bf16(bf16(silu(gate)) * up) with the rounding of hsg_silu_mul;
+//   ADDNORM: K = 1024, A is the residual stream and the operand is the add + RMSNorm of hsg_add_rmsnorm
+//            (bf16(A + mix), normalised, times w1), one wave per row in that kernel's lane layout (which is the
+//            product's chunk layout at CH = 2) through the same row function; workgroup 0 writes the new residual
+//            bf16(A + mix) to a separate buffer.
+// Either way the result is bitwise that of the separate kernel followed by the PLAIN product.
+enum SkinnyMode { PLAIN = 0, SILU = 1, ADDNORM = 2 };
+
+struct SkinnyNorm {          // ADDNORM's extra operands
+  const uint16_t* mix;
+  int64_t ldm;
+  const float* w1;
+  float eps;
+  uint16_t* hid_out;
+  int64_t ldo;
+};
+
+__device__ __forceinline__ float bf_at(uint32_t w, int hi) {
+  return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+}
+
+__device__ __forceinline__ hsg::u32x4 silu_mul8(hsg::u32x4 g, hsg::u32x4 u) {
+  hsg::u32x4 y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t gw = g[j], uw = u[j];
+    const float y0 = hsg::rbf(hsg::siluf_(bf_at(gw, 0))) * bf_at(uw, 0);
+    const float y1 = hsg::rbf(hsg::siluf_(bf_at(gw, 1))) * bf_at(uw, 1);
+    y[j] = (uint32_t)hsg::f2bf(y0) | ((uint32_t)hsg::f2bf(y1) << 16);
+  }
+  return y;
+}
+
+template <int MM, int CH, int NC, int MODE>
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int64_t lda, const uint16_t* W,
-                                                          int64_t ldw, uint16_t* D, int64_t ldd, int M, int N,
-                                                          int K) {
+                                                          int64_t ldw, uint16_t* D, int64_t ldd, int M, int N, int K,
+                                                          const SkinnyNorm nx) {
+  static_assert(MODE != ADDNORM || CH == 2, "the add + RMSNorm staging covers one 1024-wide panel");
   constexpr int PIECES = 64 * CH;                    // 8-element pieces per A row per panel
-  constexpr int STAGE = (MM * PIECES + 255) / 256;   // A pieces each thread stages per panel
+  constexpr int STAGE = (MM * PIECES + 255) / 256;   // A pieces each thread stages per panel (PLAIN, SILU)
+  constexpr int RW = (MM + 3) / 4;                   // rows each wave normalises (ADDNORM)
   __shared__ hsg::u32x4 a_lds[MM * PIECES];          // [MM][PIECES], MM * CH KiB
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int n0 = (blockIdx.x * 4 + (tid >> 6)) * NC;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * NC;
   // a column past N is computed as column N - 1 and not stored, so every wave reaches the barriers
   const uint16_t* wrow[NC];
 #pragma unroll
@@ -237,24 +275,67 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
 #pragma unroll
     for (int m = 0; m < MM; ++m) acc[t][m] = 0.f;
   for (int kb = 0; kb < K; kb += 512 * CH) {
-    hsg::u32x4 ap[STAGE];
+    // the panel's A loads first, then the W loads: waiting for A leaves W in flight
+    hsg::u32x4 ap[MODE == ADDNORM ? 1 : STAGE];
+    hsg::u32x4 hx[MODE == ADDNORM ? RW : 1][2], mx[MODE == ADDNORM ? RW : 1][2];
+    hsg::f32x4_n wv[4];
+    if constexpr (MODE == ADDNORM) {
 #pragma unroll
-    for (int i = 0; i < STAGE; ++i) {
-      const int q = min(tid + 256 * i, MM * PIECES - 1);
-      const int m = q / PIECES, p = q % PIECES;
-      ap[i] = *reinterpret_cast<const hsg::u32x4*>(A + (int64_t)min(m, M - 1) * lda + min(kb + 8 * p, K - 8));
+      for (int r = 0; r < RW; ++r) {
+        const int mr = min(wave + 4 * r, M - 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          hx[r][j] = *reinterpret_cast<const hsg::u32x4*>(A + (int64_t)mr * lda + 8 * lane + 512 * j);
+          mx[r][j] = *reinterpret_cast<const hsg::u32x4*>(nx.mix + (int64_t)mr * nx.ldm + 8 * lane + 512 * j);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        wv[2 * j] = *reinterpret_cast<const hsg::f32x4_n*>(nx.w1 + 8 * lane + 512 * j);
+        wv[2 * j + 1] = *reinterpret_cast<const hsg::f32x4_n*>(nx.w1 + 8 * lane + 512 * j + 4);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < STAGE; ++i) {
+        const int q = min(tid + 256 * i, MM * PIECES - 1);
+        const int m = q / PIECES, p = q % PIECES;
+        const uint16_t* apc = A + (int64_t)min(m, M - 1) * lda + min(kb + 8 * p, K - 8);
+        if constexpr (MODE == SILU)
+          ap[i] = silu_mul8(*reinterpret_cast<const hsg::u32x4*>(apc),
+                            *reinterpret_cast<const hsg::u32x4*>(apc + K));
+        else
+          ap[i] = *reinterpret_cast<const hsg::u32x4*>(apc);
+      }
     }
-    hsg::u32x4 wv[NC][CH];
+    hsg::u32x4 wv_[NC][CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int k0 = min(kb + 512 * c + 8 * lane, K - 8);   // clamped in bounds; pieces past K count as zero
 #pragma unroll
-      for (int t = 0; t < NC; ++t) wv[t][c] = *reinterpret_cast<const hsg::u32x4*>(wrow[t] + k0);
+      for (int t = 0; t < NC; ++t) wv_[t][c] = *reinterpret_cast<const hsg::u32x4*>(wrow[t] + k0);
     }
     __syncthreads();   // the previous panel's LDS reads are done
+    if constexpr (MODE == ADDNORM) {
 #pragma unroll
-    for (int i = 0; i < STAGE; ++i)
-      if (tid + 256 * i < MM * PIECES) a_lds[tid + 256 * i] = ap[i];
+      for (int r = 0; r < RW; ++r) {
+        const int m = wave + 4 * r;
+        if (m < MM) {   // wave-uniform: the row function reduces over the whole wave
+          hsg::u32x4 o[2];
+          hsg::rmsnorm_row1024<true>(hx[r], mx[r], wv, nx.eps, o);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) a_lds[m * PIECES + 64 * j + lane] = o[j];
+          if (blockIdx.x == 0 && m < M) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              *reinterpret_cast<hsg::u32x4*>(nx.hid_out + (int64_t)m * nx.ldo + 8 * lane + 512 * j) = hx[r][j];
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < STAGE; ++i)
+        if (tid + 256 * i < MM * PIECES) a_lds[tid + 256 * i] = ap[i];
+    }
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -265,12 +346,12 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
         const hsg::u32x4 av = a_lds[m * PIECES + 64 * c + lane];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          // both operands through plain uint32_t values: a bit_cast of a vector element lvalue (wv[t][c][j])
+          // both operands through plain uint32_t values: a bit_cast of a vector element lvalue (wv_[t][c][j])
           // reads element 0 whatever j is
           const uint32_t a2 = live ? av[j] : 0u;
 #pragma unroll
           for (int t = 0; t < NC; ++t) {
-            const uint32_t w2 = live ? wv[t][c][j] : 0u;
+            const uint32_t w2 = live ? wv_[t][c][j] : 0u;
             acc[t][m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a2),
                                                         __builtin_bit_cast(bf16x2_t, w2), acc[t][m], false);
           }
@@ -292,34 +373,37 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
 
 // columns per wave: two where K is short (K <= 1024, the products of width 7168 and more), so each wave has 4 KB of
 // W in flight and the grid fits the chip in one round; measured on MI355X against one and four per wave
-template <int MM, int CH>
+template <int MM, int CH, int MODE>
 void launch_skinny_nc(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* d, int64_t ldd,
-                      int M, int N, int K, hipStream_t st) {
+                      int M, int N, int K, const SkinnyNorm& nx, hipStream_t st) {
   if (K <= 1024)
-    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 2>), dim3((N + 7) / 8), dim3(256), 0, st, a, lda, w, ldw, d, ldd,
-                       M, N, K);
+    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 2, MODE>), dim3((N + 7) / 8), dim3(256), 0, st, a, lda, w, ldw, d,
+                       ldd, M, N, K, nx);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 1>), dim3((N + 3) / 4), dim3(256), 0, st, a, lda, w, ldw, d, ldd,
-                       M, N, K);
+    hipLaunchKernelGGL((skinny_gemm_kernel<MM, CH, 1, MODE>), dim3((N + 3) / 4), dim3(256), 0, st, a, lda, w, ldw, d,
+                       ldd, M, N, K, nx);
 }
 
-template <int MM>
-void launch_skinny(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* d, int64_t ldd, int M,
-                   int N, int K, hipStream_t st) {
+template <int MM, int MODE>
+void launch_skinny_k(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* d, int64_t ldd, int M,
+                     int N, int K, const SkinnyNorm& nx, hipStream_t st) {
   if (K <= 1024)
-    launch_skinny_nc<MM, 2>(a, lda, w, ldw, d, ldd, M, N, K, st);
-  else if (K <= 2048)
-    launch_skinny_nc<MM, 4>(a, lda, w, ldw, d, ldd, M, N, K, st);
-  else
-    launch_skinny_nc<MM, 8>(a, lda, w, ldw, d, ldd, M, N, K, st);
+    launch_skinny_nc<MM, 2, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
+  else if constexpr (MODE != ADDNORM) {
+    if (K <= 2048)
+      launch_skinny_nc<MM, 4, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
+    else
+      launch_skinny_nc<MM, 8, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
+  }
 }
 
-}  // namespace
-
-extern "C" int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd,
-                                    int32_t M, int32_t N, int32_t K, void* stream) {
+template <int MODE>
+int launch_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd, int M, int N, int K,
+                  const SkinnyNorm& nx, void* stream) {
   using namespace hsg;
-  if (!A || !W || !D || M <= 0 || N <= 0 || K <= 0 || lda < K || ldw < K || ldd < N) return HSG_ERR_ARG;
+  if (!A || !W || !D || M <= 0 || N <= 0 || K <= 0 || lda < (MODE == SILU ? 2 : 1) * (int64_t)K || ldw < K ||
+      ldd < N)
+    return HSG_ERR_ARG;
   if (M > HSG_GEMM_SKINNY_M_MAX) return HSG_ERR_SHAPE;
   if (K % 8 || lda % 8 || ldw % 8 || !aligned(A, 16) || !aligned(W, 16) || !aligned(D, 2)) return HSG_ERR_ALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -327,14 +411,38 @@ extern "C" int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, i
   const uint16_t* w = static_cast<const uint16_t*>(W);
   uint16_t* d = static_cast<uint16_t*>(D);
   if (M == 1)
-    launch_skinny<1>(a, lda, w, ldw, d, ldd, M, N, K, st);
+    launch_skinny_k<1, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
   else if (M == 2)
-    launch_skinny<2>(a, lda, w, ldw, d, ldd, M, N, K, st);
+    launch_skinny_k<2, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
   else if (M <= 4)
-    launch_skinny<4>(a, lda, w, ldw, d, ldd, M, N, K, st);
+    launch_skinny_k<4, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
   else
-    launch_skinny<8>(a, lda, w, ldw, d, ldd, M, N, K, st);
+    launch_skinny_k<8, MODE>(a, lda, w, ldw, d, ldd, M, N, K, nx, st);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd,
+                                    int32_t M, int32_t N, int32_t K, void* stream) {
+  return launch_skinny<PLAIN>(A, lda, W, ldw, D, ldd, M, N, K, SkinnyNorm{}, stream);
+}
+
+extern "C" int hsg_gemm_bf16_skinny_silu(const void* gate_up, int64_t ld_gu, const void* W, int64_t ldw, void* D,
+                                         int64_t ldd, int32_t M, int32_t N, int32_t K, void* stream) {
+  return launch_skinny<SILU>(gate_up, ld_gu, W, ldw, D, ldd, M, N, K, SkinnyNorm{}, stream);
+}
+
+extern "C" int hsg_gemm_bf16_skinny_addnorm(const void* hidden, int64_t ldh, const void* mix, int64_t ldm,
+                                            const float* w1, float eps, void* hidden_out, int64_t ldo, const void* W,
+                                            int64_t ldw, void* D, int64_t ldd, int32_t M, int32_t N, int32_t K,
+                                            void* stream) {
+  using namespace hsg;
+  if (!mix || !w1 || !hidden_out || hidden_out == hidden || ldm < K || ldo < K) return HSG_ERR_ARG;
+  if (K != 1024) return HSG_ERR_SHAPE;
+  if (ldm % 8 || ldo % 8 || !aligned(mix, 16) || !aligned(w1, 16) || !aligned(hidden_out, 16)) return HSG_ERR_ALIGN;
+  const SkinnyNorm nx{static_cast<const uint16_t*>(mix), ldm, w1, eps, static_cast<uint16_t*>(hidden_out), ldo};
+  return launch_skinny<ADDNORM>(hidden, ldh, W, ldw, D, ldd, M, N, K, nx, stream);
 }
 
 extern "C" int hsg_gemm_blas_version(void) {

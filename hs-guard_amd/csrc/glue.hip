@@ -20,12 +20,6 @@ namespace {
 constexpr int HID = 1024;
 typedef __attribute__((ext_vector_type(4))) float f32x4_;
 
-// 8 bf16 values of a 16-byte piece as fp32
-__device__ __forceinline__ void unpack8(const u32x4& w, float* x) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) unpack2(w[i], x[2 * i], x[2 * i + 1]);
-}
-
 template <bool EMBED, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* hidden, const uint16_t* mix, const int64_t* ids,
                                                       const uint16_t* emb, const float* w1, float eps,
@@ -40,54 +34,23 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t* hidden, const ui
     if (id < 0 || id >= vocab) id = 0;  // out-of-vocab ids are rejected on the host; never read OOB
     src = emb + id * HID;
   }
-  u32x4 hw[2], mw[2];
-  f32x4_ wv[4];
+  u32x4 hw[2], mw[2], o[2];
+  f32x4_n wv[4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int d = 8 * lane + 512 * j;
     hw[j] = *reinterpret_cast<const u32x4*>(src + d);
-    if constexpr (ADD) mw[j] = *reinterpret_cast<const u32x4*>(mix + row + d);
-    wv[2 * j] = *reinterpret_cast<const f32x4_*>(w1 + d);
-    wv[2 * j + 1] = *reinterpret_cast<const f32x4_*>(w1 + d + 4);
+    mw[j] = ADD ? *reinterpret_cast<const u32x4*>(mix + row + d) : u32x4{0u, 0u, 0u, 0u};
+    wv[2 * j] = *reinterpret_cast<const f32x4_n*>(w1 + d);
+    wv[2 * j + 1] = *reinterpret_cast<const f32x4_n*>(w1 + d + 4);
   }
-  float h[16];
-  unpack8(hw[0], h);
-  unpack8(hw[1], h + 8);
-  if constexpr (ADD) {
-    float m[16];
-    unpack8(mw[0], m);
-    unpack8(mw[1], m + 8);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = rbf(__fadd_rn(h[i], m[i]));
-    // h is bf16-exact: its bf16 bits are the upper half of the fp32 word
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      u32x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        o[i] = (__float_as_uint(h[8 * j + 2 * i]) >> 16) | (__float_as_uint(h[8 * j + 2 * i + 1]) & 0xffff0000u);
-      hw[j] = o;
-    }
-  }
+  rmsnorm_row1024<ADD>(hw, mw, wv, eps, o);
   if constexpr (EMBED || ADD) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(hidden + row + 8 * lane + 512 * j) = hw[j];
   }
-  float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) ss += h[i] * h[i];
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)HID + eps);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    u32x4 o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4_ w = wv[2 * j + (i >> 1)];
-      o[i] = pack_bf16x2((h[8 * j + 2 * i] * r) * w[(2 * i) & 3], (h[8 * j + 2 * i + 1] * r) * w[(2 * i + 1) & 3]);
-    }
-    *reinterpret_cast<u32x4*>(normed + row + 8 * lane + 512 * j) = o;
-  }
+  for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4*>(normed + row + 8 * lane + 512 * j) = o[j];
 }
 
 // ---------------------------------------------------------------------------------------------------

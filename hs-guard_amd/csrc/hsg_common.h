@@ -115,6 +115,57 @@ __device__ __forceinline__ float sum_stride8_dpp(float x) { return add_xor32(add
 // bitwise that of the butterfly, on every lane.
 __device__ __forceinline__ float wave_sum(float x) { return add_xor32(sum32_dpp(x)); }
 
+// ---- RMSNorm of one 1024-wide bf16 row per wave (add_square + rms_finish, src/hs_guard/engine/fused_kernels.py:
+// 30-72). Lane l holds elements 8 l .. 8 l + 7 of the row in x[0] and 512 + 8 l .. + 7 in x[1] (16-byte pieces) and
+// the matching fp32 weights w1 in w[0..3]. ADD: x = bf16(x + mix) first (one fp32 add; x is updated in place).
+// Then out = bf16((x * rsqrt(mean(x^2) + eps)) * w1). Shared by hsg_add_rmsnorm and the skinny products that apply
+// the norm while staging their operand, so both give the same bits. ----
+typedef __attribute__((ext_vector_type(4))) float f32x4_n;
+
+__device__ __forceinline__ void unpack8(const u32x4& w, float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) unpack2(w[i], x[2 * i], x[2 * i + 1]);
+}
+
+template <bool ADD>
+__device__ __forceinline__ void rmsnorm_row1024(u32x4 (&x)[2], const u32x4 (&mix)[2], const f32x4_n (&w)[4],
+                                                float eps, u32x4 (&out)[2]) {
+  float h[16];
+  unpack8(x[0], h);
+  unpack8(x[1], h + 8);
+  if constexpr (ADD) {
+    float m[16];
+    unpack8(mix[0], m);
+    unpack8(mix[1], m + 8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = rbf(__fadd_rn(h[i], m[i]));
+    // h is bf16-exact: its bf16 bits are the upper half of the fp32 word
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      u32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = (__float_as_uint(h[8 * j + 2 * i]) >> 16) | (__float_as_uint(h[8 * j + 2 * i + 1]) & 0xffff0000u);
+      x[j] = o;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss += h[i] * h[i];
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / 1024.0f + eps);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_n wq = w[2 * j + (i >> 1)];
+      o[i] = pack_bf16x2((h[8 * j + 2 * i] * r) * wq[(2 * i) & 3], (h[8 * j + 2 * i + 1] * r) * wq[(2 * i + 1) & 3]);
+    }
+    out[j] = o;
+  }
+}
+
 __device__ __forceinline__ float max_pair16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

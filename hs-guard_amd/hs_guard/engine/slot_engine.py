@@ -260,6 +260,8 @@ class SlotStreamEngine(PreparedWeights):
         widest = max(self.gdn_in, self.att_in, 2 * cfg.intermediate_size)
         self.buf = {
             "hidden": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
+            # the residual stream's second buffer for ticks whose add + RMSNorm runs inside the next product
+            "hidden2": torch.zeros(max(self.gemm_skinny_rows, 1) * cfg.hidden_size, dtype=bf16, device=dev),
             "normed": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
             "mix": torch.zeros(T * cfg.hidden_size, dtype=bf16, device=dev),
             "proj": torch.zeros(T * widest, dtype=bf16, device=dev),
@@ -294,8 +296,7 @@ class SlotStreamEngine(PreparedWeights):
         if w.shape[1] != K or out.shape != (M, N) or x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
             raise ValueError("mm: shapes or strides do not match D[M, N] = A[M, K] . W[N, K]^T")
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        if (M <= self.gemm_skinny_rows and K % 8 == 0 and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0
-                and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0):
+        if self._skinny(x, w, K):
             check(lib().hsg_gemm_bf16_skinny(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
                                              out.stride(0), M, N, K, stream), "hsg_gemm_bf16_skinny")
             return out
@@ -311,6 +312,28 @@ class SlotStreamEngine(PreparedWeights):
                                      out.stride(0), M, N, K, -1, self.gemm_ws.data_ptr(), self.gemm_ws.numel(), stream)
         check(rc, "hsg_gemm_bf16")
         return out
+
+    def _skinny(self, x, w, K):
+        """Whether the product of x's rows with w ([N, K]) runs on the skinny kernels."""
+        return (x.shape[0] <= self.gemm_skinny_rows and K % 8 == 0 and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0
+                and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+    def mm_silu(self, gu, w, out, act):
+        """out[M, N] = act . w[N, I]^T with act = bf16(bf16(silu(gu[:, :I])) * gu[:, I:]) (the MLP's SiLU gate and
+        down projection, src/hs_guard/engine/slot_engine_v8.py:52-53): one hsg_gemm_bf16_skinny_silu launch when
+        the skinny route applies (act is not written), else hsg_silu_mul into ``act`` and ``mm``. Bitwise the same
+        either way."""
+        M, I = gu.shape[0], gu.shape[1] // 2
+        if w.shape[1] != I or out.shape != (M, w.shape[0]) or gu.stride(1) != 1 or out.stride(1) != 1:
+            raise ValueError("mm_silu: shapes or strides do not match")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        if self._skinny(gu, w, I) and w.stride(1) == 1:
+            check(lib().hsg_gemm_bf16_skinny_silu(gu.data_ptr(), gu.stride(0), w.data_ptr(), w.stride(0),
+                                                  out.data_ptr(), out.stride(0), M, w.shape[0], I, stream),
+                  "hsg_gemm_bf16_skinny_silu")
+            return out
+        check(lib().hsg_silu_mul(gu.data_ptr(), gu.stride(0), I, act.data_ptr(), M, stream), "hsg_silu_mul")
+        return self.mm(act, w, out)
 
     def _view(self, name, *shape):
         n = 1
@@ -377,17 +400,41 @@ class SlotStreamEngine(PreparedWeights):
             cfg.linear_value_head_dim
         ids, pos, offsets, lens, slots, starts = (inp[k] for k in ("ids", "pos", "offsets", "lens", "slots",
                                                                     "starts"))
-        hidden = self._view("hidden", tb, H)
+        hid = [self._view("hidden", tb, H)]
         normed = self._view("normed", tb, H)
         mix = self._view("mix", tb, H)
         check(L.hsg_embed_rmsnorm(ids.data_ptr(), self.emb.data_ptr(), cfg.vocab_size,
-                                  self.layers[0]["in_w1"].data_ptr(), eps, hidden.data_ptr(), normed.data_ptr(), tb,
+                                  self.layers[0]["in_w1"].data_ptr(), eps, hid[0].data_ptr(), normed.data_ptr(), tb,
                                   H, st), "hsg_embed_rmsnorm")
+        # Each residual add + RMSNorm (hidden += mix, normed = norm(hidden) * w1) is applied by the product that
+        # reads normed. In ticks of at most gemm_skinny_rows tokens both run in one hsg_gemm_bf16_skinny_addnorm
+        # launch, which writes the residual to the other of two buffers (hid[0] -> hid[1] -> hid[0] ...); otherwise
+        # hsg_add_rmsnorm updates hid[0] in place and the product follows.
+        fuse = tb <= self.gemm_skinny_rows and H == 1024
+        if fuse:
+            hid.append(self._view("hidden2", tb, H))
+        pending = []    # the (mix, w1) of an add + RMSNorm not yet applied
+
+        def norm_mm(w, out):
+            if not pending:
+                return self.mm(normed, w, out)
+            mx, w1 = pending.pop()
+            if fuse and self._skinny(normed, w, H):
+                check(L.hsg_gemm_bf16_skinny_addnorm(hid[0].data_ptr(), H, mx.data_ptr(), H, w1.data_ptr(), eps,
+                                                     hid[1].data_ptr(), H, w.data_ptr(), w.stride(0),
+                                                     out.data_ptr(), out.stride(0), tb, w.shape[0], H, st),
+                      "hsg_gemm_bf16_skinny_addnorm")
+                hid.reverse()
+                return out
+            check(L.hsg_add_rmsnorm(hid[0].data_ptr(), mx.data_ptr(), w1.data_ptr(), eps, normed.data_ptr(), tb, H,
+                                    st), "hsg_add_rmsnorm")
+            return self.mm(normed, w, out)
+
         for i, ((kind, idx), Lw) in enumerate(zip(self.kind, self.layers)):
             if kind == "linear_attention":
                 C = cfg.conv_dim
                 proj = self._view("proj", tb, self.gdn_in)
-                self.mm(normed, Lw["w_in"], proj)
+                norm_mm(Lw["w_in"], proj)
                 out = self._view("mid", tb, cfg.value_dim)
                 base = proj.data_ptr()
                 # rows are packed longest first: in a prefill-like tick the rows of >= chunk_min_tokens tokens go
@@ -430,7 +477,7 @@ class SlotStreamEngine(PreparedWeights):
                 self.mm(out, Lw["w_out"], mix)
             else:
                 proj = self._view("proj", tb, self.att_in)
-                self.mm(normed, Lw["w_in"], proj)
+                norm_mm(Lw["w_in"], proj)
                 q = self._view("q", tb, hq * D)
                 k = self._view("k", tb, hkv * D)
                 base = proj.data_ptr()
@@ -450,27 +497,29 @@ class SlotStreamEngine(PreparedWeights):
                     nb, hkv, G, D, D ** -0.5, 1,
                     att.data_ptr(), 0, hq * D, G * D, D, self.ring_ws.data_ptr(), self.ring_ws.numel(), st),
                     "hsg_ring_decode")
-                check(L.hsg_ring_attention(
-                    q.data_ptr(), 0, hq * D, G * D, D,
-                    self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
-                    k.data_ptr(), 0, hkv * D, D,
-                    base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
-                    base, 0, self.att_in, G * 2 * D, 2 * D, D,
-                    self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
-                    nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
-                    att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
+                if tb >= 2:
+                    # a one-token bucket has no row of two or more steps: its program leaves the tiled kernel out
+                    check(L.hsg_ring_attention(
+                        q.data_ptr(), 0, hq * D, G * D, D,
+                        self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
+                        k.data_ptr(), 0, hkv * D, D,
+                        base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
+                        base, 0, self.att_in, G * 2 * D, 2 * D, D,
+                        self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(),
+                        offsets.data_ptr(), nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
+                        att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
                 self.mm(att, Lw["w_out"], mix)
-            check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), Lw["post_w1"].data_ptr(), eps,
-                                    normed.data_ptr(), tb, H, st), "hsg_add_rmsnorm")
+            pending.append((mix, Lw["post_w1"]))
             I = cfg.intermediate_size
             gu = self._view("proj", tb, 2 * I)
-            self.mm(normed, Lw["w_gu"], gu)
-            act = self._view("mid", tb, I)
-            check(L.hsg_silu_mul(gu.data_ptr(), 2 * I, I, act.data_ptr(), tb, st), "hsg_silu_mul")
-            self.mm(act, Lw["w_down"], mix)
+            norm_mm(Lw["w_gu"], gu)
+            self.mm_silu(gu, Lw["w_down"], mix, self._view("mid", tb, I))
             nxt = self.layers[i + 1]["in_w1"] if i + 1 < len(self.layers) else self.final_w1
-            check(L.hsg_add_rmsnorm(hidden.data_ptr(), mix.data_ptr(), nxt.data_ptr(), eps, normed.data_ptr(), tb, H,
-                                    st), "hsg_add_rmsnorm")
+            pending.append((mix, nxt))
+        # the final norm feeds the heads' addmm
+        mx, w1 = pending.pop()
+        check(L.hsg_add_rmsnorm(hid[0].data_ptr(), mx.data_ptr(), w1.data_ptr(), eps, normed.data_ptr(), tb, H, st),
+              "hsg_add_rmsnorm")
         R, E = len(self.roles), cfg.head_hidden
         y = self._view("head", tb, R * E)
         torch.addmm(self.head_b1, normed, self.head_w1.t(), out=y)

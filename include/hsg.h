@@ -419,6 +419,29 @@ int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_
 int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd, int32_t M,
                          int32_t N, int32_t K, void* stream);
 
+/*
+ * The MLP's down projection of a tick of at most HSG_GEMM_SKINNY_M_MAX tokens with the SiLU gate applied on the fly:
+ * D[M, N] = act . W[N, K]^T with act[m, k] = bf16(bf16(silu(gate_up[m, k])) * gate_up[m, K + k]), i.e.
+ * hsg_silu_mul (width K) followed by hsg_gemm_bf16_skinny, bitwise, in one launch and without act in memory.
+ * Replaces silu_mul + down_proj (src/hs_guard/engine/slot_engine_v8.py:52-53; fused_kernels.py:86). ld_gu (>= 2 K) is
+ * gate_up's row stride; requirements and errors as hsg_gemm_bf16_skinny.
+ */
+int hsg_gemm_bf16_skinny_silu(const void* gate_up, int64_t ld_gu, const void* W, int64_t ldw, void* D, int64_t ldd,
+                              int32_t M, int32_t N, int32_t K, void* stream);
+
+/*
+ * The residual add + RMSNorm of a tick of at most HSG_GEMM_SKINNY_M_MAX tokens inside the product that reads it:
+ * hidden_out = bf16(hidden + mix), D[M, N] = norm . W[N, K]^T with norm = bf16((hidden_out * rsqrt(mean(hidden_out^2)
+ * + eps)) * w1), i.e. hsg_add_rmsnorm (w1 fp32 [K]) followed by hsg_gemm_bf16_skinny, bitwise, in one launch.
+ * Replaces add_square + rms_finish + the Linear that reads the norm (src/hs_guard/engine/slot_engine_v8.py:49-52,
+ * 53-55; fused_kernels.py:44,67). Supported: K == 1024 (HSG_ERR_SHAPE). hidden_out must not overlap
+ * hidden or mix (every workgroup reads them; workgroup 0 writes hidden_out). Other requirements and errors as
+ * hsg_gemm_bf16_skinny, with mix, w1 and hidden_out 16-byte aligned and ldm, ldo multiples of 8.
+ */
+int hsg_gemm_bf16_skinny_addnorm(const void* hidden, int64_t ldh, const void* mix, int64_t ldm, const float* w1,
+                                 float eps, void* hidden_out, int64_t ldo, const void* W, int64_t ldw, void* D,
+                                 int64_t ldd, int32_t M, int32_t N, int32_t K, void* stream);
+
 /* hipBLASLt's version on the current device (solution indices are valid only for the version they came from). */
 int hsg_gemm_blas_version(void);
 

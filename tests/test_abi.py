@@ -117,3 +117,11 @@ def test_argument_errors_are_rejected_before_launch():
     assert L.hsg_gemm_bf16_skinny(256, 1020, 256, 1020, 256, 64, 1, 64, 1020, None) == -2
     assert L.hsg_gemm_bf16_skinny(258, 1024, 256, 1024, 256, 64, 1, 64, 1024, None) == -2
     assert L.hsg_gemm_bf16_skinny(256, 1000, 256, 1024, 256, 64, 1, 64, 1024, None) == -1   # lda < K
+    # the SiLU-gated variant needs the gate|up row (2 K) within the row stride
+    assert L.hsg_gemm_bf16_skinny_silu(256, 1024, 256, 1024, 256, 64, 1, 64, 1024, None) == -1
+    assert L.hsg_gemm_bf16_skinny_silu(256, 2048, 256, 1024, 256, 64, 9, 64, 1024, None) == -3
+    # the add + RMSNorm variant: K must be 1024, the residual output a separate buffer
+    assert L.hsg_gemm_bf16_skinny_addnorm(256, 1024, 256, 1024, 256, 1e-6, 512, 1024, 256, 1024, 256, 64, 1, 64, 512,
+                                          None) == -3
+    assert L.hsg_gemm_bf16_skinny_addnorm(256, 1024, 256, 1024, 256, 1e-6, 256, 1024, 256, 1024, 256, 64, 1, 64, 1024,
+                                          None) == -1

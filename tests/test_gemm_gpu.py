@@ -259,3 +259,83 @@ def test_engine_mm_routes_small_products_to_the_skinny_kernel():
         assert torch.equal(got0, ref0), M
     with pytest.raises(ValueError):
         SlotStreamEngine(model, 4, use_graphs=False, gemm_skinny_rows=9)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_skinny_silu_equals_silu_mul_then_skinny(M):
+    """hsg_gemm_bf16_skinny_silu (the SiLU gate applied while staging A) is bitwise hsg_silu_mul followed by
+    hsg_gemm_bf16_skinny, at the MLP's down projection and at ragged shapes with a padded gate|up row stride."""
+    from hs_guard._lib import lib
+    L = lib()
+    st = torch.cuda.current_stream().cuda_stream
+    print(f"[gemm] skinny silu M={M}", flush=True)
+    for N, K, pad in ((1024, 3584, 0), (1027, 1016, 8), (9, 4104, 16)):
+        gen = torch.Generator(device="cuda").manual_seed(100 + M)
+        gu = (torch.randn(M, 2 * K + pad, generator=gen, device="cuda") * 2).bfloat16()
+        W = (torch.randn(N, K, generator=gen, device="cuda") * 0.02).bfloat16()
+        act = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+        assert L.hsg_silu_mul(gu.data_ptr(), gu.stride(0), K, act.data_ptr(), M, st) == 0
+        rc, ref = _skinny(act, W)
+        got = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        rc2 = L.hsg_gemm_bf16_skinny_silu(gu.data_ptr(), gu.stride(0), W.data_ptr(), K, got.data_ptr(), N, M, N, K,
+                                          st)
+        torch.cuda.synchronize()
+        assert rc == 0 and rc2 == 0, (M, N, K)
+        assert torch.equal(got, ref), (M, N, K)
+        assert _within_rounding(got, act, W) == 0, (M, N, K)
+
+
+def test_engine_mm_silu_both_routes():
+    """The engine's mm_silu: one fused launch at M <= 8, hsg_silu_mul + mm above; both equal the two-step product."""
+    from hs_guard._lib import lib
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from hs_guard.model import GuardConfig, GuardModel
+    cfg = GuardConfig(vocab_size=1000, hidden_size=1024, num_hidden_layers=4, intermediate_size=1024,
+                      linear_num_key_heads=2, linear_num_value_heads=4, num_attention_heads=8,
+                      num_key_value_heads=2, window_tokens=32)
+    eng = SlotStreamEngine(GuardModel.random(cfg, seed=0, device="cuda"), 4, use_graphs=False)
+    w = eng.layers[0]["w_down"]
+    N, I = w.shape
+    st = torch.cuda.current_stream().cuda_stream
+    for M in (1, 8, 16):
+        gu = torch.randn(M, 2 * I, device="cuda").bfloat16()
+        act = torch.full((M, I), float("nan"), dtype=torch.bfloat16, device="cuda")
+        got = eng.mm_silu(gu, w, torch.empty(M, N, dtype=torch.bfloat16, device="cuda"), act)
+        act_ref = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+        assert lib().hsg_silu_mul(gu.data_ptr(), 2 * I, I, act_ref.data_ptr(), M, st) == 0
+        ref = eng.mm(act_ref, w, torch.empty(M, N, dtype=torch.bfloat16, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), M
+        assert bool(torch.isnan(act).all()) == (M <= 8), M      # the fused route leaves act unwritten
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_skinny_addnorm_equals_add_rmsnorm_then_skinny(M):
+    """hsg_gemm_bf16_skinny_addnorm (residual add + RMSNorm while staging A) is bitwise hsg_add_rmsnorm followed by
+    hsg_gemm_bf16_skinny: the same product, the new residual in the output buffer, the input residual untouched;
+    at the wide projections (two columns per wave) and a narrow ragged N."""
+    from hs_guard._lib import lib
+    L = lib()
+    st = torch.cuda.current_stream().cuda_stream
+    H = 1024
+    print(f"[gemm] skinny addnorm M={M}", flush=True)
+    for N in (8448, 7168, 37):
+        gen = torch.Generator(device="cuda").manual_seed(200 + M)
+        hidden = (torch.randn(M, H, generator=gen, device="cuda") * 3).bfloat16()
+        mix = torch.randn(M, H, generator=gen, device="cuda").bfloat16()
+        w1 = 1 + 0.1 * torch.randn(H, generator=gen, device="cuda")
+        W = (torch.randn(N, H, generator=gen, device="cuda") * 0.02).bfloat16()
+        h_ref, normed = hidden.clone(), torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
+        assert L.hsg_add_rmsnorm(h_ref.data_ptr(), mix.data_ptr(), w1.data_ptr(), 1e-6, normed.data_ptr(), M, H,
+                                 st) == 0
+        rc, ref = _skinny(normed, W)
+        h_in = hidden.clone()
+        h_out = torch.full((M, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+        got = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        rc2 = L.hsg_gemm_bf16_skinny_addnorm(h_in.data_ptr(), H, mix.data_ptr(), H, w1.data_ptr(), 1e-6,
+                                             h_out.data_ptr(), H, W.data_ptr(), H, got.data_ptr(), N, M, N, H, st)
+        torch.cuda.synchronize()
+        assert rc == 0 and rc2 == 0, (M, N)
+        assert torch.equal(got, ref), (M, N)
+        assert torch.equal(h_out, h_ref), (M, N)
+        assert torch.equal(h_in, hidden), (M, N)
