@@ -630,6 +630,10 @@ def main():
     ap.add_argument("--lone-row-only", action="store_true",
                     help="only the GDN slot step on one 64-token row at --gdn-burst-min (profiled under rocprofv3 "
                          "--pmc)")
+    ap.add_argument("--single-token-only", action="store_true",
+                    help="only the single-token step latency: slot 0 of the --slots engine after a 512-token context, "
+                         "--warmup + --steps timed steps (the command whose kernel statistics give the single-token "
+                         "breakdown)")
     ap.add_argument("--mixed-only", action="store_true",
                     help="only the prefill and the mixed steps (no kernel legs, decode legs, context sweep or CPU "
                          "baseline): the command whose kernel statistics give the per-step kernel breakdown")
@@ -712,6 +716,22 @@ def main():
         eng.chunk_min_tokens = args.chunk_min_tokens   # before the first tick: every graph is captured with it
     if args.gdn_burst_min is not None:
         eng.gdn_burst_min = args.gdn_burst_min   # before the first tick, as chunk_min_tokens
+    if args.single_token_only:
+        rng1 = np.random.default_rng(args.seed + 1)
+        eng.step([(0, rng1.integers(0, cfg.vocab_size, 512).tolist())])
+        one = []
+        for i in range(args.warmup + args.steps):
+            req = [(0, [int(rng1.integers(0, cfg.vocab_size))])]
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            eng.step_packed(req)
+            torch.cuda.synchronize()
+            if i >= args.warmup:
+                one.append((time.perf_counter() - t) * 1e3)
+        print(json.dumps({"single_token_ms": {"p50": round(percentile(one, 50), 3),
+                                              "p95": round(percentile(one, 95), 3)},
+                          "slots": args.slots, "context": 512, "steps": len(one)}), flush=True)
+        return
     load = MixedServingLoad(slots=args.slots, vocab=cfg.vocab_size, seed=args.seed,
                             contexts=tuple(int(x) for x in args.contexts.split(",")), reset_p=args.reset_p)
 
