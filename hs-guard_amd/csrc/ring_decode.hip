@@ -749,8 +749,10 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
   using namespace hsg;
   if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
-  // the workspace is the split-K path's (groups > 8); the fused kernel below that neither needs nor reads it
-  const bool split = groups > 8;
+  // the split-K path: always above 8 query heads per kv head; up to 8 for a few rows when the caller gives a workspace
+  // (a row's ring then spreads over 4 workgroups). The fused kernel neither needs nor reads the workspace.
+  const bool split = groups > 8 || (workspace && (int64_t)n_rows * hkv <= HSG_RING_DECODE_SPLIT_UNITS &&
+                                    workspace_bytes >= hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window));
   if (!q || !ring_k || !ring_v || !new_k || !new_v || !ring_pos || !slots || !starts || !lens || !out ||
       (split && !workspace))
     return HSG_ERR_ARG;
@@ -837,16 +839,17 @@ extern "C" int hsg_ring_decode_noalloc(const void* q, int64_t q_sn, int64_t q_sl
                                        int64_t o_sg, void* stream) {
   if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
   if (n_rows == 0) return HSG_OK;
-  // only the split-K path (groups > 8) uses the workspace, so only it is bounded by the scratch
+  // the scratch bounds only the split-K path above 8 query heads per kv head (up to 8 it runs for at most
+  // HSG_RING_DECODE_SPLIT_UNITS rows x kv heads, which the scratch always holds)
   if (groups > 8 &&
       hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) > (size_t)HSG_RING_DECODE_SCRATCH_BYTES)
     return HSG_ERR_SHAPE;
   void* ws = nullptr;
   const int rc = current_scratch(&ws);
   if (rc != HSG_OK) return rc;
-  // the fused kernel (up to 8 query heads per kv head) does not touch the workspace; the split-K kernels write
-  // every workspace word they read (scores of visible blocks, every block maximum, every split's partial sums),
-  // so nothing left by an earlier call is read and nothing needs clearing
+  // the fused kernel does not touch the workspace; the split-K kernels write every workspace word they read
+  // (scores of visible blocks, every block maximum, every split's partial sums), so nothing left by an earlier call
+  // is read and nothing needs clearing
   return hsg_ring_decode(q, q_sn, q_sl, q_sh, q_sg, ring_k, ring_v, ring_rows, window, new_k, nk_sn, nk_sl, nk_sh,
                          new_v, nv_sn, nv_sl, nv_sh, gate, g_sn, g_sl, g_sh, g_sg, g_off, ring_pos, slots, starts,
                          lens, offsets, n_rows, hkv, groups, head_dim, scale, write_ring, out, o_sn, o_sl, o_sh,

@@ -186,13 +186,17 @@ int hsg_ring_attention(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, 
  * recovered as the prefix maximum of the block maxima, so the blocks are processed in parallel. groups <= 8:
  * one launch on `stream` (one workgroup per row and kv head, scores in LDS, the workspace untouched); groups
  * 9..16: three launches (scores and block maxima per quarter of the ring columns into the workspace; per-block
- * probabilities times values; combine, gate, ring write). Packed layout: rows with lens[n] != 1 are not
- * touched. Padded layout: rows with lens[n] == 0 (or a slot outside [0, ring_rows)) get zero outputs.
- * workspace (groups > 8 only; ignored, and may be NULL, up to 8): device memory of at least
+ * probabilities times values; combine, gate, ring write). With groups <= 8, calls of at most
+ * HSG_RING_DECODE_SPLIT_UNITS rows x kv heads that pass a large enough workspace also take the three launches:
+ * there a row's ring is read by 4 workgroups instead of 1 (one CU moves only a few tens of GB/s of it), e.g. a
+ * lone row at W = 512 in 16 instead of 21.5 us. Packed layout: rows with lens[n] != 1 are not touched. Padded
+ * layout: rows with lens[n] == 0 (or a slot outside [0, ring_rows)) get zero outputs.
+ * workspace (required for groups > 8; up to 8 optional, may be NULL): device memory of at least
  * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) bytes, 16-byte aligned; its contents need no
  * initialisation and are garbage afterwards. Supported: head_dim == 256, window <= 512 and a multiple of 32,
  * groups <= 16.
  */
+#define HSG_RING_DECODE_SPLIT_UNITS 64
 size_t hsg_ring_decode_workspace_bytes(int32_t n_rows, int32_t hkv, int32_t groups, int32_t window);
 int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int64_t q_sg, void* ring_k,
                     void* ring_v, int64_t ring_rows, int32_t window, const void* new_k, int64_t nk_sn,
@@ -210,8 +214,9 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
  * static device array of HSG_RING_DECODE_SCRATCH_BYTES, one copy per GPU, held until the process ends; its
  * device address is looked up on the first call made on each device (make that first call outside graph
  * capture). Arguments, outputs and
- * numerics are those of hsg_ring_decode, bit for bit. Up to 8 query heads per kv head the call runs the fused kernel,
- * which uses no workspace, and takes any number of rows; above that it returns HSG_ERR_SHAPE when
+ * numerics are those of hsg_ring_decode, bit for bit (with the scratch as its workspace). Up to 8 query heads per kv
+ * head the call runs the fused kernel, which uses no workspace, and takes any number of rows (the three-launch path of
+ * at most HSG_RING_DECODE_SPLIT_UNITS rows x kv heads fits the scratch); above that it returns HSG_ERR_SHAPE when
  * hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window) exceeds the scratch (48 MiB: 122 rows at 4 kv heads,
  * G = 16, W = 512). All calls on one GPU share its scratch, so calls that overlap on one GPU (two streams, or two
  * threads) race and must be serialised by the caller; nothing left by an earlier call is read.

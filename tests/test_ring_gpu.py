@@ -152,6 +152,53 @@ def test_split_k_decode_matches_oracle_and_tiled_kernel(G, W):
         np.testing.assert_array_equal(rv, rv_ref)
 
 
+@pytest.mark.parametrize("G,W", [(4, 512), (8, 128), (2, 256)])
+def test_few_row_decode_with_workspace_takes_split_k(G, W):
+    """Up to 8 query heads per kv head, a call of at most HSG_RING_DECODE_SPLIT_UNITS rows x kv heads that passes a
+    workspace runs the three split-K kernels: against the blockwise oracle, and against the fused kernel (the same
+    call without a workspace) within one bf16 rounding; ring writes bit-exact both ways."""
+    from hs_guard._lib import lib
+    print(f"[ring] few-row split-K decode G={G} W={W}", flush=True)
+    L = lib()
+    N, Hkv, S, D = 6, 2, 8, 256
+    assert N * Hkv <= 64
+    fills = [W, W // 2, 0, 5, W - 1, W]
+    lens = [1, 1, 1, 1, 0, 1]
+    q, ring_k, ring_v, new_k, value, gate, ring_pos, slots, starts, lens_t = _decode_case(31 + G, N, Hkv, G, W, S,
+                                                                                         fills, lens)
+    dev = torch.device("cuda:0")
+    d = {n: t.to(dev) for n, t in dict(q=q, new_k=new_k, value=value, gate=gate, ring_pos=ring_pos, slots=slots,
+                                         starts=starts, lens=lens_t).items()}
+    st = torch.cuda.current_stream().cuda_stream
+    m = G
+    outs, rings = [], []
+    for with_ws in (True, False):
+        rk, rv = ring_k.to(dev), ring_v.to(dev)
+        out = torch.zeros(N, 1, Hkv * G * D, dtype=torch.bfloat16, device=dev)
+        need = L.hsg_ring_decode_workspace_bytes(N, Hkv, G, W)
+        ws = torch.empty(need, dtype=torch.uint8, device=dev) if with_ws else None
+        rc = L.hsg_ring_decode(
+            d["q"].data_ptr(), Hkv * m * D, D, m * D, D, rk.data_ptr(), rv.data_ptr(), S, W,
+            d["new_k"].data_ptr(), Hkv * D, D, D, d["value"].data_ptr(), d["value"].stride(0), d["value"].stride(1), D,
+            d["gate"].data_ptr(), d["gate"].stride(0), d["gate"].stride(1), G * 2 * D, 2 * D, D,
+            d["ring_pos"].data_ptr(), d["slots"].data_ptr(), d["starts"].data_ptr(), d["lens"].data_ptr(), None,
+            N, Hkv, G, D, D ** -0.5, 1, out.data_ptr(), Hkv * G * D, Hkv * G * D, G * D, D,
+            ws.data_ptr() if with_ws else None, need if with_ws else 0, st)
+        torch.cuda.synchronize()
+        assert rc == 0, rc
+        outs.append(_np(out))
+        rings.append((_np(rk), _np(rv)))
+    ref, _, rk_ref, rv_ref = oring.ring_attention_v8(
+        _np(q), _np(ring_k), _np(ring_v), _np(new_k), _np(value), _np(gate), ring_pos.numpy(), slots.numpy(),
+        starts.numpy(), lens_t.numpy(), D ** -0.5, W, True)
+    _check(outs[0], ref, what="split-K (workspace) vs oracle")
+    _check(outs[0], outs[1], rtol=2.0 ** -8, what="split-K vs fused")
+    assert np.count_nonzero(outs[0][4]) == 0            # lens 0 row
+    for rk, rv in rings:
+        np.testing.assert_array_equal(rk, rk_ref)
+        np.testing.assert_array_equal(rv, rv_ref)
+
+
 def test_mixed_packed_tick_split_between_kernels():
     """A packed tick with single- and multi-step rows: hsg_ring_decode takes the single-step rows and
     hsg_ring_attention (min_len 2) the rest; the result equals hsg_ring_attention on every row (min_len 0)
