@@ -7,10 +7,12 @@
  * as the numpy route in hs_guard/engine/slot_engine.py (pack_ticks, padded_rows), which stays the reference
  * for the tests:
  *
- *   scan(requests, max_slots, vocab) -> (n, total, max_len), or None when a request would fail the tick's checks
- *       (a slot outside [0, max_slots), a slot twice, an empty request, a token id that is not an integer in
- *       [0, vocab)); the caller then runs its own checks, which raise the reference's errors
- *       (src/hs_guard/runtime.py:148-174; docs/ENGINE.md:9 requires in-vocabulary ids).
+ *   scan(requests, max_slots, vocab[, strict]) -> (n, total, max_len), or None when a request would fail the
+ *       tick's checks (a slot outside [0, max_slots), a slot twice, an empty request, a token id that is not an
+ *       integer in [0, vocab)); the caller then runs its own checks, which raise the reference's errors
+ *       (src/hs_guard/runtime.py:148-174; docs/ENGINE.md:9 requires in-vocabulary ids). strict: slots and ids
+ *       must be Python ints (bool included), as the reference's isinstance(x, int) checks have it; otherwise
+ *       numpy integers pass too.
  *   fill(requests, length, nb, tb, max_slots, vocab, out, lens, offsets, slots) -> None (ValueError for an id
  *       outside [0, vocab))
  *       out [2 tb + 4 nb] int64: ids | positions | offsets | lens | slots | starts of the packed tick with the
@@ -65,8 +67,9 @@ static int request_at(PyObject* seq, Py_ssize_t i, long long* slot, PyObject** i
   return 0;
 }
 
-/* every id of a request an integer in [0, vocab) (numpy integers included); 0 otherwise, with no error set */
-static int ids_in_vocab(PyObject* ids, long long vocab) {
+/* every id of a request an integer in [0, vocab) (numpy integers included unless strict); 0 otherwise, with no
+   error set */
+static int ids_in_vocab(PyObject* ids, long long vocab, int strict) {
   PyObject* fast = PySequence_Fast(ids, "token ids must be a sequence");
   if (!fast) {
     PyErr_Clear();
@@ -76,7 +79,8 @@ static int ids_in_vocab(PyObject* ids, long long vocab) {
   PyObject** items = PySequence_Fast_ITEMS(fast);
   int ok = 1;
   for (Py_ssize_t t = 0; t < len && ok; ++t) {
-    if (PyFloat_Check(items[t])) {   /* integers only (bool is an int, as the reference's isinstance check has it) */
+    if (PyFloat_Check(items[t]) || (strict && !PyLong_Check(items[t]))) {
+      /* integers only (bool is an int, as the reference's isinstance check has it) */
       ok = 0;
       break;
     }
@@ -95,7 +99,8 @@ static int ids_in_vocab(PyObject* ids, long long vocab) {
 static PyObject* scan(PyObject* self, PyObject* args) {
   PyObject *requests, *seq;
   long long max_slots, vocab;
-  if (!PyArg_ParseTuple(args, "OLL", &requests, &max_slots, &vocab)) return NULL;
+  int strict = 0;
+  if (!PyArg_ParseTuple(args, "OLL|i", &requests, &max_slots, &vocab, &strict)) return NULL;
   seq = PySequence_Fast(requests, "requests must be a sequence");
   if (!seq) return NULL;
   const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
@@ -113,7 +118,7 @@ static PyObject* scan(PyObject* self, PyObject* args) {
       ok = 0;   /* let the caller's checks report it */
       break;
     }
-    if (request_at(seq, i, &slot, NULL) != 0) {
+    if ((strict && !PyLong_Check(PySequence_Fast_GET_ITEM(item, 0))) || request_at(seq, i, &slot, NULL) != 0) {
       PyErr_Clear();
       ok = 0;
       break;
@@ -125,7 +130,7 @@ static PyObject* scan(PyObject* self, PyObject* args) {
       break;
     }
     if (slot < 0 || slot >= max_slots || seen[slot] || len == 0 ||
-        !ids_in_vocab(PySequence_Fast_GET_ITEM(item, 1), vocab)) {
+        !ids_in_vocab(PySequence_Fast_GET_ITEM(item, 1), vocab, strict)) {
       ok = 0;
       break;
     }

@@ -670,17 +670,28 @@ class SlotStreamEngine(PreparedWeights):
         lb = bucket(int(lens.max()), (1, 2, 4, 8, 16, 32, 64))
         return padded_rows(flat, lens, offsets, lb), lens
 
+    def one_tick(self, scan):
+        """Whether requests whose ``_hostpack.scan`` result is ``scan`` (they passed its checks) fit one tick."""
+        return scan is not None and 0 < scan[0] <= self.max_rows and scan[2] <= self.max_tick_tokens
+
+    @torch.inference_mode()
+    def step_flat(self, requests, scan):
+        """One tick of checked requests (``one_tick(scan)``), host work native: (probabilities [roles, total, 3]
+        float32 with the requests' tokens one after another in request order, lens [n] int64)."""
+        n, total, _ = scan
+        out_np, tb, lens, offsets = self._run_native(requests, n, total)
+        flat = np.empty((len(self.roles), total, 3), dtype=np.float32)
+        _hostpack.gather_rows(out_np, len(self.roles), tb, lens, offsets, flat)
+        return flat, lens
+
     @torch.inference_mode()
     def step(self, requests):
         """requests: list of (slot, token_ids), each slot at most once. Returns {role: [CPU tensor [L_i, 3]]}
         (src/hs_guard/engine/slot_engine_v7.py:147-167)."""
         scan = _hostpack.scan(requests, self.max_slots, self.cfg.vocab_size)
-        if scan is not None and 0 < scan[0] <= self.max_rows and scan[2] <= self.max_tick_tokens:
+        if self.one_tick(scan):
             # one tick (the serving case), host work native: the request-ordered outputs split per role
-            n, total, _ = scan
-            out_np, tb, lens, offsets = self._run_native(requests, n, total)
-            flat = np.empty((len(self.roles), total, 3), dtype=np.float32)
-            _hostpack.gather_rows(out_np, len(self.roles), tb, lens, offsets, flat)
+            flat, lens = self.step_flat(requests, scan)
             probs = torch.from_numpy(flat)
             sizes = lens.tolist()
             return {role: list(torch.split(probs[r], sizes)) for r, role in enumerate(self.roles)}

@@ -119,9 +119,8 @@ class StreamingGuard:
     def reset(self):
         self.engine.reset()
 
-    def step(self, requests, role="assistant"):
-        if role not in ("user", "assistant"):
-            raise ValueError("role must be user or assistant")
+    def _check(self, requests):
+        """The reference's request checks and errors (src/hs_guard/runtime.py:164-171)."""
         slots = [s for s, _ in requests]
         if not requests or len(set(slots)) != len(slots):
             raise ValueError("Each tick requires nonempty requests and unique slots")
@@ -130,15 +129,32 @@ class StreamingGuard:
                 raise ValueError("Slot is outside the allocated range")
             if not ids or any(not isinstance(i, int) or not 0 <= i < self.vocab_size for i in ids):
                 raise ValueError("Each request requires nonempty in-vocabulary integer token IDs")
-        outputs = self.engine.step(requests)[role]
+
+    def step(self, requests, role="assistant"):
+        if role not in ("user", "assistant"):
+            raise ValueError("role must be user or assistant")
+        from .engine.slot_engine import _hostpack
+        eng = self.engine
+        # the checks in C over the request list (Python ints only, as the reference's isinstance checks); the
+        # Python checks run only when one fails, to raise the reference's error
+        scan = _hostpack.scan(requests, self.max_slots, self.vocab_size, 1) if requests else None
+        if scan is None:
+            self._check(requests)
         tau = self.metadata["thresholds"][role]
         # 1 - p(safe) for every position at once (float32, as per row), then cut per request
-        import torch
-        cut = (1 - torch.cat(outputs)[:, 0]).tolist()
+        if eng.one_tick(scan):
+            flat, lens = eng.step_flat(requests, scan)
+            cut = (1 - flat[eng.roles.index(role), :, 0]).tolist()
+            sizes = lens.tolist()
+        else:
+            import torch
+            outputs = eng.step(requests)[role]
+            cut = (1 - torch.cat(outputs)[:, 0]).tolist()
+            sizes = [len(p) for p in outputs]
         records, at = [], 0
-        for (s, _), p in zip(requests, outputs):
-            records.append({"slot": s, "cut_scores": cut[at:at + len(p)], "threshold": tau})
-            at += len(p)
+        for (s, _), k in zip(requests, sizes):
+            records.append({"slot": s, "cut_scores": cut[at:at + k], "threshold": tau})
+            at += k
         return records
 
 

@@ -335,6 +335,10 @@ def test_streaming_guard_api(setup):
         guard.step([(3, [1])])
     with pytest.raises(ValueError):
         guard.step([(0, [cfg.vocab_size])])
+    # a tick shape first captured by step_packed (under inference mode), then stepped through the guard
+    guard.engine.step_packed([(2, ids[:2])])
+    rec = guard.step([(2, ids[2:4])])
+    assert len(rec) == 1 and len(rec[0]["cut_scores"]) == 2
     # the engine's own entry points (step_packed is the serving backend's call) refuse out-of-vocabulary ids too,
     # before anything runs: lengths, rings and state stay as they were
     eng = guard.engine

@@ -50,10 +50,13 @@ class _FakeEngine:
     """The reference's fake-backend pattern (examples/demo/test_batching.py:7-27): scores from an integer
     recurrence instead of a GPU."""
 
-    def __init__(self):
+    roles = ("user", "assistant")
+
+    def __init__(self, one_tick=True):
         import torch
         self.torch = torch
         self.calls = []
+        self.max_rows, self.max_tick_tokens, self.native = 4, 64, one_tick
 
     def step(self, requests):
         self.calls.append(requests)
@@ -64,14 +67,22 @@ class _FakeEngine:
             out.append(p)
         return {"user": out, "assistant": out}
 
+    def one_tick(self, scan):
+        return self.native and scan is not None and scan[0] <= self.max_rows and scan[2] <= self.max_tick_tokens
+
+    def step_flat(self, requests, scan):
+        out = self.step(requests)
+        flat = np.stack([self.torch.cat(out[r]).numpy() for r in self.roles])
+        return flat, np.array([len(ids) for _, ids in requests], dtype=np.int64)
+
     def reset(self):
         self.calls.append("reset")
 
 
-def _guard():
+def _guard(one_tick=True):
     from hs_guard.runtime import StreamingGuard, random_metadata
     g = StreamingGuard.__new__(StreamingGuard)
-    g.engine, g.metadata, g.vocab_size, g.max_slots = _FakeEngine(), random_metadata(), 100, 4
+    g.engine, g.metadata, g.vocab_size, g.max_slots = _FakeEngine(one_tick), random_metadata(), 100, 4
     return g
 
 
@@ -87,25 +98,33 @@ def test_streaming_guard_validation_matches_reference_messages():
              (([(True, [1])], "user"), None),   # bool is an int in Python, as in the reference
              (([(0, [])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
              (([(0, [100])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
-             (([(0, [1.0])], "user"), "Each request requires nonempty in-vocabulary integer token IDs")]
-    for (req, role), msg in cases:
-        if msg is None:
-            g.step(req, role=role)
-            continue
-        with pytest.raises(ValueError, match=msg):
-            g.step(req, role=role)
+             (([(0, [1.0])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
+             # numpy integers are not ints to the reference's isinstance checks
+             (([(0, [np.int64(1)])], "user"), "Each request requires nonempty in-vocabulary integer token IDs"),
+             (([(np.int64(0), [1])], "user"), "Slot is outside the allocated range"),
+             (([(0, [True, 2])], "user"), None)]
+    for one_tick in (True, False):   # the native checks and the Python ones
+        g = _guard(one_tick)
+        for (req, role), msg in cases:
+            if msg is None:
+                g.step(req, role=role)
+                continue
+            with pytest.raises(ValueError, match=msg):
+                g.step(req, role=role)
     for bad in (0, -1, 1.5, "2"):
         with pytest.raises(ValueError, match="max_slots must be a positive integer"):
             StreamingGuard(None, {}, max_slots=bad)
 
 
 def test_streaming_guard_cut_scores():
+    """Records through the one-tick native route equal those through engine.step, bit for bit (1 - p in float32)."""
     g = _guard()
     out = g.step([(2, [3, 4]), (0, [9])], role="assistant")
     assert out[0]["slot"] == 2 and out[1]["slot"] == 0
     np.testing.assert_allclose(out[0]["cut_scores"], [1 - 0.7, 1 - 0.8], rtol=1e-6)
     np.testing.assert_allclose(out[1]["cut_scores"], [1 - 0.9], rtol=1e-6)
     assert out[0]["threshold"] == pytest.approx(0.1117895246)
+    assert _guard(False).step([(2, [3, 4]), (0, [9])], role="assistant") == out
     g.reset()
     assert g.engine.calls[-1] == "reset"
 
@@ -243,6 +262,11 @@ def test_native_host_packing_matches_numpy_route():
                 [(0, [1, 10])], [(0, [-1])], [(0, [np.int64(10)])], [(0, [2.0])], [(0, [np.float32(2)])],
                 [(2, [3]), (0, [1 << 40])]):
         assert _hostpack.scan(bad, 4, 10) is None, bad
+        assert _hostpack.scan(bad, 4, 10, 1) is None, bad
+    # strict: Python ints only (bool included), as the reference's isinstance(x, int) checks
+    assert _hostpack.scan([(0, [1, True]), (True, [2])], 4, 10, 1) == (2, 3, 2)
+    for bad in ([(0, [np.int32(9)])], [(np.int64(0), [1])]):
+        assert _hostpack.scan(bad, 4, 10) is not None and _hostpack.scan(bad, 4, 10, 1) is None, bad
     # fill refuses an out-of-vocabulary id itself (the docs/ENGINE.md:9 contract), before the tick could run
     out, l3 = np.zeros(2 * 8 + 4 * 2, np.int64), np.zeros(2, np.int64)
     with pytest.raises(ValueError, match="in-vocabulary"):
