@@ -74,11 +74,12 @@ def _scratch_cap():
 def test_noalloc_equals_workspace_entry_point(groups):
     """G = 16: the largest first call that fits the scratch, then a much smaller one. G = 4 (the fused kernel, which
     uses no workspace): a first call with more rows than the scratch would hold as a split-K workspace, which the
-    fused path takes, then a smaller one."""
+    fused path takes, then a smaller one. Then a call of at most HSG_RING_DECODE_SPLIT_UNITS rows x kv heads, which
+    both entry points give to the split-K kernels (through the scratch, and through the caller's workspace)."""
     from hs_guard._lib import lib
     unit = lib().hsg_ring_decode_workspace_bytes(1, HKV, groups, W)
     first = _scratch_cap() // unit if groups > 8 else _scratch_cap() // unit + 14
-    for seed, n, slots_total in ((0, first, first + 8), (1, 24, 40)):
+    for seed, n, slots_total in ((0, first, first + 8), (1, 24, 40), (2, 12, 20)):
         print(f"[noalloc] G {groups}, seed {seed}: {n} rows, then the workspace entry point", flush=True)
         inp = _case(seed, n, slots_total, groups)
         a = _call(inp, noalloc=True)
