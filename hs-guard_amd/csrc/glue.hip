@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
   const int d0 = lane * 4;   // D / 64 = 4 dims per lane
   // loads retire in order, so the cos/sin wait only for the rotary inputs; rows past the last head reload the
   // last one and are not stored
-  const float fpos = (float)pos[tok];
+  const int64_t tpos = pos[tok];
   const float ifreq = inv_freq[threadIdx.x & (half - 1)];
   uint2 xw[ROPE_HEADS_PER_WAVE];
 #pragma unroll
@@ -185,56 +185,20 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
     const uint16_t* src = is_a ? a.src + tok * a.src_row + hh * a.src_head : b.src + tok * b.src_row + hh * b.src_head;
     xw[i] = *reinterpret_cast<const uint2*>(src + d0);
   }
-  f32x4_ wa = {0.f, 0.f, 0.f, 0.f}, wb = {0.f, 0.f, 0.f, 0.f};
-  if (a.heads) wa = *reinterpret_cast<const f32x4_*>(a.w1 + d0);
-  if (b.heads) wb = *reinterpret_cast<const f32x4_*>(b.w1 + d0);
-  if (threadIdx.x < half) {
-    const float f = fpos * ifreq;
-    cs_[threadIdx.x] = rbf(cosf(f));
-    sn_[threadIdx.x] = rbf(sinf(f));
-  }
+  f32x4_n wa = {0.f, 0.f, 0.f, 0.f}, wb = {0.f, 0.f, 0.f, 0.f};
+  if (a.heads) wa = *reinterpret_cast<const f32x4_n*>(a.w1 + d0);
+  if (b.heads) wb = *reinterpret_cast<const f32x4_n*>(b.w1 + d0);
+  if (threadIdx.x < half) rope_pair(tpos, ifreq, cs_[threadIdx.x], sn_[threadIdx.x]);
   lds_barrier();
-  // the partner of dim d (d +- half) sits in lane ^ (half / 4) at the same slot
-  const int pmask = PM ? PM : half / 4;
 #pragma unroll
   for (int i = 0; i < ROPE_HEADS_PER_WAVE; ++i) {
     const int head = wave + 4 * i;
     if (head < heads_total) {
       const bool is_a = head < a.heads;
       const int hh = is_a ? head : head - a.heads;
-      const f32x4_ w4 = is_a ? wa : wb;
-      const float eps = is_a ? eps_a : eps_b;
-      float x[4];
-      unpack2(xw[i].x, x[0], x[1]);
-      unpack2(xw[i].y, x[2], x[3]);
-      const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
-      // D == 256 (the entry point rejects others): ss / D is exactly ss * 2^-8
-      const float r = rsqrtf(ss * (1.0f / 256.0f) + eps);
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = rbf((x[e] * r) * w4[e]);
-      float yp[4];
-      if constexpr (PM == 8) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) yp[e] = dpp_<0x128>(y[e]);   // row_ror:8 is lane xor 8 within a 16-lane row
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) yp[e] = __shfl_xor(y[e], pmask, 64);
-      }
-      float o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = d0 + e;
-        if (d < rot) {
-          const int fi = d < half ? d : d - half;
-          const float rh = d < half ? -yp[e] : yp[e];
-          o[e] = __fadd_rn(rbf(y[e] * cs_[fi]), rbf(rh * sn_[fi]));
-        } else {
-          o[e] = y[e];
-        }
-      }
+      const uint2 o = norm_rope_head256<PM>(xw[i], is_a ? wa : wb, is_a ? eps_a : eps_b, cs_, sn_, rot, lane);
       uint16_t* dst = is_a ? a.out + tok * a.out_row + hh * a.out_head : b.out + tok * b.out_row + hh * b.out_head;
-      store4_bf16(dst + d0, o);
+      *reinterpret_cast<uint2*>(dst + d0) = o;
     }
   }
 }

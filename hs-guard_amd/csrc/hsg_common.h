@@ -115,13 +115,65 @@ __device__ __forceinline__ float sum_stride8_dpp(float x) { return add_xor32(add
 // bitwise that of the butterfly, on every lane.
 __device__ __forceinline__ float wave_sum(float x) { return add_xor32(sum32_dpp(x)); }
 
+typedef __attribute__((ext_vector_type(4))) float f32x4_n;
+
+// ---- Per-head RMSNorm(1 + w) and partial rotate-half RoPE of one 256-wide bf16 head row per wave (square_rows +
+// norm_rope, src/hs_guard/engine/fused_kernels.py:237-284). Lane l holds dims 4 l .. 4 l + 3 (x, 8 bytes) and their
+// fp32 weights w4; cs / sn hold the rot / 2 rotary pairs, bf16-rounded. y = bf16(x * rsqrt(mean(x^2) + eps) * w);
+// for d < rot: out = bf16(y cos) + bf16(rot_half(y) sin) (one fp32 add), else out = y. PM: the lane distance of
+// a dim's rotate-half partner (rot / 8) when it is 8 (a DPP row rotate), 0 for any rot (a shuffle). Shared by
+// hsg_norm_rope and the decode that applies it on the fly, so both give the same bits. ----
+__device__ __forceinline__ void rope_pair(int64_t pos, float inv_freq, float& c, float& s) {
+  const float f = (float)pos * inv_freq;
+  c = rbf(cosf(f));
+  s = rbf(sinf(f));
+}
+
+template <int PM>
+__device__ __forceinline__ uint2 norm_rope_head256(uint2 xw, f32x4_n w4, float eps, const float* cs, const float* sn,
+                                                  int rot, int lane) {
+  const int half = rot / 2;
+  const int d0 = 4 * lane;
+  float x[4];
+  unpack2(xw.x, x[0], x[1]);
+  unpack2(xw.y, x[2], x[3]);
+  const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+  // 256 dims: ss / 256 is exactly ss * 2^-8
+  const float r = rsqrtf(ss * (1.0f / 256.0f) + eps);
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = rbf((x[e] * r) * w4[e]);
+  float yp[4];
+  if constexpr (PM == 8) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yp[e] = dpp_<0x128>(y[e]);   // row_ror:8 is lane xor 8 within a 16-lane row
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yp[e] = __shfl_xor(y[e], half / 4, 64);
+  }
+  float o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = d0 + e;
+    if (d < rot) {
+      const int fi = d < half ? d : d - half;
+      const float rh = d < half ? -yp[e] : yp[e];
+      o[e] = __fadd_rn(rbf(y[e] * cs[fi]), rbf(rh * sn[fi]));
+    } else {
+      o[e] = y[e];
+    }
+  }
+  uint2 w;
+  w.x = pack_bf16x2(o[0], o[1]);
+  w.y = pack_bf16x2(o[2], o[3]);
+  return w;
+}
+
 // ---- RMSNorm of one 1024-wide bf16 row per wave (add_square + rms_finish, src/hs_guard/engine/fused_kernels.py:
 // 30-72). Lane l holds elements 8 l .. 8 l + 7 of the row in x[0] and 512 + 8 l .. + 7 in x[1] (16-byte pieces) and
 // the matching fp32 weights w1 in w[0..3]. ADD: x = bf16(x + mix) first (one fp32 add; x is updated in place).
 // Then out = bf16((x * rsqrt(mean(x^2) + eps)) * w1). Shared by hsg_add_rmsnorm and the skinny products that apply
 // the norm while staging their operand, so both give the same bits. ----
-typedef __attribute__((ext_vector_type(4))) float f32x4_n;
-
 __device__ __forceinline__ void unpack8(const u32x4& w, float* x) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) unpack2(w[i], x[2 * i], x[2 * i + 1]);

@@ -62,6 +62,13 @@ struct DecParams {
   float* ws;
   int64_t unit;     // floats of workspace per (row, kv head)
   int sc_stride;    // floats per query head in the score area (W + KB)
+  // hsg_ring_decode_rope: raw q / k rows, their norm weights and the rotary inputs; the scores kernel normalises
+  // and rotates them itself and writes the new keys to k_out (read back as new_k by the combine kernel)
+  const uint16_t* q_raw; int64_t qr_sl, qr_sh;
+  const uint16_t* k_raw; int64_t kr_sl, kr_sh;
+  const float* q_w1; const float* k_w1; float q_eps, k_eps;
+  const int64_t* pos; const float* inv_freq; int rot;
+  uint16_t* k_out;
 };
 
 // Workspace of one (row, kv head): scores [G][W + KB] | block maxima [G][KB] | partial sums [NS][G][D] |
@@ -90,6 +97,11 @@ __device__ __forceinline__ int64_t row_base(const DecParams& p, int64_t sn, int6
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// ROPE (hsg_ring_decode_rope, packed layout): the kv head's G queries and the step's own key arrive raw; the
+// workgroup first gives each the per-head RMSNorm(1 + w) and rotate-half RoPE of hsg_norm_rope (the same
+// norm_rope_head256, one head row per wave, so the bits are those of the separate launch) into LDS, and the last
+// split's workgroup writes the new key to k_out for the combine kernel's ring write.
+template <bool ROPE>
 __global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m16 = lane & 15, g4 = lane >> 4;
@@ -105,6 +117,43 @@ __global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
   float* bm = sc + (int64_t)G * p.sc_stride;
   const int64_t qpos = ri.start;
   const uint16_t* qrow = p.q + row_base(p, p.q_sn, p.q_sl, n, ri.tok) + h * p.q_sh;
+  __shared__ __align__(16) uint16_t qr_s[ROPE ? G_MAX * D : 8];   // the group's queries, normalised and rotated
+  __shared__ __align__(16) uint16_t kr_s[ROPE ? D : 8];           // the step's own key, likewise
+  __shared__ float cs_s[ROPE ? D / 2 : 1], sn_s[ROPE ? D / 2 : 1];
+  if constexpr (ROPE) {
+    // items 0 .. G - 1: query heads h G + g; item G: the own key. Wave w takes items w, w + 4, ...; every load is
+    // issued before the rotary pairs are computed.
+    constexpr int IT = (G_MAX + 1 + 3) / 4;
+    uint2 xw[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int item = min(wave + 4 * i, G);
+      const uint16_t* src = item < G ? p.q_raw + ri.tok * p.qr_sl + (h * G + item) * p.qr_sh
+                                     : p.k_raw + ri.tok * p.kr_sl + h * p.kr_sh;
+      xw[i] = *reinterpret_cast<const uint2*>(src + 4 * lane);
+    }
+    const f32x4_n wq = *reinterpret_cast<const f32x4_n*>(p.q_w1 + 4 * lane);
+    const f32x4_n wk = *reinterpret_cast<const f32x4_n*>(p.k_w1 + 4 * lane);
+    if (threadIdx.x < p.rot / 2)
+      rope_pair(p.pos[ri.tok], p.inv_freq[threadIdx.x], cs_s[threadIdx.x], sn_s[threadIdx.x]);
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int item = wave + 4 * i;
+      if (item <= G) {   // wave-uniform
+        const bool is_q = item < G;
+        const uint2 o = norm_rope_head256<8>(xw[i], is_q ? wq : wk, is_q ? p.q_eps : p.k_eps, cs_s, sn_s, p.rot, lane);
+        if (is_q) {
+          *reinterpret_cast<uint2*>(&qr_s[item * D + 4 * lane]) = o;
+        } else {
+          *reinterpret_cast<uint2*>(&kr_s[4 * lane]) = o;
+          if (s == NS - 1)
+            *reinterpret_cast<uint2*>(p.k_out + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh + 4 * lane) = o;
+        }
+      }
+    }
+    lds_barrier();
+  }
 
   if (wave < bps && b < RB) {
     // Two memory round trips: the block's positions (and the queries), then its keys only if one of them
@@ -120,7 +169,9 @@ __global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
       uint4 w = make_uint4(0u, 0u, 0u, 0u);
-      if (m16 < G) w = *reinterpret_cast<const uint4*>(qrow + m16 * p.q_sg + 32 * ks + 8 * g4);
+      if (m16 < G)
+        w = ROPE ? *reinterpret_cast<const uint4*>(&qr_s[m16 * D + 32 * ks + 8 * g4])
+                 : *reinterpret_cast<const uint4*>(qrow + m16 * p.q_sg + 32 * ks + 8 * g4);
       qb[ks] = __builtin_bit_cast(bf16x8, w);
     }
     bool vis = false;
@@ -163,12 +214,12 @@ __global__ __launch_bounds__(256) void decode_scores_kernel(const DecParams p) {
 
   // the step's own key: block RB, one key, always visible to its own query
   if (s == NS - 1 && wave == 0) {
-    const uint16_t* kn = p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh;
+    const uint16_t* kn = ROPE ? kr_s : p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh;
     float k4[4];
     load4_bf16(kn + 4 * lane, k4);
     for (int g = 0; g < G; ++g) {
       float q4[4];
-      load4_bf16(qrow + g * p.q_sg + 4 * lane, q4);
+      load4_bf16(ROPE ? qr_s + g * D + 4 * lane : qrow + g * p.q_sg + 4 * lane, q4);
       const float part = q4[0] * k4[0] + q4[1] * k4[1] + q4[2] * k4[2] + q4[3] * k4[3];
       const float v = wave_sum(part) * p.scale;
       if (lane == 0) {
@@ -788,7 +839,64 @@ extern "C" int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_
     else hipLaunchKernelGGL(decode_fused_kernel<8>, dim3(units), dim3(256), 0, st, p);
     return launch_status();
   }
-  hipLaunchKernelGGL(decode_scores_kernel, dim3(units * NS), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(decode_scores_kernel<false>, dim3(units * NS), dim3(256), 0, st, p);
+  if (groups <= 4) hipLaunchKernelGGL(decode_values_kernel<4>, dim3(units * NS), dim3(256), 0, st, p);
+  else if (groups <= 8) hipLaunchKernelGGL(decode_values_kernel<8>, dim3(units * NS), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(decode_values_kernel<16>, dim3(units * NS), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(units), dim3(256), 0, st, p);
+  return launch_status();
+}
+
+extern "C" int hsg_ring_decode_rope(const void* q_raw, int64_t q_row, int64_t q_head, const float* q_w1, float q_eps,
+                                    const void* k_raw, int64_t k_row, int64_t k_head, const float* k_w1, float k_eps,
+                                    const int64_t* pos, const float* inv_freq, int32_t rot, void* k_out,
+                                    int64_t ko_row, void* ring_k, void* ring_v, int64_t ring_rows, int32_t window,
+                                    const void* new_v, int64_t nv_row, int64_t nv_head, const void* gate,
+                                    int64_t g_row, int64_t g_head, int64_t g_group, int64_t g_off,
+                                    const int64_t* ring_pos, const int64_t* slots, const int64_t* starts,
+                                    const int64_t* lens, const int64_t* offsets, int32_t n_rows, int32_t hkv,
+                                    int32_t groups, int32_t head_dim, float scale, int32_t write_ring, void* out,
+                                    int64_t o_row, int64_t o_head, int64_t o_group, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  using namespace hsg;
+  if (n_rows < 0 || hkv <= 0 || groups <= 0 || ring_rows <= 0) return HSG_ERR_ARG;
+  if (n_rows == 0) return HSG_OK;
+  if (!q_raw || !q_w1 || !k_raw || !k_w1 || !pos || !inv_freq || !k_out || !ring_k || !ring_v || !new_v ||
+      !ring_pos || !slots || !starts || !lens || !offsets || !out || !workspace)
+    return HSG_ERR_ARG;
+  if (head_dim != D || rot != 64 || window <= 0 || window > W_MAX || window % KB != 0 || groups > G_MAX ||
+      workspace_bytes < hsg_ring_decode_workspace_bytes(n_rows, hkv, groups, window))
+    return HSG_ERR_SHAPE;
+  const int64_t s8[] = {q_row, q_head, k_row, k_head, ko_row, nv_row, nv_head, g_row, g_head, g_group, g_off, o_row,
+                        o_head, o_group};
+  for (int64_t v : s8)
+    if (v % 4) return HSG_ERR_ALIGN;
+  if (!aligned(q_raw, 8) || !aligned(k_raw, 8) || !aligned(k_out, 8) || !aligned(q_w1, 16) || !aligned(k_w1, 16) ||
+      !aligned(ring_k, 16) || !aligned(ring_v, 16) || !aligned(new_v, 8) || !aligned(out, 8) ||
+      (gate && !aligned(gate, 8)) || !aligned(workspace, 16))
+    return HSG_ERR_ALIGN;
+  DecParams p{};
+  p.q = static_cast<const uint16_t*>(q_raw);   // not read: the scores kernel takes q_raw
+  p.ring_k = static_cast<uint16_t*>(ring_k); p.ring_v = static_cast<uint16_t*>(ring_v);
+  p.ring_rows = ring_rows; p.W = window;
+  p.new_k = static_cast<const uint16_t*>(k_out); p.nk_sl = ko_row; p.nk_sh = D;   // the combine's ring write
+  p.new_v = static_cast<const uint16_t*>(new_v); p.nv_sl = nv_row; p.nv_sh = nv_head;
+  p.gate = static_cast<const uint16_t*>(gate);
+  p.g_sl = g_row; p.g_sh = g_head; p.g_sg = g_group; p.g_off = g_off;
+  p.ring_pos = ring_pos; p.slots = slots; p.starts = starts; p.lens = lens; p.offsets = offsets;
+  p.hkv = hkv; p.G = groups; p.scale = scale; p.write_ring = write_ring;
+  p.out = static_cast<uint16_t*>(out); p.o_sl = o_row; p.o_sh = o_head; p.o_sg = o_group;
+  p.ws = static_cast<float*>(workspace);
+  p.unit = unit_floats(groups, window);
+  p.sc_stride = window + KB;
+  p.q_raw = static_cast<const uint16_t*>(q_raw); p.qr_sl = q_row; p.qr_sh = q_head;
+  p.k_raw = static_cast<const uint16_t*>(k_raw); p.kr_sl = k_row; p.kr_sh = k_head;
+  p.q_w1 = q_w1; p.k_w1 = k_w1; p.q_eps = q_eps; p.k_eps = k_eps;
+  p.pos = pos; p.inv_freq = inv_freq; p.rot = rot;
+  p.k_out = static_cast<uint16_t*>(k_out);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned units = (unsigned)(n_rows * hkv);
+  hipLaunchKernelGGL(decode_scores_kernel<true>, dim3(units * NS), dim3(256), 0, st, p);
   if (groups <= 4) hipLaunchKernelGGL(decode_values_kernel<4>, dim3(units * NS), dim3(256), 0, st, p);
   else if (groups <= 8) hipLaunchKernelGGL(decode_values_kernel<8>, dim3(units * NS), dim3(256), 0, st, p);
   else hipLaunchKernelGGL(decode_values_kernel<16>, dim3(units * NS), dim3(256), 0, st, p);

@@ -90,6 +90,17 @@ SIGNATURES = {
         _I32, _I32, _I32, _I32, _F, _I32,    # n_rows, hkv, groups, head_dim, scale, write_ring
         _P, _I64, _I64, _I64, _I64,          # out, o_sn, o_sl, o_sh, o_sg
         _P, ctypes.c_size_t, _P]),           # workspace, workspace_bytes, stream
+    "hsg_ring_decode_rope": (ctypes.c_int, [
+        _P, _I64, _I64, _P, _F,              # q_raw, q_row, q_head, q_w1, q_eps
+        _P, _I64, _I64, _P, _F,              # k_raw, k_row, k_head, k_w1, k_eps
+        _P, _P, _I32, _P, _I64,              # pos, inv_freq, rot, k_out, ko_row
+        _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window
+        _P, _I64, _I64,                      # new_v, nv_row, nv_head
+        _P, _I64, _I64, _I64, _I64,          # gate, g_row, g_head, g_group, g_off
+        _P, _P, _P, _P, _P,                  # ring_pos, slots, starts, lens, offsets
+        _I32, _I32, _I32, _I32, _F, _I32,    # n_rows, hkv, groups, head_dim, scale, write_ring
+        _P, _I64, _I64, _I64,                # out, o_row, o_head, o_group
+        _P, ctypes.c_size_t, _P]),           # workspace, workspace_bytes, stream
     "hsg_ring_decode_noalloc": (ctypes.c_int, [
         _P, _I64, _I64, _I64, _I64,          # q, q_sn, q_sl, q_sh, q_sg
         _P, _P, _I64, _I32,                  # ring_k, ring_v, ring_rows, window

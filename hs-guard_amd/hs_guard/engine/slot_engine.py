@@ -481,33 +481,49 @@ class SlotStreamEngine(PreparedWeights):
                 q = self._view("q", tb, hq * D)
                 k = self._view("k", tb, hkv * D)
                 base = proj.data_ptr()
-                check(L.hsg_norm_rope(base, self.att_in, 2 * D, hq, Lw["q_w1"].data_ptr(), eps, q.data_ptr(), hq * D,
-                                      D, base + 2 * hq * 2 * D, self.att_in, D, hkv, Lw["k_w1"].data_ptr(), eps,
-                                      k.data_ptr(), hkv * D, D, pos.data_ptr(), self.inv_freq.data_ptr(),
-                                      cfg.rotary_dim, tb, D, st), "hsg_norm_rope")
                 att = self._view("mid", tb, hq * D)
-                # single-step rows: hsg_ring_decode; rows of two or more steps: the tiled kernel (min_len 2)
-                check(L.hsg_ring_decode(
-                    q.data_ptr(), 0, hq * D, G * D, D,
-                    self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
-                    k.data_ptr(), 0, hkv * D, D,
-                    base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
-                    base, 0, self.att_in, G * 2 * D, 2 * D, D,
-                    self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(), offsets.data_ptr(),
-                    nb, hkv, G, D, D ** -0.5, 1,
-                    att.data_ptr(), 0, hq * D, G * D, D, self.ring_ws.data_ptr(), self.ring_ws.numel(), st),
-                    "hsg_ring_decode")
-                if tb >= 2:
-                    # a one-token bucket has no row of two or more steps: its program leaves the tiled kernel out
-                    check(L.hsg_ring_attention(
+                if tb == 1 and cfg.rotary_dim == 64 and D == 256:
+                    # a one-token tick: the q / k norm and RoPE run inside the decode's scores kernel (one launch
+                    # fewer), bitwise hsg_norm_rope + hsg_ring_decode; k receives the new keys
+                    check(L.hsg_ring_decode_rope(
+                        base, self.att_in, 2 * D, Lw["q_w1"].data_ptr(), eps,
+                        base + 2 * hq * 2 * D, self.att_in, D, Lw["k_w1"].data_ptr(), eps,
+                        pos.data_ptr(), self.inv_freq.data_ptr(), cfg.rotary_dim, k.data_ptr(), hkv * D,
+                        self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
+                        base + 2 * (hq * 2 * D + hkv * D), self.att_in, D,
+                        base, self.att_in, G * 2 * D, 2 * D, D,
+                        self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(),
+                        offsets.data_ptr(), nb, hkv, G, D, D ** -0.5, 1,
+                        att.data_ptr(), hq * D, G * D, D, self.ring_ws.data_ptr(), self.ring_ws.numel(), st),
+                        "hsg_ring_decode_rope")
+                else:
+                    check(L.hsg_norm_rope(base, self.att_in, 2 * D, hq, Lw["q_w1"].data_ptr(), eps, q.data_ptr(),
+                                          hq * D, D, base + 2 * hq * 2 * D, self.att_in, D, hkv,
+                                          Lw["k_w1"].data_ptr(), eps, k.data_ptr(), hkv * D, D, pos.data_ptr(),
+                                          self.inv_freq.data_ptr(), cfg.rotary_dim, tb, D, st), "hsg_norm_rope")
+                    # single-step rows: hsg_ring_decode; rows of two or more steps: the tiled kernel (min_len 2)
+                    check(L.hsg_ring_decode(
                         q.data_ptr(), 0, hq * D, G * D, D,
                         self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
                         k.data_ptr(), 0, hkv * D, D,
                         base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
                         base, 0, self.att_in, G * 2 * D, 2 * D, D,
                         self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(),
-                        offsets.data_ptr(), nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
-                        att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
+                        offsets.data_ptr(), nb, hkv, G, D, D ** -0.5, 1,
+                        att.data_ptr(), 0, hq * D, G * D, D, self.ring_ws.data_ptr(), self.ring_ws.numel(), st),
+                        "hsg_ring_decode")
+                    if tb >= 2:
+                        # a one-token bucket has no row of two or more steps: its program leaves the tiled kernel
+                        # out
+                        check(L.hsg_ring_attention(
+                            q.data_ptr(), 0, hq * D, G * D, D,
+                            self.ring_k[idx].data_ptr(), self.ring_v[idx].data_ptr(), S, W,
+                            k.data_ptr(), 0, hkv * D, D,
+                            base + 2 * (hq * 2 * D + hkv * D), 0, self.att_in, D,
+                            base, 0, self.att_in, G * 2 * D, 2 * D, D,
+                            self.ring_pos.data_ptr(), slots.data_ptr(), starts.data_ptr(), lens.data_ptr(),
+                            offsets.data_ptr(), nb, self.max_tick_tokens, hkv, G, D, D ** -0.5, 1, 2,
+                            att.data_ptr(), 0, hq * D, G * D, D, st), "hsg_ring_attention")
                 self.mm(att, Lw["w_out"], mix)
             pending.append((mix, Lw["post_w1"]))
             I = cfg.intermediate_size

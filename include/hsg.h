@@ -208,6 +208,29 @@ int hsg_ring_decode(const void* q, int64_t q_sn, int64_t q_sl, int64_t q_sh, int
                     int64_t o_sh, int64_t o_sg, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * hsg_ring_decode (three-launch split-K path, packed layout) with the attention front's per-head q / k norm and
+ * partial RoPE applied on the fly: replaces square_rows + norm_rope + ring_attention_v8 at the decode shape
+ * (src/hs_guard/engine/fused_kernels.py:237-284,358-376; slot_engine_v8.py:79-85) for a tick's single-step rows,
+ * bitwise hsg_norm_rope followed by hsg_ring_decode's split-K path. q_raw / k_raw: the projection's raw query and
+ * key rows (token t, query head j at q_raw + t q_row + j q_head; kv head h at k_raw + t k_row + h k_head), q_w1 /
+ * k_w1 [head_dim] fp32 (1 + weight), pos [tokens] int64, inv_freq [rot / 2] fp32; the normalised, rotated new keys
+ * are written to k_out (token t, kv head h at k_out + t ko_row + h head_dim) and into the ring. new_v, gate, out
+ * and their strides as hsg_ring_decode's packed-layout arguments (row = token). One launch fewer than the separate
+ * kernels, for ticks of one token (the single-session step). Supported: head_dim 256, rot 64, groups <= 16, the
+ * workspace of hsg_ring_decode_workspace_bytes (required).
+ */
+int hsg_ring_decode_rope(const void* q_raw, int64_t q_row, int64_t q_head, const float* q_w1, float q_eps,
+                         const void* k_raw, int64_t k_row, int64_t k_head, const float* k_w1, float k_eps,
+                         const int64_t* pos, const float* inv_freq, int32_t rot, void* k_out, int64_t ko_row,
+                         void* ring_k, void* ring_v, int64_t ring_rows, int32_t window, const void* new_v,
+                         int64_t nv_row, int64_t nv_head, const void* gate, int64_t g_row, int64_t g_head,
+                         int64_t g_group, int64_t g_off, const int64_t* ring_pos, const int64_t* slots,
+                         const int64_t* starts, const int64_t* lens, const int64_t* offsets, int32_t n_rows,
+                         int32_t hkv, int32_t groups, int32_t head_dim, float scale, int32_t write_ring, void* out,
+                         int64_t o_row, int64_t o_head, int64_t o_group, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
  * hsg_ring_decode without the workspace argument: it allocates nothing. No counterpart in the reference; it is
  * for callers that cannot allocate device memory (code under hipGraph capture, allocation-free serving loops,
  * harnesses that forbid hipMalloc). The workspace (used by the split-K path, groups > 8) is the library's own

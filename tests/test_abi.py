@@ -125,3 +125,11 @@ def test_argument_errors_are_rejected_before_launch():
                                           None) == -3
     assert L.hsg_gemm_bf16_skinny_addnorm(256, 1024, 256, 1024, 256, 1e-6, 256, 1024, 256, 1024, 256, 64, 1, 64, 1024,
                                           None) == -1
+    # decode with on-the-fly norm + RoPE: no workspace, another rotary width (placeholders, never read)
+    rope = [256, 10240, 512, 256, 1e-6, 256, 10240, 256, 256, 1e-6, 256, 256, 64, 256, 1024, 256, 256, 9, 512, 256,
+            10240, 256, 256, 10240, 1024, 512, 256, 256, 256, 256, 256, 256, 2, 4, 4, 256, 0.0625, 1, 256, 4096,
+            1024, 256]
+    need = L.hsg_ring_decode_workspace_bytes(2, 4, 4, 512)
+    assert L.hsg_ring_decode_rope(*rope, None, need, None) == -1
+    rope[12] = 32
+    assert L.hsg_ring_decode_rope(*rope, 256, need, None) == -3

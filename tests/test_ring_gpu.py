@@ -332,3 +332,76 @@ def test_config4_window_fill_64_tokens():
     # the scratch column W takes the padded steps in the reference's scatter; this build never writes it
     np.testing.assert_array_equal(_np(d["ring_k"])[:, :, :W], rk[:, :, :W])
     np.testing.assert_array_equal(_np(d["ring_v"])[:, :, :W], rv[:, :, :W])
+
+
+@pytest.mark.parametrize("hq", [16, 8])
+def test_decode_rope_equals_norm_rope_then_decode(hq):
+    """hsg_ring_decode_rope (q / k norm + RoPE inside the split-K scores kernel) is bitwise hsg_norm_rope followed by
+    hsg_ring_decode on the same packed single-step rows: outputs, the new keys it writes out and both rings; a row
+    with no step is left alone."""
+    from hs_guard._lib import lib
+    L = lib()
+    print(f"[ring] decode with on-the-fly norm + RoPE, hq={hq}", flush=True)
+    gen = torch.Generator().manual_seed(40 + hq)
+    hkv, D, W, S = 4, 256, 512, 9
+    G = hq // hkv
+    lens = torch.tensor([1, 1, 0, 1, 1], dtype=torch.long)
+    N = T = len(lens)
+    att_in = hq * 2 * D + 2 * hkv * D
+    proj = torch.randn(T, att_in, generator=gen).to(torch.bfloat16)
+    ring_k = torch.randn(S, hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    ring_v = torch.randn(S, hkv, W + 1, D, generator=gen).to(torch.bfloat16)
+    slots = torch.randperm(S - 1, generator=gen)[:N]
+    starts = torch.randint(0, 3000, (N,), generator=gen)
+    ring_pos = torch.full((S, W + 1), -1, dtype=torch.long)
+    for s_, st_ in zip(slots.tolist(), starts.tolist()):
+        for p_ in range(max(0, st_ - 450), st_):
+            ring_pos[s_, p_ % W] = p_
+    offsets = torch.arange(N, dtype=torch.long)
+    pos = starts.clone()                      # one step per row: its position is its start
+    qw = 1 + 0.1 * torch.randn(D, generator=gen)
+    kw = 1 + 0.1 * torch.randn(D, generator=gen)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2).float() / 64))
+    dev = torch.device("cuda:0")
+    d = {k: v.to(dev) for k, v in dict(proj=proj, slots=slots, starts=starts, lens=lens, offsets=offsets, pos=pos,
+                                        ring_pos=ring_pos, qw=qw, kw=kw, inv=inv).items()}
+    st = torch.cuda.current_stream().cuda_stream
+    base = d["proj"].data_ptr()
+    kbase, vbase = base + 2 * hq * 2 * D, base + 2 * (hq * 2 * D + hkv * D)
+    need = L.hsg_ring_decode_workspace_bytes(N, hkv, G, W)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    results = []
+    for fused in (False, True):
+        rk, rv = ring_k.to(dev), ring_v.to(dev)
+        out = torch.zeros(T, hq * D, dtype=torch.bfloat16, device=dev)
+        kbuf = torch.zeros(T, hkv * D, dtype=torch.bfloat16, device=dev)
+        common_tail = (rk.data_ptr(), rv.data_ptr(), S, W)
+        if fused:
+            rc = L.hsg_ring_decode_rope(base, att_in, 2 * D, d["qw"].data_ptr(), 1e-6, kbase, att_in, D,
+                                        d["kw"].data_ptr(), 1e-6, d["pos"].data_ptr(), d["inv"].data_ptr(), 64,
+                                        kbuf.data_ptr(), hkv * D, *common_tail, vbase, att_in, D,
+                                        base, att_in, G * 2 * D, 2 * D, D, d["ring_pos"].data_ptr(),
+                                        d["slots"].data_ptr(), d["starts"].data_ptr(), d["lens"].data_ptr(),
+                                        d["offsets"].data_ptr(), N, hkv, G, D, D ** -0.5, 1, out.data_ptr(),
+                                        hq * D, G * D, D, ws.data_ptr(), need, st)
+            assert rc == 0, rc
+        else:
+            q = torch.zeros(T, hq * D, dtype=torch.bfloat16, device=dev)
+            rc = L.hsg_norm_rope(base, att_in, 2 * D, hq, d["qw"].data_ptr(), 1e-6, q.data_ptr(), hq * D, D,
+                                 kbase, att_in, D, hkv, d["kw"].data_ptr(), 1e-6, kbuf.data_ptr(), hkv * D, D,
+                                 d["pos"].data_ptr(), d["inv"].data_ptr(), 64, T, D, st)
+            assert rc == 0, rc
+            rc = L.hsg_ring_decode(q.data_ptr(), 0, hq * D, G * D, D, *common_tail, kbuf.data_ptr(), 0, hkv * D, D,
+                                   vbase, 0, att_in, D, base, 0, att_in, G * 2 * D, 2 * D, D,
+                                   d["ring_pos"].data_ptr(), d["slots"].data_ptr(), d["starts"].data_ptr(),
+                                   d["lens"].data_ptr(), d["offsets"].data_ptr(), N, hkv, G, D, D ** -0.5, 1,
+                                   out.data_ptr(), 0, hq * D, G * D, D, ws.data_ptr(), need, st)
+            assert rc == 0, rc
+        torch.cuda.synchronize()
+        results.append((out.cpu(), kbuf.cpu(), rk.cpu(), rv.cpu()))
+    (o0, k0, rk0, rv0), (o1, k1, rk1, rv1) = results
+    live = lens.numpy() == 1
+    assert torch.equal(o0[live], o1[live])
+    assert torch.equal(k0[live], k1[live])
+    assert torch.equal(rk0, rk1) and torch.equal(rv0, rv1)
+    assert not torch.equal(rk1, ring_k)                 # the steps' keys were written
