@@ -231,13 +231,14 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 // Either way the result is bitwise that of the separate kernel followed by the PLAIN product.
 enum SkinnyMode { PLAIN = 0, SILU = 1, ADDNORM = 2 };
 
-struct SkinnyNorm {          // ADDNORM's extra operands
+struct SkinnyNorm {          // ADDNORM's extra operands, and an optional bias added before the output rounding
   const uint16_t* mix;
   int64_t ldm;
   const float* w1;
   float eps;
   uint16_t* hid_out;
   int64_t ldo;
+  const uint16_t* bias;      // [N] bf16 or null
 };
 
 __device__ __forceinline__ float bf_at(uint32_t w, int hi) {
@@ -370,7 +371,10 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
       const float s = hsg::wave_sum(acc[t][m]);
       if (lane == m) out = s;
     }
-    if (n0 + t < N && lane < M) D[(int64_t)lane * ldd + n0 + t] = hsg::f2bf(out);
+    if (n0 + t < N && lane < M) {
+      if (nx.bias) out += hsg::bf2f(nx.bias[n0 + t]);   // the Linear's bias in fp32, then one rounding
+      D[(int64_t)lane * ldd + n0 + t] = hsg::f2bf(out);
+    }
   }
 }
 
@@ -439,12 +443,15 @@ extern "C" int hsg_gemm_bf16_skinny_silu(const void* gate_up, int64_t ld_gu, con
 extern "C" int hsg_gemm_bf16_skinny_addnorm(const void* hidden, int64_t ldh, const void* mix, int64_t ldm,
                                             const float* w1, float eps, void* hidden_out, int64_t ldo, const void* W,
                                             int64_t ldw, void* D, int64_t ldd, int32_t M, int32_t N, int32_t K,
-                                            void* stream) {
+                                            const void* bias, void* stream) {
   using namespace hsg;
   if (!mix || !w1 || !hidden_out || hidden_out == hidden || ldm < K || ldo < K) return HSG_ERR_ARG;
   if (K != 1024) return HSG_ERR_SHAPE;
-  if (ldm % 8 || ldo % 8 || !aligned(mix, 16) || !aligned(w1, 16) || !aligned(hidden_out, 16)) return HSG_ERR_ALIGN;
-  const SkinnyNorm nx{static_cast<const uint16_t*>(mix), ldm, w1, eps, static_cast<uint16_t*>(hidden_out), ldo};
+  if (ldm % 8 || ldo % 8 || !aligned(mix, 16) || !aligned(w1, 16) || !aligned(hidden_out, 16) ||
+      (bias && !aligned(bias, 2)))
+    return HSG_ERR_ALIGN;
+  const SkinnyNorm nx{static_cast<const uint16_t*>(mix), ldm, w1, eps, static_cast<uint16_t*>(hidden_out), ldo,
+                      static_cast<const uint16_t*>(bias)};
   return launch_skinny<ADDNORM>(hidden, ldh, W, ldw, D, ldd, M, N, K, nx, stream);
 }
 

@@ -135,7 +135,7 @@ SIGNATURES = {
     "hsg_gemm_bf16_skinny_silu": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _I32,
                                                  _P]),   # gate_up, ld_gu, W, ldw, D, ldd, M, N, K, stream
     "hsg_gemm_bf16_skinny_addnorm": (ctypes.c_int, [_P, _I64, _P, _I64, _P, _F, _P, _I64, _P, _I64, _P, _I64, _I32,
-                                                    _I32, _I32, _P]),
+                                                    _I32, _I32, _P, _P]),
     "hsg_gemm_candidates": (ctypes.c_int, [_I32, _I32, _I32, _P, _P, _I32, ctypes.c_size_t]),
     "hsg_gemm_blas_version": (ctypes.c_int, []),
 }

@@ -422,7 +422,7 @@ class SlotStreamEngine(PreparedWeights):
             if fuse and self._skinny(normed, w, H):
                 check(L.hsg_gemm_bf16_skinny_addnorm(hid[0].data_ptr(), H, mx.data_ptr(), H, w1.data_ptr(), eps,
                                                      hid[1].data_ptr(), H, w.data_ptr(), w.stride(0),
-                                                     out.data_ptr(), out.stride(0), tb, w.shape[0], H, st),
+                                                     out.data_ptr(), out.stride(0), tb, w.shape[0], H, None, st),
                       "hsg_gemm_bf16_skinny_addnorm")
                 hid.reverse()
                 return out
@@ -532,13 +532,20 @@ class SlotStreamEngine(PreparedWeights):
             self.mm_silu(gu, Lw["w_down"], mix, self._view("mid", tb, I))
             nxt = self.layers[i + 1]["in_w1"] if i + 1 < len(self.layers) else self.final_w1
             pending.append((mix, nxt))
-        # the final norm feeds the heads' addmm
+        # the final norm feeds the heads' first Linear (with bias): one skinny launch in small ticks, else the norm
+        # and torch.addmm
         mx, w1 = pending.pop()
-        check(L.hsg_add_rmsnorm(hid[0].data_ptr(), mx.data_ptr(), w1.data_ptr(), eps, normed.data_ptr(), tb, H, st),
-              "hsg_add_rmsnorm")
         R, E = len(self.roles), cfg.head_hidden
         y = self._view("head", tb, R * E)
-        torch.addmm(self.head_b1, normed, self.head_w1.t(), out=y)
+        if fuse and self._skinny(normed, self.head_w1, H):
+            check(L.hsg_gemm_bf16_skinny_addnorm(hid[0].data_ptr(), H, mx.data_ptr(), H, w1.data_ptr(), eps,
+                                                 hid[1].data_ptr(), H, self.head_w1.data_ptr(), self.head_w1.stride(0),
+                                                 y.data_ptr(), y.stride(0), tb, R * E, H, self.head_b1.data_ptr(), st),
+                  "hsg_gemm_bf16_skinny_addnorm")
+        else:
+            check(L.hsg_add_rmsnorm(hid[0].data_ptr(), mx.data_ptr(), w1.data_ptr(), eps, normed.data_ptr(), tb, H,
+                                    st), "hsg_add_rmsnorm")
+            torch.addmm(self.head_b1, normed, self.head_w1.t(), out=y)
         probs = self._view("probs", R, tb, 3)
         check(L.hsg_risk_head(y.data_ptr(), R * E, self.head_ln_w.data_ptr(), self.head_ln_b.data_ptr(),
                               self.head_w2.data_ptr(), self.head_b2.data_ptr(), cfg.layer_norm_eps, R, E,

@@ -464,11 +464,13 @@ int hsg_gemm_bf16_skinny_silu(const void* gate_up, int64_t ld_gu, const void* W,
  * Replaces add_square + rms_finish + the Linear that reads the norm (src/hs_guard/engine/slot_engine_v8.py:49-52,
  * 53-55; fused_kernels.py:44,67). Supported: K == 1024 (HSG_ERR_SHAPE). hidden_out must not overlap
  * hidden or mix (every workgroup reads them; workgroup 0 writes hidden_out). Other requirements and errors as
- * hsg_gemm_bf16_skinny, with mix, w1 and hidden_out 16-byte aligned and ldm, ldo multiples of 8.
+ * hsg_gemm_bf16_skinny, with mix, w1 and hidden_out 16-byte aligned and ldm, ldo multiples of 8. bias ([N] bf16, or
+ * NULL): added to the fp32 sum before its bf16 rounding, for a Linear with bias (the risk heads' first projection,
+ * src/hs_guard/engine/slot_engine_v7.py:58-61, after the final norm).
  */
 int hsg_gemm_bf16_skinny_addnorm(const void* hidden, int64_t ldh, const void* mix, int64_t ldm, const float* w1,
                                  float eps, void* hidden_out, int64_t ldo, const void* W, int64_t ldw, void* D,
-                                 int64_t ldd, int32_t M, int32_t N, int32_t K, void* stream);
+                                 int64_t ldd, int32_t M, int32_t N, int32_t K, const void* bias, void* stream);
 
 /* hipBLASLt's version on the current device (solution indices are valid only for the version they came from). */
 int hsg_gemm_blas_version(void);

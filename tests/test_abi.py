@@ -122,9 +122,9 @@ def test_argument_errors_are_rejected_before_launch():
     assert L.hsg_gemm_bf16_skinny_silu(256, 2048, 256, 1024, 256, 64, 9, 64, 1024, None) == -3
     # the add + RMSNorm variant: K must be 1024, the residual output a separate buffer
     assert L.hsg_gemm_bf16_skinny_addnorm(256, 1024, 256, 1024, 256, 1e-6, 512, 1024, 256, 1024, 256, 64, 1, 64, 512,
-                                          None) == -3
+                                          None, None) == -3
     assert L.hsg_gemm_bf16_skinny_addnorm(256, 1024, 256, 1024, 256, 1e-6, 256, 1024, 256, 1024, 256, 64, 1, 64, 1024,
-                                          None) == -1
+                                          None, None) == -1
     # decode with on-the-fly norm + RoPE: no workspace, another rotary width (placeholders, never read)
     rope = [256, 10240, 512, 256, 1e-6, 256, 10240, 256, 256, 1e-6, 256, 256, 64, 256, 1024, 256, 256, 9, 512, 256,
             10240, 256, 256, 10240, 1024, 512, 256, 256, 256, 256, 256, 256, 2, 4, 4, 256, 0.0625, 1, 256, 4096,

@@ -333,9 +333,42 @@ def test_skinny_addnorm_equals_add_rmsnorm_then_skinny(M):
         h_out = torch.full((M, H), float("nan"), dtype=torch.bfloat16, device="cuda")
         got = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         rc2 = L.hsg_gemm_bf16_skinny_addnorm(h_in.data_ptr(), H, mix.data_ptr(), H, w1.data_ptr(), 1e-6,
-                                             h_out.data_ptr(), H, W.data_ptr(), H, got.data_ptr(), N, M, N, H, st)
+                                             h_out.data_ptr(), H, W.data_ptr(), H, got.data_ptr(), N, M, N, H, None,
+                                             st)
         torch.cuda.synchronize()
         assert rc == 0 and rc2 == 0, (M, N)
         assert torch.equal(got, ref), (M, N)
         assert torch.equal(h_out, h_ref), (M, N)
         assert torch.equal(h_in, hidden), (M, N)
+
+
+def test_skinny_addnorm_with_bias():
+    """The add + RMSNorm product with a Linear's bias (the risk heads' first projection after the final norm): the
+    same bits as without the bias up to the bias, which enters the fp32 sum before the one rounding; every element
+    within the rounding bound of the float64 normed . W^T + b."""
+    from hs_guard._lib import lib
+    L = lib()
+    st = torch.cuda.current_stream().cuda_stream
+    H, N = 1024, 1024
+    for M in (1, 3, 8):
+        gen = torch.Generator(device="cuda").manual_seed(300 + M)
+        hidden = (torch.randn(M, H, generator=gen, device="cuda") * 3).bfloat16()
+        mix = torch.randn(M, H, generator=gen, device="cuda").bfloat16()
+        w1 = 1 + 0.1 * torch.randn(H, generator=gen, device="cuda")
+        W = (torch.randn(N, H, generator=gen, device="cuda") * 0.02).bfloat16()
+        b = torch.randn(N, generator=gen, device="cuda").bfloat16()
+        h_ref, normed = hidden.clone(), torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
+        assert L.hsg_add_rmsnorm(h_ref.data_ptr(), mix.data_ptr(), w1.data_ptr(), 1e-6, normed.data_ptr(), M, H,
+                                 st) == 0
+        h_out = torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
+        got = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        rc = L.hsg_gemm_bf16_skinny_addnorm(hidden.data_ptr(), H, mix.data_ptr(), H, w1.data_ptr(), 1e-6,
+                                            h_out.data_ptr(), H, W.data_ptr(), H, got.data_ptr(), N, M, N, H,
+                                            b.data_ptr(), st)
+        torch.cuda.synchronize()
+        assert rc == 0
+        assert torch.equal(h_out, h_ref)
+        ref = normed.double().cpu() @ W.double().cpu().t() + b.double().cpu()
+        mag = normed.double().cpu().abs() @ W.double().cpu().abs().t() + b.double().cpu().abs()
+        err = (got.double().cpu() - ref).abs()
+        assert int((err > 2.0 ** -8 * ref.abs() + 2.0 ** -16 * mag).sum()) == 0, M
