@@ -442,7 +442,8 @@ int hsg_gemm_candidates(int32_t M, int32_t N, int32_t K, int32_t* indices, size_
  * (src/hs_guard/engine/slot_engine_v8.py:52-53,63-65,72,78,89) when a tick has at most 8 tokens. Each output is a
  * fixed reduction over k (per lane in k order, then a fixed tree over 64 lanes): the result depends on the inputs
  * and K only, not on M, N or timing. Requires K, lda and ldw multiples of 8 and A, W 16-byte aligned
- * (HSG_ERR_ALIGN), M <= HSG_GEMM_SKINNY_M_MAX (HSG_ERR_SHAPE). Allocates nothing; capturable.
+ * (HSG_ERR_ALIGN), M <= HSG_GEMM_SKINNY_M_MAX (HSG_ERR_SHAPE). D must not overlap an operand (every workgroup reads
+ * all of A while others store their columns of D). Allocates nothing; capturable.
  */
 int hsg_gemm_bf16_skinny(const void* A, int64_t lda, const void* W, int64_t ldw, void* D, int64_t ldd, int32_t M,
                          int32_t N, int32_t K, void* stream);
