@@ -1,8 +1,8 @@
 """Helpers shared by the engine-vs-oracle GPU tests (imported by them; holds no tests itself).
 
 ``matched_gemm(engine)`` gives the oracle (``StreamOracle.tick(..., gemm=...)``) the engine's own bf16 product:
-the engine's ``mm`` (hsg_gemm_bf16 with the same committed hipBLASLt solution for (tb, N, K)), or torch.addmm for
-the heads' biased product, into a [tb, N] buffer, tb the engine's token bucket, with the rows packed in the
+the engine's ``mm`` (hsg_gemm_bf16 with the same committed hipBLASLt solution for (tb, N, K), or the skinny product
+for tb <= 8), or torch.addmm for the heads' biased product, into a [tb, N] buffer, tb the engine's token bucket, with the rows packed in the
 engine's order (longest first, ties in request order). Each output row is then bitwise the engine's for the same
 input row, so an engine-vs-oracle comparison checks every other kernel (conv, recurrence, norms, RoPE, ring
 attention, heads, bookkeeping) against the CPU restatement.

@@ -6,8 +6,8 @@ columns and multi-tick appends are all exercised in a few hundred tokens.
 
 Two comparisons:
 * Matched GEMMs, on a 2-layer net (one GDN and one attention layer): the oracle's
-  projections go through the same hipBLASLt product at the engine's packed shape, so they are bitwise the
-  engine's; everything else (conv, recurrence, norms, RoPE, ring attention, heads, bookkeeping) is the CPU
+  projections go through the product the engine runs at its packed shape (hipBLASLt, or the skinny kernel in
+  ticks of at most 8 tokens), so they are bitwise the engine's; everything else (conv, recurrence, norms, RoPE, ring attention, heads, bookkeeping) is the CPU
   restatement. Per-token class probabilities (so 1 - p(safe)) within 2e-3 absolute; a planted mistake in
   the oracle (dropped attention gate) must exceed it several times.
 * Independent GEMMs (numpy fp32 products), on a 4-layer net: hipBLASLt and the CPU round 0.02% of bf16
@@ -147,6 +147,45 @@ def test_engine_fp16_state_matches_oracle(setup_small, chunk_min_tokens):
         rel = np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
         print(f"[engine] fp16 state slot {s} rel err {rel:.2e}", flush=True)
         assert rel < 4e-3, f"slot {s} state rel err {rel:.2e}"
+
+
+def test_single_token_ticks_match_oracle(setup_small):
+    """The single-slot single-token path (ticks of one token in graphs, as the serving loop replays them): every
+    product on the skinny kernels with the residual add + RMSNorm and the SiLU gate inside them, the attention's
+    q / k norm and RoPE inside the split-K decode (hsg_ring_decode_rope), the final norm with the heads' first
+    Linear in one launch. Rings run past the 32-token window first; a tick of two one-token rows takes the skinny
+    products with the separate norm + RoPE. Matched GEMMs (the oracle's biased head product is torch.addmm, which
+    the engine's one-launch norm + Linear may differ from by one bf16 step in a few outputs), cut scores within
+    2e-3 of the oracle, ring_pos and length bit-exact, state within 1e-3 relative."""
+    from hs_guard.engine.slot_engine import SlotStreamEngine
+    from oracle.backbone import StreamOracle
+    cfg, model, weights = setup_small
+    assert cfg.rotary_dim == 64 and cfg.head_dim == 256 and cfg.hidden_size == 1024   # the fused routes' geometry
+    print("[engine] one-token ticks vs oracle, matched GEMMs", flush=True)
+    eng = SlotStreamEngine(model, 4)
+    assert eng.gemm_skinny_rows >= 2
+    orc = StreamOracle(weights, cfg, 4)
+    gemm = _matched_gemm(eng)
+    rng = np.random.default_rng(4)
+    V = cfg.vocab_size
+    ticks = [[(0, rng.integers(0, V, 40).tolist()), (1, rng.integers(0, V, 36).tolist())],
+             [(2, rng.integers(0, V, 33).tolist())]]
+    ticks += [[(t % 3, [int(rng.integers(0, V))])] for t in range(14)]
+    ticks.append([(0, [int(rng.integers(0, V))]), (3, [int(rng.integers(0, V))])])
+    ticks += [[(3, [int(rng.integers(0, V))])], [(1, [int(rng.integers(0, V))])]]
+    worst = 0.0
+    for t, tick in enumerate(ticks):
+        diff = _max_diff(eng.step(tick), orc.step(tick, gemm=gemm))
+        worst = max(worst, diff)
+        assert diff <= PROB_TOL, f"tick {t}: prob diff {diff:.2e}"
+    print(f"[engine] one-token ticks worst prob diff {worst:.2e}", flush=True)
+    assert (orc.length[:3] > cfg.window_tokens).all()
+    np.testing.assert_array_equal(eng.length, orc.length)
+    np.testing.assert_array_equal(eng.ring_pos.cpu().numpy(), orc.ring_pos)
+    rec = eng.rec.double().cpu().numpy()
+    for s in range(4):
+        rel = np.linalg.norm(rec[:, s] - orc.rec[:, s]) / np.linalg.norm(orc.rec[:, s])
+        assert rel < 1e-3, f"slot {s} state rel err {rel:.2e}"
 
 
 def test_engine_matches_oracle_matched_gemms(setup2):
