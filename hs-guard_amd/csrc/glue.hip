@@ -173,9 +173,14 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
   const int heads_total = a.heads + b.heads;
   const int d0 = lane * 4;   // D / 64 = 4 dims per lane
   // loads retire in order, so the cos/sin wait only for the rotary inputs; rows past the last head reload the
-  // last one and are not stored
+  // last one and are not stored. Every load is unconditional (a tensor without heads reads the other's weights,
+  // unused): a load under a branch made the compiler wait for all outstanding memory operations before each
+  // head, the previous head's store included, one round trip per head.
   const int64_t tpos = pos[tok];
   const float ifreq = inv_freq[threadIdx.x & (half - 1)];
+  const f32x4_n wa = *reinterpret_cast<const f32x4_n*>((a.heads ? a.w1 : b.w1) + d0);
+  const f32x4_n wb = *reinterpret_cast<const f32x4_n*>((b.heads ? b.w1 : a.w1) + d0);
+  __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the rows'
   uint2 xw[ROPE_HEADS_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < ROPE_HEADS_PER_WAVE; ++i) {
@@ -185,9 +190,6 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeTensor a, RopeTensor
     const uint16_t* src = is_a ? a.src + tok * a.src_row + hh * a.src_head : b.src + tok * b.src_row + hh * b.src_head;
     xw[i] = *reinterpret_cast<const uint2*>(src + d0);
   }
-  f32x4_n wa = {0.f, 0.f, 0.f, 0.f}, wb = {0.f, 0.f, 0.f, 0.f};
-  if (a.heads) wa = *reinterpret_cast<const f32x4_n*>(a.w1 + d0);
-  if (b.heads) wb = *reinterpret_cast<const f32x4_n*>(b.w1 + d0);
   if (threadIdx.x < half) rope_pair(tpos, ifreq, cs_[threadIdx.x], sn_[threadIdx.x]);
   lds_barrier();
 #pragma unroll
