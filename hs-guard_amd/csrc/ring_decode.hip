@@ -497,37 +497,42 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(const DecParams p) {
   const uint16_t* qrow = p.q + row_base(p, p.q_sn, p.q_sl, n, ri.tok) + h * p.q_sh;
   const int64_t ring_at = (ri.slot * p.hkv + h) * (int64_t)(W + 1);
 
-  // ---- round trip 1: queries into LDS, the blocks' positions, the step's own key and value ----
+  // ---- round trip 1: queries into LDS, the blocks' positions, the step's own key and value. Every load here is
+  // unconditional (addresses clamped in bounds, what a thread does not need discarded) and issued before the
+  // first use: loads under branches were compiled as one wait per branch, five round trips instead of one. ----
+  const int qc = threadIdx.x % (D / 8);
+  const uint4 qw = *reinterpret_cast<const uint4*>(qrow + min((int)threadIdx.x / (D / 8), G - 1) * p.q_sg + 8 * qc);
+  int64_t kp[BPW][2][4];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int64_t* rpos = p.ring_pos + ri.slot * (int64_t)(W + 1) + min(wave + NWV * i, RB - 1) * KB;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) kp[i][t][r] = rpos[16 * t + 4 * g4 + r];
+  }
+  const uint2 kown = *reinterpret_cast<const uint2*>(p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) +
+                                                     h * p.nk_sh + 4 * lane);
+  const uint2 vown = *reinterpret_cast<const uint2*>(p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) +
+                                                     h * p.nv_sh + 4 * lane);
   if (threadIdx.x < GT * D / 8) {
-    const int g = threadIdx.x / (D / 8), c = threadIdx.x - g * (D / 8);
-    uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if (g < G) w = *reinterpret_cast<const uint4*>(qrow + g * p.q_sg + 8 * c);
-    *reinterpret_cast<uint4*>(&q_s[g * D + 8 * c]) = w;
+    const int g = threadIdx.x / (D / 8);
+    *reinterpret_cast<uint4*>(&q_s[g * D + 8 * qc]) = g < G ? qw : make_uint4(0u, 0u, 0u, 0u);
   }
   uint32_t okbits = 0;   // bit 8 i + 4 t + r: key 16 t + 4 g4 + r of block i is visible
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
-    const int b = wave + NWV * i;
-    if (b < RB) {
-      const int64_t* rpos = p.ring_pos + ri.slot * (int64_t)(W + 1) + b * KB;
+    const bool in_ring = wave + NWV * i < RB;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t kp = rpos[16 * t + 4 * g4 + r];
-          okbits |= (uint32_t)(kp >= 0 && kp <= qpos && kp > qpos - W) << (8 * i + 4 * t + r);
-        }
-    }
+      for (int r = 0; r < 4; ++r) {
+        const int64_t k = kp[i][t][r];
+        okbits |= (uint32_t)(in_ring && k >= 0 && k <= qpos && k > qpos - W) << (8 * i + 4 * t + r);
+      }
   }
   const bool own_wave = wave == NWV - 1;
-  uint2 kown = make_uint2(0u, 0u);
-  if (own_wave) {
-    kown = *reinterpret_cast<const uint2*>(p.new_k + row_base(p, p.nk_sn, p.nk_sl, n, ri.tok) + h * p.nk_sh +
-                                           4 * lane);
-    // parked in LDS until the end, where it is the last value added
-    vown_s[lane] = *reinterpret_cast<const uint2*>(p.new_v + row_base(p, p.nv_sn, p.nv_sl, n, ri.tok) +
-                                                   h * p.nv_sh + 4 * lane);
-  }
+  if (own_wave) vown_s[lane] = vown;   // parked in LDS until the end, where it is the last value added
   bool has[BPW];   // wave-uniform: block i has a visible key (false past the ring)
 #pragma unroll
   for (int i = 0; i < BPW; ++i) has[i] = __ballot(((okbits >> (8 * i)) & 0xffu) != 0) != 0;
