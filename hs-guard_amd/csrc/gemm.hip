@@ -272,6 +272,12 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
   const uint16_t* wrow[NC];
 #pragma unroll
   for (int t = 0; t < NC; ++t) wrow[t] = W + (int64_t)min(n0 + t, N - 1) * ldw;
+  // the bias, loaded up front (without one, W's first row stands in and is not used): a load under the output's
+  // branch was compiled with a wait of its own at the end of the kernel
+  const uint16_t* bsrc = nx.bias ? nx.bias : W;
+  uint16_t bias_v[NC];
+#pragma unroll
+  for (int t = 0; t < NC; ++t) bias_v[t] = bsrc[min(n0 + t, N - 1)];
   float acc[NC][MM];
 #pragma unroll
   for (int t = 0; t < NC; ++t)
@@ -372,7 +378,7 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(const uint16_t* A, int
       if (lane == m) out = s;
     }
     if (n0 + t < N && lane < M) {
-      if (nx.bias) out += hsg::bf2f(nx.bias[n0 + t]);   // the Linear's bias in fp32, then one rounding
+      if (nx.bias) out += hsg::bf2f(bias_v[t]);   // the Linear's bias in fp32, then one rounding
       D[(int64_t)lane * ldd + n0 + t] = hsg::f2bf(out);
     }
   }
