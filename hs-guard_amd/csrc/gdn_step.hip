@@ -128,13 +128,18 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   const int hv = blockIdx.x - ib * p.HV;
   const int n = dispatch_row(ib, gridDim.x / p.HV);
   const int h = hv / (p.HV / p.H);
-  const int64_t slot = p.slots[n];
-  int ntok = (int)p.lens[n];
+  // The row's slot, length and token offset are read together (padded: lens stands in for the offset, unused)
+  // and checked without short-circuit branches: each branch made the compiler wait for one value before issuing
+  // the next read, three dependent round trips before the first burst's loads.
   const bool padded = p.offsets == nullptr;
-  if (slot < 0 || slot >= p.state_rows || ntok < 0) ntok = 0;
-  if (padded && ntok > p.L) ntok = p.L;  // a row never reads past its L padded positions
-  if (!padded && n < p.skip_rows && ntok >= p.skip_min_len) ntok = 0;   // routed to the chunk kernels
-  const int64_t tok0 = padded ? (int64_t)n * p.L : p.offsets[n];
+  const int64_t slot = p.slots[n];
+  const int64_t len_n = p.lens[n];
+  const int64_t off_n = (padded ? p.lens : p.offsets)[n];
+  int ntok = (int)len_n;
+  const bool rejected = (slot < 0) | (slot >= p.state_rows) | (ntok < 0);
+  const bool chunked = !padded & (n < p.skip_rows) & (ntok >= p.skip_min_len);   // routed to the chunk kernels
+  ntok = (rejected | chunked) ? 0 : padded ? min(ntok, p.L) : ntok;   // padded: never past its L positions
+  const int64_t tok0 = padded ? (int64_t)n * p.L : off_n;
   const int col = wave * TILE_V + c * 4;
   // padded layout: the row's outputs at positions t >= ntok are zeros
   auto zero_tail = [&]() __attribute__((always_inline)) {
@@ -161,8 +166,9 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
   float S[ROWS][4];
   float D = 1.0f;
   ST* sp = reinterpret_cast<ST*>(p.state) + ((slot * p.HV + hv) * KD + rg * ROWS) * (int64_t)VD + col;
-  const float A = expf(bf2f(p.A_log[hv]));
-  const float dt = bf2f(p.dt_bias[hv]);
+  // the head's decay parameters, read here and converted where the staging uses them, so their wait falls after
+  // the first burst's loads are issued instead of before
+  const uint16_t a_log_h = p.A_log[hv], dt_h = p.dt_bias[hv];
   // per burst: normalised q (times scale) and k in fp32, one 16-row piece per lane group (stride 20 floats, so
   // the 8 pieces a wave reads at once fall on distinct banks); raw v and z; exp(g) and beta per token
   __shared__ __align__(16) float fq_[CT][KD / ROWS][ROWS + 4];
@@ -356,8 +362,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       }
     }
     if (tid < nt) {
-      const float x = bf2f(pa) + dt;
-      const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
+      uint32_t al = a_log_h, dh = dt_h;
+      asm volatile("" : "+v"(al), "+v"(dh));   // an empty fence: the conversion below is not hoisted above here
+      const float x = bf2f((uint16_t)pa) + bf2f((uint16_t)dh);
+      const float g = -expf(bf2f((uint16_t)al)) * (x > 20.0f ? x : logf(1.0f + expf(x)));
       sdec_[tid] = expf(g);
       sbe_[tid] = sigmoidf_(bf2f(pb));
     }
@@ -412,8 +420,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(const GdnParams p) {
       }
     }
     if (tid < nt) {
-      const float x = bf2f(pa) + dt;
-      const float g = -A * (x > 20.0f ? x : logf(1.0f + expf(x)));
+      uint32_t al = a_log_h, dh = dt_h;
+      asm volatile("" : "+v"(al), "+v"(dh));   // an empty fence: the conversion below is not hoisted above here
+      const float x = bf2f((uint16_t)pa) + bf2f((uint16_t)dh);
+      const float g = -expf(bf2f((uint16_t)al)) * (x > 20.0f ? x : logf(1.0f + expf(x)));
       sdec_[tid] = expf(g);
       sbe_[tid] = sigmoidf_(bf2f(pb));
     }
