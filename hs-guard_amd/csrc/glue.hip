@@ -215,11 +215,11 @@ __device__ __forceinline__ float lane_bf(const u32x4& v, int j) {   // bf16 elem
 }
 
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64_t gu_stride, int width,
-                                                       uint16_t* out, int tokens) {
-  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-  const int tok = (int)(idx / width);
-  const int c = (int)(idx - (int64_t)tok * width);
-  if (tok >= tokens) return;
+                                                       uint16_t* out) {
+  // grid: x = 2,048-element column blocks of the row, y = token (no division of a flat index by the width)
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c >= width) return;
+  const int64_t tok = blockIdx.y;
   const u32x4 g = *reinterpret_cast<const u32x4*>(gu + tok * gu_stride + c);
   const u32x4 u = *reinterpret_cast<const u32x4*>(gu + tok * gu_stride + width + c);
   u32x4 y;
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gu, int64
     const float y1 = rbf(siluf_(lane_bf(g, j + 1))) * lane_bf(u, j + 1);
     y[j >> 1] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
   }
-  *reinterpret_cast<u32x4*>(out + (int64_t)tok * width + c) = y;
+  *reinterpret_cast<u32x4*>(out + tok * width + c) = y;
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -423,10 +423,12 @@ extern "C" int hsg_silu_mul(const void* gate_up, int64_t row_stride, int32_t wid
   if (tokens == 0) return HSG_OK;
   if (!gate_up || !out) return HSG_ERR_ARG;
   if (!aligned(gate_up, 16) || !aligned(out, 16)) return HSG_ERR_ALIGN;
-  const int64_t total = (int64_t)tokens * width / 8;
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate_up), row_stride, width,
-                     static_cast<uint16_t*>(out), tokens);
+  // at most 65,535 tokens per launch (the grid's y limit)
+  for (int32_t t0 = 0; t0 < tokens; t0 += 65535)
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((width / 8 + 255) / 256), (unsigned)min(tokens - t0, 65535)),
+                       dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(gate_up) + (int64_t)t0 * row_stride, row_stride, width,
+                       static_cast<uint16_t*>(out) + (int64_t)t0 * width);
   return launch_status();
 }
 
