@@ -339,17 +339,21 @@ __global__ __launch_bounds__(NW * 64, 2) void ring_attn_mfma_kernel(const RingPa
 __global__ __launch_bounds__(256) void ring_write_kernel(const RingParams p) {
   const int n = blockIdx.x / p.hkv;
   const int h = blockIdx.x - n * p.hkv;
+  // the row's reads are issued together (padded: lens stands in for the offset, unused) and checked without
+  // short-circuit branches, each of which made the compiler wait for one read before issuing the next
+  const bool padded = p.offsets == nullptr;
   const int64_t slot = p.slots[n];
   int64_t len = p.lens[n];
-  const bool padded = p.offsets == nullptr;
-  if (slot < 0 || slot >= p.ring_rows || len < 0 || len > (padded ? LB_MAX : p.lb)) return;
+  const int64_t off = (padded ? p.lens : p.offsets)[n];
+  const int64_t start = p.starts[n];
+  const bool rejected = (slot < 0) | (slot >= p.ring_rows) | (len < 0) | (len > (padded ? LB_MAX : p.lb));
+  if (rejected | (!padded & (len < p.min_len))) return;
   if (padded && len > p.lb) len = p.lb;
-  if (!padded && len < p.min_len) return;
-  const int64_t base_tok = padded ? 0 : p.offsets[n];
+  const int64_t base_tok = padded ? 0 : off;
   const int64_t nk_row = padded ? n * p.nk_sn : base_tok * p.nk_sl;
   const int64_t nv_row = padded ? n * p.nv_sn : base_tok * p.nv_sl;
   const int64_t ring_base = ((slot * p.hkv + h) * (int64_t)(p.W + 1)) * D;
-  const int c0 = (int)(p.starts[n] % p.W);   // ring column of the tick's first step; j < len <= W follow it
+  const int c0 = (int)(start % p.W);   // ring column of the tick's first step; j < len <= W follow it
   // 8-byte pieces e = (token j, dims 4 i ..): a thread's pieces are loaded in batches of WB before any of them
   // is stored (the ring and the new rows could alias as far as the compiler knows, so a load after a store
   // would wait for it)
