@@ -166,6 +166,13 @@ def test_silu_mul_and_risk_head():
     act = torch.empty(T, I, dtype=torch.bfloat16, device=DEV)
     assert lib().hsg_silu_mul(gu_d.data_ptr(), 2 * I, I, act.data_ptr(), T, _stream()) == 0
     _close(_np(act), oglue.silu_mul(gu[:, :I], gu[:, I:]), "silu_mul")
+    # more tokens than one launch's grid holds (65,535 rows): the entry point splits them; a row stride wider than
+    # the gate|up pair and widths that are not a multiple of the 2,048-element column block
+    for T, I, ld in ((70001, 8, 24), (3, 2056, 4120)):
+        gu = bf16(rng.standard_normal((T, ld)) * 2)
+        act = torch.empty(T, I, dtype=torch.bfloat16, device=DEV)
+        assert lib().hsg_silu_mul(_bf(gu).to(DEV).data_ptr(), ld, I, act.data_ptr(), T, _stream()) == 0
+        _close(_np(act), oglue.silu_mul(gu[:, :I], gu[:, I:2 * I]), f"silu_mul {T} x {I}")
     # heads at the model's scale (weights N(0, 0.02)), LayerNorm parameters fp32 values bf16 cannot hold
     T, E, R = 64, 512, 2
     y = bf16(rng.standard_normal((T, R * E)))
